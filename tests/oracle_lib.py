@@ -1,0 +1,238 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so). Test infrastructure only: the checker, never the
+thing under test. Builds the library on first use if it is missing."""
+import ctypes as C
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
+
+F32, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 2, 8, 12, 13, 14
+TYPE_BY_NAME = {"F32": F32, "Q4_0": Q4_0, "Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
+BLOCK = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+
+
+def row_bytes(t, cols):
+    bs, ts = BLOCK[t]
+    return cols // bs * ts
+
+
+class AqTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("ggml_type", C.c_int32), ("rows", C.c_int64), ("cols", C.c_int64),
+                ("data", C.c_void_p), ("nbytes", C.c_size_t)]
+
+
+class AqModelConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("n_layer", "hidden", "ffn", "vocab", "n_head", "n_head_kv", "head_dim",
+                                          "rope_dim")] + [("rope_theta", C.c_float), ("rms_eps", C.c_float)] + \
+               [(n, C.c_uint32) for n in ("full_attention_interval", "dn_n_k_heads", "dn_n_v_heads", "dn_head_dim_k",
+                                          "dn_head_dim_v", "dn_conv_kernel", "has_mtp")]
+
+
+def tensor_table(tensors):
+    """tensors: list of (name, type, rows, cols, numpy uint8/float32 array). Returns (array, keepalive)."""
+    arr = (AqTensor * len(tensors))()
+    keep = []
+    for i, (name, t, rows, cols, data) in enumerate(tensors):
+        data = np.ascontiguousarray(data)
+        nb = name.encode()
+        keep += [nb, data]
+        arr[i] = AqTensor(nb, t, rows, cols, data.ctypes.data, data.nbytes)
+    return arr, keep
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("build_oracle", os.path.join(ROOT, "oracle", "build_oracle.py"))
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    L = C.CDLL(LIB_PATH)
+    P = C.c_void_p
+    sz = C.c_size_t
+    sigs = {
+        "or_f16_to_f32": (C.c_float, [C.c_uint16]),
+        "or_f32_to_f16": (C.c_uint16, [C.c_float]),
+        "or_q8k_quantize": (None, [P, sz, P]),
+        "or_q8_0_quantize": (None, [P, sz, P]),
+        "or_dequant": (C.c_int, [C.c_int, P, sz, P]),
+        "or_row_bytes": (sz, [C.c_int, sz]),
+        "or_dot_q8k": (C.c_float, [C.c_int, P, P, sz]),
+        "or_dot_q8k_t": (None, [C.c_int, P, P, sz, sz, P]),
+        "or_kq_isums": (None, [C.c_int, P, P, sz, P, P]),
+        "or_dot_q8": (C.c_float, [C.c_int, P, P, sz]),
+        "or_dot_f32": (C.c_float, [P, P, sz]),
+        "or_matmul": (None, [C.c_int, P, sz, sz, P, sz, P, C.c_int]),
+        "or_rmsnorm": (None, [P, P, C.c_float, P, sz]),
+        "or_rmsnorm_gated": (None, [P, P, P, C.c_float, P, sz]),
+        "or_softmax": (None, [P, P, sz]),
+        "or_silu": (C.c_float, [C.c_float]),
+        "or_sigmoid": (C.c_float, [C.c_float]),
+        "or_softplus": (C.c_float, [C.c_float]),
+        "or_swiglu": (None, [P, P, P, sz]),
+        "or_inv_freq": (None, [sz, C.c_float, P]),
+        "or_cos_sin": (None, [C.c_uint32, P, sz, P, P]),
+        "or_apply_rope": (None, [P, sz, sz, sz, P, P]),
+        "or_conv1d_step": (None, [P, P, sz, P, P, sz, C.c_int]),
+        "or_l2norm": (None, [P, sz, C.c_float]),
+        "or_gate_g": (C.c_float, [C.c_float, C.c_float, C.c_float]),
+        "or_deltanet_step": (None, [P, P, P, C.c_float, C.c_float, P, P, sz, sz]),
+        "or_model_new": (P, [P, P, sz, C.c_int]),
+        "or_model_free": (None, [P]),
+        "or_state_new": (P, [P, C.c_uint32, C.c_uint32]),
+        "or_state_free": (None, [P]),
+        "or_forward_token": (C.c_uint32, [P, P, C.c_uint32, P]),
+        "or_prefill": (C.c_uint32, [P, P, P, sz, P]),
+        "or_spec_prefill": (C.c_uint32, [P, P, P, sz]),
+        "or_spec_round": (C.c_uint32, [P, P, C.c_uint32, P, P]),
+        "or_spec_set_drafts": (None, [P, P, sz]),
+        "or_spec_get_drafts": (None, [P, P]),
+        "or_spec_logits_row": (None, [P, sz, P]),
+        "or_state_pos": (C.c_uint32, [P]),
+        "or_state_export": (sz, [P, P]),
+        "or_layer_run": (C.c_int, [P, P, sz, C.c_int, P, sz, C.c_uint32, P, P, P, P, P, C.c_uint32, P]),
+    }
+    for name, (res, args) in sigs.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+def ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+# ------------------------------------------------------------------------------------------- thin wrappers
+
+def q8k_quantize(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 256 * 292, np.uint8)
+    lib().or_q8k_quantize(ptr(x), x.size, ptr(out))
+    return out
+
+
+def q8_0_quantize(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 32 * 34, np.uint8)
+    lib().or_q8_0_quantize(ptr(x), x.size, ptr(out))
+    return out
+
+
+def dequant(t, raw, n):
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.zeros(n, np.float32)
+    assert lib().or_dequant(t, ptr(raw), n, ptr(out)) == 0
+    return out
+
+
+def dot_q8k(t, wrow, xq, n):
+    return lib().or_dot_q8k(t, ptr(np.ascontiguousarray(wrow)), ptr(np.ascontiguousarray(xq)), n)
+
+
+def kq_isums(t, wrow, xq, n):
+    nb = n // 256
+    lanes = np.zeros(nb * 8, np.int32)
+    mins = np.zeros(nb * 4, np.int32)
+    lib().or_kq_isums(t, ptr(np.ascontiguousarray(wrow)), ptr(np.ascontiguousarray(xq)), n, ptr(lanes), ptr(mins))
+    return lanes, mins
+
+
+def dot_q8k_t(t, wrow, xqs, n):
+    xqs = [np.ascontiguousarray(x) for x in xqs]
+    arr = (C.c_void_p * len(xqs))(*[x.ctypes.data for x in xqs])
+    out = np.zeros(len(xqs), np.float32)
+    lib().or_dot_q8k_t(t, ptr(np.ascontiguousarray(wrow)), arr, len(xqs), n, ptr(out))
+    return out
+
+
+def dot_q8(t, wrow, xq, n):
+    return lib().or_dot_q8(t, ptr(np.ascontiguousarray(wrow)), ptr(np.ascontiguousarray(xq)), n)
+
+
+def matmul(t, w, rows, cols, x, threads=4):
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, cols)
+    y = np.zeros((x.shape[0], rows), np.float32)
+    lib().or_matmul(t, ptr(np.ascontiguousarray(w)), rows, cols, ptr(x), x.shape[0], ptr(y), threads)
+    return y
+
+
+class Model:
+    """The oracle model over a tensor table (borrowed: the table's arrays are kept alive here)."""
+
+    def __init__(self, cfg: AqModelConfig, tensors, threads=8):
+        self.cfg = cfg
+        self.table, self.keep = tensor_table(tensors)
+        self.h = lib().or_model_new(C.byref(cfg), self.table, len(tensors), threads)
+        assert self.h, "oracle model load failed"
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_model_free(self.h)
+            self.h = None
+
+
+class State:
+    def __init__(self, model: Model, spec_k=0, max_pos=512):
+        self.model = model
+        self.k = spec_k
+        self.h = lib().or_state_new(model.h, spec_k, max_pos)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_state_free(self.h)
+            self.h = None
+
+    @property
+    def pos(self):
+        return lib().or_state_pos(self.h)
+
+    def forward_token(self, tok, want_logits=False):
+        lg = np.zeros(self.model.cfg.vocab, np.float32) if want_logits else None
+        a = lib().or_forward_token(self.model.h, self.h, tok, ptr(lg))
+        return (a, lg) if want_logits else a
+
+    def prefill(self, ids, want_logits=False):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        lg = np.zeros(self.model.cfg.vocab, np.float32) if want_logits else None
+        a = lib().or_prefill(self.model.h, self.h, ptr(ids), ids.size, ptr(lg))
+        return (a, lg) if want_logits else a
+
+    def spec_prefill(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        return lib().or_spec_prefill(self.model.h, self.h, ptr(ids), ids.size)
+
+    def spec_round(self, x_p):
+        em = np.zeros(self.k + 1, np.uint32)
+        n = C.c_uint32(0)
+        m = lib().or_spec_round(self.model.h, self.h, x_p, ptr(em), C.byref(n))
+        return m, em[: n.value].tolist()
+
+    def set_drafts(self, d):
+        d = np.ascontiguousarray(d, dtype=np.uint32)
+        lib().or_spec_set_drafts(self.h, ptr(d), d.size)
+
+    def drafts(self):
+        d = np.zeros(self.k, np.uint32)
+        lib().or_spec_get_drafts(self.h, ptr(d))
+        return d.tolist()
+
+    def logits_row(self, i):
+        out = np.zeros(self.model.cfg.vocab, np.float32)
+        lib().or_spec_logits_row(self.h, i, ptr(out))
+        return out
+
+    def export(self):
+        n = lib().or_state_export(self.h, None)
+        out = np.zeros(n, np.float32)
+        lib().or_state_export(self.h, ptr(out))
+        return out
