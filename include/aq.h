@@ -137,6 +137,25 @@ int aq_matmul(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, fl
  * mins_dev: rows*nb*4 (zero for Q6_K). */
 int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, int32_t *lanes_dev, int32_t *mins_dev);
 
+/* ------------------------------------------------------------------------------------ synthetic tensors */
+
+/* A deterministic synthetic tensor: value i is drawn from splitmix64 of (seed, i) (normal: Irwin-Hall of four
+ * 16-bit fields; uniform; or constant) and quantised to ggml bytes by this library's block quantisers, with
+ * plain IEEE f32 arithmetic, so the host and the device produce the same bytes. No counterpart in the reference
+ * (its fixtures come from real GGUF rows and gguf-py quantisers); it builds the benchmark's random-init models. */
+typedef struct aq_synth_spec {
+    int32_t ggml_type;
+    int64_t rows, cols;
+    uint64_t seed;
+    uint32_t dist; /* 0 normal(mean a, sigma b), 1 uniform [a, b), 2 constant a */
+    float a, b;
+} aq_synth_spec;
+
+/* ggml bytes of the tensor on the host, `threads` workers (<= 0: all cores). */
+int aq_synth_host(const aq_synth_spec *spec, void *ggml_out, int threads);
+/* The same tensor generated directly on the device as an aq_weight. */
+int aq_weight_synth(aq_ctx *ctx, const aq_synth_spec *spec, aq_weight **out);
+
 /* Time `iters` launches of aq_matmul, cycling over `nw` distinct weights (so the 256 MB MALL is defeated),
  * with HIP events on the context stream. Writes the mean device time per launch in microseconds. */
 int aq_matmul_time(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_act *x, size_t ncols,

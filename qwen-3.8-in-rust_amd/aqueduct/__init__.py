@@ -1,0 +1,269 @@
+"""Python binding of libaq.so, the MI355X speculative-decode library (C-ABI in include/aq.h).
+
+Mirrors the reference engine's operator and model entry points (crates/core/src/kernels/matvec.rs, model.rs,
+spec.rs) for tests and benchmarks. There is no fallback: if libaq.so is missing or the device is not a gfx950
+GPU, every call raises AqError.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libaq.so")
+
+F32, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 2, 8, 12, 13, 14
+BLOCK = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+
+
+class AqError(RuntimeError):
+    pass
+
+
+def row_bytes(t, cols):
+    bs, ts = BLOCK[t]
+    return cols // bs * ts
+
+
+class AqTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("ggml_type", C.c_int32), ("rows", C.c_int64), ("cols", C.c_int64),
+                ("data", C.c_void_p), ("nbytes", C.c_size_t)]
+
+
+class AqModelConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("n_layer", "hidden", "ffn", "vocab", "n_head", "n_head_kv", "head_dim",
+                                          "rope_dim")] + [("rope_theta", C.c_float), ("rms_eps", C.c_float)] + \
+               [(n, C.c_uint32) for n in ("full_attention_interval", "dn_n_k_heads", "dn_n_v_heads", "dn_head_dim_k",
+                                          "dn_head_dim_v", "dn_conv_kernel", "has_mtp")]
+
+
+class AqSpecStats(C.Structure):
+    _fields_ = [("rounds", C.c_uint64), ("drafted", C.c_uint64), ("accepted", C.c_uint64), ("emitted", C.c_uint64),
+                ("hist", C.c_uint64 * 17), ("verify_ms", C.c_double), ("commit_ms", C.c_double),
+                ("refeed_ms", C.c_double), ("chain_ms", C.c_double)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise AqError(f"{LIB_PATH} is not built: run __graft_entry__.build() (hipcc, gfx950)")
+    L = C.CDLL(LIB_PATH)
+    P, sz, i = C.c_void_p, C.c_size_t, C.c_int
+    sigs = {
+        "aq_last_error": (C.c_char_p, []),
+        "aq_device_count": (i, [C.POINTER(C.c_int)]),
+        "aq_init": (i, [i, C.POINTER(P)]),
+        "aq_ctx_free": (i, [P]),
+        "aq_synchronize": (i, [P]),
+        "aq_dev_alloc": (i, [P, sz, C.POINTER(P)]),
+        "aq_dev_free": (i, [P, P]),
+        "aq_memcpy_htod": (i, [P, P, P, sz]),
+        "aq_memcpy_dtoh": (i, [P, P, P, sz]),
+        "aq_weight_upload": (i, [P, i, sz, sz, P, C.POINTER(P)]),
+        "aq_weight_free": (i, [P]),
+        "aq_weight_download": (i, [P, P]),
+        "aq_act_new": (i, [P, sz, sz, C.POINTER(P)]),
+        "aq_act_free": (i, [P]),
+        "aq_act_set_f32": (i, [P, P, sz]),
+        "aq_act_quantize": (i, [P, i, sz]),
+        "aq_act_get_q8k": (i, [P, P, sz]),
+        "aq_act_get_q8_0": (i, [P, P, sz]),
+        "aq_matmul": (i, [P, P, P, sz, P]),
+        "aq_kq_isums": (i, [P, P, P, P, P]),
+        "aq_matmul_time": (i, [P, P, sz, P, sz, P, i, C.POINTER(C.c_double)]),
+        "aq_synth_host": (i, [P, P, i]),
+        "aq_weight_synth": (i, [P, P, C.POINTER(P)]),
+    }
+    for name, (res, args) in sigs.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+def check(rc):
+    if rc != 0:
+        raise AqError(f"libaq error {rc}: {lib().aq_last_error().decode()}")
+
+
+def ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+class Context:
+    """aq_ctx: one device, one HIP stream."""
+
+    def __init__(self, device=0):
+        h = C.c_void_p()
+        check(lib().aq_init(device, C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().aq_ctx_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def sync(self):
+        check(lib().aq_synchronize(self.h))
+
+
+class DeviceBuffer:
+    def __init__(self, ctx: Context, nbytes):
+        self.ctx = ctx
+        self.nbytes = nbytes
+        p = C.c_void_p()
+        check(lib().aq_dev_alloc(ctx.h, nbytes, C.byref(p)))
+        self.p = p
+
+    def free(self):
+        if getattr(self, "p", None):
+            lib().aq_dev_free(self.ctx.h, self.p)
+            self.p = None
+
+    def __del__(self):
+        self.free()
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        check(lib().aq_memcpy_htod(self.ctx.h, self.p, ptr(arr), arr.nbytes))
+
+    def download(self, dtype, count):
+        out = np.zeros(count, dtype)
+        check(lib().aq_memcpy_dtoh(self.ctx.h, ptr(out), self.p, out.nbytes))
+        return out
+
+
+class Weight:
+    """A weight matrix on the device (the reference's WeightMat, matvec.rs:49-119)."""
+
+    def __init__(self, ctx: Context, ggml_type, rows, cols, data):
+        data = np.ascontiguousarray(data, dtype=np.uint8) if ggml_type != F32 else \
+            np.ascontiguousarray(data).view(np.uint8)
+        assert data.nbytes == rows * row_bytes(ggml_type, cols)
+        self.ctx, self.type, self.rows, self.cols = ctx, ggml_type, rows, cols
+        h = C.c_void_p()
+        check(lib().aq_weight_upload(ctx.h, ggml_type, rows, cols, ptr(data), C.byref(h)))
+        self.h = h
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().aq_weight_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()
+
+    def download(self):
+        out = np.zeros(self.rows * row_bytes(self.type, self.cols), np.uint8)
+        check(lib().aq_weight_download(self.h, ptr(out)))
+        return out
+
+
+class Act:
+    """Activation rows on the device with their quantised forms (the reference's ActBuf)."""
+
+    def __init__(self, ctx: Context, n, ncols):
+        self.ctx, self.n, self.ncols = ctx, n, ncols
+        h = C.c_void_p()
+        check(lib().aq_act_new(ctx.h, n, ncols, C.byref(h)))
+        self.h = h
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().aq_act_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()
+
+    def set(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.n)
+        check(lib().aq_act_set_f32(self.h, ptr(x), x.shape[0]))
+        return x.shape[0]
+
+    def quantize(self, weight_type, ncols):
+        check(lib().aq_act_quantize(self.h, weight_type, ncols))
+
+    def q8k(self, ncols):
+        out = np.zeros(ncols * self.n // 256 * 292, np.uint8)
+        check(lib().aq_act_get_q8k(self.h, ptr(out), ncols))
+        return out.reshape(ncols, -1)
+
+    def q8_0(self, ncols):
+        out = np.zeros(ncols * self.n // 32 * 34, np.uint8)
+        check(lib().aq_act_get_q8_0(self.h, ptr(out), ncols))
+        return out.reshape(ncols, -1)
+
+
+def matmul(ctx: Context, w: Weight, x: Act, ncols, y: DeviceBuffer = None):
+    """y[c, r] = W[r] . x[c] (matvec.rs:336 / 377); returns host f32 [ncols, rows]."""
+    own = y is None
+    if own:
+        y = DeviceBuffer(ctx, ncols * w.rows * 4)
+    check(lib().aq_matmul(ctx.h, w.h, x.h, ncols, y.p))
+    out = y.download(np.float32, ncols * w.rows).reshape(ncols, w.rows)
+    if own:
+        y.free()
+    return out
+
+
+def kq_isums(ctx: Context, w: Weight, x: Act):
+    nb = w.cols // 256
+    lanes = DeviceBuffer(ctx, w.rows * nb * 8 * 4)
+    mins = DeviceBuffer(ctx, w.rows * nb * 4 * 4)
+    check(lib().aq_kq_isums(ctx.h, w.h, x.h, lanes.p, mins.p))
+    return (lanes.download(np.int32, w.rows * nb * 8).reshape(w.rows, nb, 8),
+            mins.download(np.int32, w.rows * nb * 4).reshape(w.rows, nb, 4))
+
+
+def matmul_time(ctx: Context, ws, x: Act, ncols, y: DeviceBuffer, iters):
+    arr = (C.c_void_p * len(ws))(*[w.h.value for w in ws])
+    us = C.c_double()
+    check(lib().aq_matmul_time(ctx.h, arr, len(ws), x.h, ncols, y.p, iters, C.byref(us)))
+    return us.value
+
+
+class AqSynthSpec(C.Structure):
+    _fields_ = [("ggml_type", C.c_int32), ("rows", C.c_int64), ("cols", C.c_int64), ("seed", C.c_uint64),
+                ("dist", C.c_uint32), ("a", C.c_float), ("b", C.c_float)]
+
+
+NORMAL, UNIFORM, CONST = 0, 1, 2
+
+
+def synth_spec(ggml_type, rows, cols, seed, dist=NORMAL, a=0.0, b=0.02):
+    return AqSynthSpec(ggml_type, rows, cols, seed, dist, a, b)
+
+
+def synth_host(spec: AqSynthSpec, threads=0):
+    """ggml bytes of a synthetic tensor (aq_synth_host); F32 comes back as float32."""
+    n = spec.rows * row_bytes(spec.ggml_type, spec.cols)
+    out = np.zeros(n, np.uint8)
+    check(lib().aq_synth_host(C.byref(spec), ptr(out), threads))
+    return out.view(np.float32) if spec.ggml_type == F32 else out
+
+
+class SynthWeight(Weight):
+    """A synthetic weight generated directly on the device (aq_weight_synth)."""
+
+    def __init__(self, ctx: Context, spec: AqSynthSpec):
+        self.ctx, self.type, self.rows, self.cols = ctx, spec.ggml_type, spec.rows, spec.cols
+        h = C.c_void_p()
+        check(lib().aq_weight_synth(ctx.h, C.byref(spec), C.byref(h)))
+        self.h = h
+
+
+def device_count():
+    n = C.c_int()
+    check(lib().aq_device_count(C.byref(n)))
+    return n.value

@@ -1,0 +1,118 @@
+// aq_common.h — shared definitions of the MI355X (gfx950) speculative-decode library: error handling, the
+// device data layouts (weight planes, activation buffers) and small device helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/aq.h"
+
+#pragma clang fp contract(off)
+
+namespace aq {
+
+// ------------------------------------------------------------------------------------------ error plumbing
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+
+#define AQ_HIP(call)                                                                                          \
+    do {                                                                                                      \
+        hipError_t e_ = (call);                                                                               \
+        if (e_ != hipSuccess)                                                                                 \
+            return ::aq::fail(AQ_EHIP, std::string(#call) + ": " + hipGetErrorString(e_) + " at " + __FILE__ +  \
+                                           ":" + std::to_string(__LINE__));                                   \
+    } while (0)
+
+#define AQ_REQUIRE(cond, msg)                                                                                 \
+    do {                                                                                                      \
+        if (!(cond)) return ::aq::fail(AQ_EINVAL, msg);                                                       \
+    } while (0)
+
+// ------------------------------------------------------------------------------------------- block layouts
+// ggml block sizes (ggml-common.h; the reference's quant.rs:15-20).
+constexpr int QK_K = 256;
+constexpr int QK32 = 32;
+inline int block_elems(int t) { return (t == AQ_TYPE_Q4_0 || t == AQ_TYPE_Q8_0) ? 32 : (t == AQ_TYPE_F32 ? 1 : 256); }
+inline int block_bytes(int t) {
+    switch (t) {
+    case AQ_TYPE_F32: return 4;
+    case AQ_TYPE_Q4_0: return 18;
+    case AQ_TYPE_Q8_0: return 34;
+    case AQ_TYPE_Q4_K: return 144;
+    case AQ_TYPE_Q5_K: return 176;
+    case AQ_TYPE_Q6_K: return 210;
+    default: return 0;
+    }
+}
+inline bool is_kquant(int t) { return t == AQ_TYPE_Q4_K || t == AQ_TYPE_Q5_K || t == AQ_TYPE_Q6_K; }
+
+// Device weight planes. A ggml row of `nb` blocks is split into planes so that every kernel load is an
+// aligned vector load; the integer math is unchanged (the GGUF bytes are the source of truth and
+// aq_weight_download restores them exactly). Per super-block (K-quants):
+//   Q4_K: qa 128 B  lane-permuted nibbles: qa[l*16 + j*4 + b] = qs[32j + 4l + b]
+//         sc  12 B  packed 6-bit scales/mins (as stored)      dm 4 B  f16 d, f16 dmin
+//   Q5_K: as Q4_K plus qb 32 B = qh (already lane-contiguous: lane l reads qh[4l..4l+3])
+//   Q6_K: qa 128 B  ql lane-permuted: qa[l*16 + (h*2 + jj)*4 + b] = ql[h*64 + jj*32 + 4l + b]
+//         qb  64 B  qh lane-permuted: qb[l*8 + h*4 + b] = qh[h*32 + 4l + b]
+//         sc  16 B  int8 group scales                        dm 2 B  f16 d
+// Per 32-block (Q8_0 / Q4_0): qa 32 B / 16 B codes (as stored), dm 2 B f16 d. F32: qa = the rows.
+// Lane l (0..7) of a super-block owns elements 32s + 4l + j (s = sub-block 0..7, j = 0..3): the lane of the
+// reference's 8 exact i32 partial sums (kdot.rs:1-18).
+struct Weight {
+    int type = 0;
+    size_t rows = 0, cols = 0, nb = 0; // nb: blocks per row
+    uint8_t *base = nullptr;            // one allocation holding every plane
+    uint8_t *qa = nullptr, *qb = nullptr, *sc = nullptr, *dm = nullptr;
+    size_t qa_bytes = 0, qb_bytes = 0, sc_bytes = 0, dm_bytes = 0; // per block
+    size_t total = 0;
+    int device = 0;
+};
+
+// Device activation buffer: `ncols` rows of `n` values.
+//   f32   : ncols x n
+//   Q8_K  : qs  ncols x n int8, lane-permuted per 256-block: qs[b*256 + l*32 + s*4 + j] = q[b*256 + 32s + 4l + j]
+//           d   ncols x nb f32; bs ncols x nb x 16 i16 (group sums); q8s ncols x nb x 8 i16 (sub-block sums)
+//   Q8_0  : q0  ncols x n int8 (natural order); d0 ncols x n/32 f32 (the f16 scale widened); h0 the f16 bits;
+//           s0  ncols x n/32 i32 (sum of the block's codes, for the Q4_0 -8 offset)
+struct Act {
+    size_t n = 0, ncols = 0, nb = 0, nb32 = 0;
+    float *f32 = nullptr;
+    int8_t *qs = nullptr;
+    float *d = nullptr;
+    int16_t *bs = nullptr, *q8s = nullptr;
+    int8_t *q0 = nullptr;
+    float *d0 = nullptr;
+    uint16_t *h0 = nullptr;
+    int32_t *s0 = nullptr;
+    void *base = nullptr;
+    int device = 0;
+};
+
+// ----------------------------------------------------------------------------------------- kernel launchers
+// All launches go to `stream`; they return 0 or an AQ_E* code.
+int launch_q8k_quantize(const Act &a, size_t ncols, const float *src, size_t src_stride, hipStream_t stream);
+int launch_q8_0_quantize(const Act &a, size_t ncols, const float *src, size_t src_stride, hipStream_t stream);
+int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
+int launch_kq_isums(const Weight &w, const Act &x, int32_t *lanes, int32_t *mins, hipStream_t stream);
+int launch_repack(Weight &w, const uint8_t *ggml_dev, bool to_planes, hipStream_t stream);
+
+} // namespace aq
+
+struct aq_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+struct aq_weight {
+    aq_ctx *ctx = nullptr;
+    aq::Weight w;
+};
+
+struct aq_act {
+    aq_ctx *ctx = nullptr;
+    aq::Act a;
+};

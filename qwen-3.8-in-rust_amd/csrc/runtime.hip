@@ -1,0 +1,390 @@
+// runtime.hip — lifecycle, device memory, weights, activation buffers and the operator-level C-ABI
+// (include/aq.h). Every entry point validates its arguments and returns an AQ_E* code instead of aborting.
+#include <cstring>
+#include <vector>
+
+#include "aq_common.h"
+
+namespace aq {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+
+int fail(int code, const std::string &msg) {
+    set_error(msg);
+    return code;
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Allocate the planes of a weight (layouts in aq_common.h).
+static int alloc_weight(Weight &w, int type, size_t rows, size_t cols, int device) {
+    const int be = block_elems(type);
+    AQ_REQUIRE(block_bytes(type) > 0, "weight: unsupported ggml type " + std::to_string(type));
+    AQ_REQUIRE(rows > 0 && cols > 0, "weight: empty shape");
+    AQ_REQUIRE(cols % be == 0, "weight: cols " + std::to_string(cols) + " is not a multiple of the block size " +
+                                   std::to_string(be));
+    if (type == AQ_TYPE_F32) AQ_REQUIRE(cols % 32 == 0, "weight: F32 cols must be a multiple of 32");
+    w.type = type;
+    w.rows = rows;
+    w.cols = cols;
+    w.nb = cols / be;
+    w.device = device;
+    switch (type) {
+    case AQ_TYPE_Q4_K: w.qa_bytes = 128; w.qb_bytes = 0; w.sc_bytes = 12; w.dm_bytes = 4; break;
+    case AQ_TYPE_Q5_K: w.qa_bytes = 128; w.qb_bytes = 32; w.sc_bytes = 12; w.dm_bytes = 4; break;
+    case AQ_TYPE_Q6_K: w.qa_bytes = 128; w.qb_bytes = 64; w.sc_bytes = 16; w.dm_bytes = 2; break;
+    case AQ_TYPE_Q8_0: w.qa_bytes = 32; w.qb_bytes = 0; w.sc_bytes = 0; w.dm_bytes = 2; break;
+    case AQ_TYPE_Q4_0: w.qa_bytes = 16; w.qb_bytes = 0; w.sc_bytes = 0; w.dm_bytes = 2; break;
+    default: w.qa_bytes = 4; w.qb_bytes = 0; w.sc_bytes = 0; w.dm_bytes = 0; break;
+    }
+    const size_t nbl = rows * w.nb;
+    const size_t sa = align256(nbl * w.qa_bytes), sb = align256(nbl * w.qb_bytes), ss = align256(nbl * w.sc_bytes),
+                 sd = align256(nbl * w.dm_bytes);
+    w.total = sa + sb + ss + sd;
+    void *p = nullptr;
+    if (hipMalloc(&p, w.total) != hipSuccess) return fail(AQ_ENOMEM, "weight: hipMalloc of " + std::to_string(w.total) + " bytes");
+    w.base = (uint8_t *)p;
+    w.qa = w.base;
+    w.qb = w.qb_bytes ? w.base + sa : nullptr;
+    w.sc = w.sc_bytes ? w.base + sa + sb : nullptr;
+    w.dm = w.dm_bytes ? w.base + sa + sb + ss : nullptr;
+    return 0;
+}
+
+int weight_from_ggml(Weight &w, int type, size_t rows, size_t cols, const void *ggml, bool ggml_on_device,
+                     int device, hipStream_t stream) {
+    int rc = alloc_weight(w, type, rows, cols, device);
+    if (rc) return rc;
+    const size_t bytes = rows * (cols / block_elems(type)) * block_bytes(type);
+    const uint8_t *src = (const uint8_t *)ggml;
+    void *tmp = nullptr;
+    if (!ggml_on_device) {
+        if (hipMalloc(&tmp, bytes) != hipSuccess) return fail(AQ_ENOMEM, "weight: staging hipMalloc");
+        AQ_HIP(hipMemcpyAsync(tmp, ggml, bytes, hipMemcpyHostToDevice, stream));
+        src = (const uint8_t *)tmp;
+    }
+    rc = launch_repack(w, src, true, stream);
+    if (tmp) {
+        AQ_HIP(hipStreamSynchronize(stream));
+        AQ_HIP(hipFree(tmp));
+    }
+    return rc;
+}
+
+void free_weight(Weight &w) {
+    if (w.base) (void)hipFree(w.base);
+    w.base = nullptr;
+}
+
+int alloc_act(Act &a, size_t n, size_t ncols, int device) {
+    AQ_REQUIRE(n > 0 && ncols > 0, "act: empty shape");
+    AQ_REQUIRE(n % 32 == 0, "act: n must be a multiple of 32");
+    a.n = n;
+    a.ncols = ncols;
+    a.nb = n / 256;
+    a.nb32 = n / 32;
+    a.device = device;
+    const size_t f = align256(ncols * n * 4), q = align256(ncols * n), d = align256(ncols * a.nb * 4 + 4),
+                 bs = align256(ncols * a.nb * 32 + 4), q8s = align256(ncols * a.nb * 16 + 4), q0 = align256(ncols * n),
+                 d0 = align256(ncols * a.nb32 * 4), h0 = align256(ncols * a.nb32 * 2), s0 = align256(ncols * a.nb32 * 4);
+    const size_t total = f + q + d + bs + q8s + q0 + d0 + h0 + s0;
+    void *p = nullptr;
+    if (hipMalloc(&p, total) != hipSuccess) return fail(AQ_ENOMEM, "act: hipMalloc");
+    if (hipMemset(p, 0, total) != hipSuccess) return fail(AQ_EHIP, "act: hipMemset");
+    uint8_t *b = (uint8_t *)p;
+    a.base = p;
+    a.f32 = (float *)b;
+    b += f;
+    a.qs = (int8_t *)b;
+    b += q;
+    a.d = (float *)b;
+    b += d;
+    a.bs = (int16_t *)b;
+    b += bs;
+    a.q8s = (int16_t *)b;
+    b += q8s;
+    a.q0 = (int8_t *)b;
+    b += q0;
+    a.d0 = (float *)b;
+    b += d0;
+    a.h0 = (uint16_t *)b;
+    b += h0;
+    a.s0 = (int32_t *)b;
+    return 0;
+}
+
+void free_act(Act &a) {
+    if (a.base) (void)hipFree(a.base);
+    a.base = nullptr;
+}
+
+} // namespace aq
+
+using namespace aq;
+
+// ================================================================================================== C-ABI
+extern "C" {
+
+const char *aq_last_error(void) { return g_last_error.c_str(); }
+
+int aq_device_count(int *out) {
+    AQ_REQUIRE(out, "aq_device_count: null out");
+    int n = 0;
+    AQ_HIP(hipGetDeviceCount(&n));
+    *out = n;
+    return 0;
+}
+
+int aq_init(int device, aq_ctx **out) {
+    AQ_REQUIRE(out, "aq_init: null out");
+    int n = 0;
+    AQ_HIP(hipGetDeviceCount(&n));
+    AQ_REQUIRE(device >= 0 && device < n, "aq_init: device " + std::to_string(device) + " of " + std::to_string(n));
+    AQ_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    AQ_HIP(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(AQ_EUNSUP, std::string("aq_init: this build targets gfx950, device is ") + prop.gcnArchName);
+    aq_ctx *c = new aq_ctx();
+    c->device = device;
+    AQ_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    AQ_HIP(hipEventCreate(&c->ev0));
+    AQ_HIP(hipEventCreate(&c->ev1));
+    *out = c;
+    return 0;
+}
+
+int aq_ctx_free(aq_ctx *ctx) {
+    if (!ctx) return 0;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipEventDestroy(ctx->ev0);
+    (void)hipEventDestroy(ctx->ev1);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return 0;
+}
+
+int aq_synchronize(aq_ctx *ctx) {
+    AQ_REQUIRE(ctx, "aq_synchronize: null ctx");
+    AQ_HIP(hipSetDevice(ctx->device));
+    AQ_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int aq_dev_alloc(aq_ctx *ctx, size_t nbytes, void **dev_out) {
+    AQ_REQUIRE(ctx && dev_out, "aq_dev_alloc: null argument");
+    AQ_HIP(hipSetDevice(ctx->device));
+    void *p = nullptr;
+    if (hipMalloc(&p, nbytes ? nbytes : 1) != hipSuccess) return fail(AQ_ENOMEM, "aq_dev_alloc");
+    *dev_out = p;
+    return 0;
+}
+
+int aq_dev_free(aq_ctx *ctx, void *dev) {
+    AQ_REQUIRE(ctx, "aq_dev_free: null ctx");
+    if (dev) AQ_HIP(hipFree(dev));
+    return 0;
+}
+
+int aq_memcpy_htod(aq_ctx *ctx, void *dev, const void *host, size_t nbytes) {
+    AQ_REQUIRE(ctx && dev && host, "aq_memcpy_htod: null argument");
+    AQ_HIP(hipMemcpyAsync(dev, host, nbytes, hipMemcpyHostToDevice, ctx->stream));
+    AQ_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int aq_memcpy_dtoh(aq_ctx *ctx, void *host, const void *dev, size_t nbytes) {
+    AQ_REQUIRE(ctx && dev && host, "aq_memcpy_dtoh: null argument");
+    AQ_HIP(hipMemcpyAsync(host, dev, nbytes, hipMemcpyDeviceToHost, ctx->stream));
+    AQ_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int aq_weight_upload(aq_ctx *ctx, int ggml_type, size_t rows, size_t cols, const void *ggml_bytes, aq_weight **out) {
+    AQ_REQUIRE(ctx && ggml_bytes && out, "aq_weight_upload: null argument");
+    AQ_HIP(hipSetDevice(ctx->device));
+    aq_weight *w = new aq_weight();
+    w->ctx = ctx;
+    int rc = weight_from_ggml(w->w, ggml_type, rows, cols, ggml_bytes, false, ctx->device, ctx->stream);
+    if (rc == 0) rc = hipStreamSynchronize(ctx->stream) == hipSuccess ? 0 : fail(AQ_EHIP, "aq_weight_upload: sync");
+    if (rc) {
+        free_weight(w->w);
+        delete w;
+        return rc;
+    }
+    *out = w;
+    return 0;
+}
+
+int aq_weight_free(aq_weight *w) {
+    if (!w) return 0;
+    (void)hipSetDevice(w->ctx->device);
+    free_weight(w->w);
+    delete w;
+    return 0;
+}
+
+int aq_weight_download(const aq_weight *w, void *ggml_bytes_out) {
+    AQ_REQUIRE(w && ggml_bytes_out, "aq_weight_download: null argument");
+    aq_ctx *ctx = w->ctx;
+    AQ_HIP(hipSetDevice(ctx->device));
+    const size_t bytes = w->w.rows * w->w.nb * block_bytes(w->w.type);
+    void *tmp = nullptr;
+    if (hipMalloc(&tmp, bytes) != hipSuccess) return fail(AQ_ENOMEM, "aq_weight_download: staging");
+    Weight copy = w->w;
+    int rc = launch_repack(copy, (const uint8_t *)tmp, false, ctx->stream);
+    if (rc == 0) {
+        AQ_HIP(hipMemcpyAsync(ggml_bytes_out, tmp, bytes, hipMemcpyDeviceToHost, ctx->stream));
+        AQ_HIP(hipStreamSynchronize(ctx->stream));
+    }
+    (void)hipFree(tmp);
+    return rc;
+}
+
+int aq_act_new(aq_ctx *ctx, size_t n, size_t ncols, aq_act **out) {
+    AQ_REQUIRE(ctx && out, "aq_act_new: null argument");
+    AQ_REQUIRE(ncols >= 1 && ncols <= 16, "aq_act_new: ncols must be 1..16");
+    AQ_HIP(hipSetDevice(ctx->device));
+    aq_act *a = new aq_act();
+    a->ctx = ctx;
+    int rc = alloc_act(a->a, n, ncols, ctx->device);
+    if (rc) {
+        delete a;
+        return rc;
+    }
+    *out = a;
+    return 0;
+}
+
+int aq_act_free(aq_act *a) {
+    if (!a) return 0;
+    (void)hipSetDevice(a->ctx->device);
+    free_act(a->a);
+    delete a;
+    return 0;
+}
+
+int aq_act_set_f32(aq_act *a, const float *host, size_t ncols) {
+    AQ_REQUIRE(a && host, "aq_act_set_f32: null argument");
+    AQ_REQUIRE(ncols <= a->a.ncols, "aq_act_set_f32: more columns than the buffer holds");
+    AQ_HIP(hipSetDevice(a->ctx->device));
+    AQ_HIP(hipMemcpyAsync(a->a.f32, host, ncols * a->a.n * 4, hipMemcpyHostToDevice, a->ctx->stream));
+    AQ_HIP(hipStreamSynchronize(a->ctx->stream));
+    return 0;
+}
+
+int aq_act_quantize(aq_act *a, int weight_type, size_t ncols) {
+    AQ_REQUIRE(a, "aq_act_quantize: null act");
+    AQ_REQUIRE(ncols >= 1 && ncols <= a->a.ncols, "aq_act_quantize: ncols out of range");
+    AQ_HIP(hipSetDevice(a->ctx->device));
+    if (is_kquant(weight_type)) {
+        AQ_REQUIRE(a->a.n % 256 == 0, "aq_act_quantize: Q8_K needs n % 256 == 0 (matvec.rs:73-77)");
+        return launch_q8k_quantize(a->a, ncols, a->a.f32, a->a.n, a->ctx->stream);
+    }
+    if (weight_type == AQ_TYPE_Q8_0 || weight_type == AQ_TYPE_Q4_0)
+        return launch_q8_0_quantize(a->a, ncols, a->a.f32, a->a.n, a->ctx->stream);
+    if (weight_type == AQ_TYPE_F32) return 0;
+    return fail(AQ_EUNSUP, "aq_act_quantize: unsupported weight type");
+}
+
+int aq_act_get_q8k(const aq_act *a, void *ggml_out, size_t ncols) {
+    AQ_REQUIRE(a && ggml_out, "aq_act_get_q8k: null argument");
+    AQ_REQUIRE(ncols <= a->a.ncols && a->a.n % 256 == 0, "aq_act_get_q8k: shape");
+    const Act &x = a->a;
+    AQ_HIP(hipSetDevice(a->ctx->device));
+    std::vector<int8_t> qs(ncols * x.n);
+    std::vector<float> d(ncols * x.nb);
+    std::vector<int16_t> bs(ncols * x.nb * 16);
+    AQ_HIP(hipMemcpyAsync(qs.data(), x.qs, qs.size(), hipMemcpyDeviceToHost, a->ctx->stream));
+    AQ_HIP(hipMemcpyAsync(d.data(), x.d, d.size() * 4, hipMemcpyDeviceToHost, a->ctx->stream));
+    AQ_HIP(hipMemcpyAsync(bs.data(), x.bs, bs.size() * 2, hipMemcpyDeviceToHost, a->ctx->stream));
+    AQ_HIP(hipStreamSynchronize(a->ctx->stream));
+    uint8_t *o = (uint8_t *)ggml_out;
+    for (size_t c = 0; c < ncols; c++)
+        for (size_t b = 0; b < x.nb; b++) {
+            uint8_t *blk = o + (c * x.nb + b) * 292;
+            std::memcpy(blk, &d[c * x.nb + b], 4);
+            const int8_t *src = qs.data() + c * x.n + b * 256;
+            for (int s = 0; s < 8; s++)
+                for (int l = 0; l < 8; l++)
+                    for (int j = 0; j < 4; j++) blk[4 + 32 * s + 4 * l + j] = (uint8_t)src[l * 32 + s * 4 + j];
+            std::memcpy(blk + 260, &bs[(c * x.nb + b) * 16], 32);
+        }
+    return 0;
+}
+
+int aq_act_get_q8_0(const aq_act *a, void *ggml_out, size_t ncols) {
+    AQ_REQUIRE(a && ggml_out, "aq_act_get_q8_0: null argument");
+    AQ_REQUIRE(ncols <= a->a.ncols, "aq_act_get_q8_0: shape");
+    const Act &x = a->a;
+    AQ_HIP(hipSetDevice(a->ctx->device));
+    std::vector<int8_t> q(ncols * x.n);
+    std::vector<uint16_t> h(ncols * x.nb32);
+    AQ_HIP(hipMemcpyAsync(q.data(), x.q0, q.size(), hipMemcpyDeviceToHost, a->ctx->stream));
+    AQ_HIP(hipMemcpyAsync(h.data(), x.h0, h.size() * 2, hipMemcpyDeviceToHost, a->ctx->stream));
+    AQ_HIP(hipStreamSynchronize(a->ctx->stream));
+    uint8_t *o = (uint8_t *)ggml_out;
+    for (size_t i = 0; i < ncols * x.nb32; i++) {
+        std::memcpy(o + i * 34, &h[i], 2);
+        std::memcpy(o + i * 34 + 2, q.data() + i * 32, 32);
+    }
+    return 0;
+}
+
+static int check_matmul(const aq_weight *w, const aq_act *x, size_t ncols, const void *y) {
+    AQ_REQUIRE(w && x && y, "aq_matmul: null argument");
+    AQ_REQUIRE(x->a.n == w->w.cols, "aq_matmul: activation length " + std::to_string(x->a.n) + " != weight cols " +
+                                        std::to_string(w->w.cols) + " (matvec.rs:338-339)");
+    AQ_REQUIRE(ncols >= 1 && ncols <= x->a.ncols && ncols <= 8, "aq_matmul: ncols must be 1..min(8, act columns)");
+    AQ_REQUIRE(w->ctx == x->ctx, "aq_matmul: weight and activation belong to different contexts");
+    return 0;
+}
+
+int aq_matmul(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, float *y_dev) {
+    AQ_REQUIRE(ctx, "aq_matmul: null ctx");
+    int rc = check_matmul(w, x, ncols, y_dev);
+    if (rc) return rc;
+    AQ_HIP(hipSetDevice(ctx->device));
+    rc = launch_matmul(w->w, x->a, ncols, y_dev, nullptr, ctx->stream);
+    if (rc) return rc;
+    AQ_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, int32_t *lanes_dev, int32_t *mins_dev) {
+    AQ_REQUIRE(ctx && w && x && lanes_dev && mins_dev, "aq_kq_isums: null argument");
+    AQ_REQUIRE(is_kquant(w->w.type), "aq_kq_isums: K-quant weights only");
+    AQ_REQUIRE(x->a.n == w->w.cols, "aq_kq_isums: activation length");
+    AQ_HIP(hipSetDevice(ctx->device));
+    int rc = launch_kq_isums(w->w, x->a, lanes_dev, mins_dev, ctx->stream);
+    if (rc) return rc;
+    AQ_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int aq_matmul_time(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_act *x, size_t ncols, float *y_dev,
+                   int iters, double *us_per_launch) {
+    AQ_REQUIRE(ctx && ws && nw > 0 && us_per_launch && iters > 0, "aq_matmul_time: bad argument");
+    for (size_t i = 0; i < nw; i++) {
+        int rc = check_matmul(ws[i], x, ncols, y_dev);
+        if (rc) return rc;
+        AQ_REQUIRE(ws[i]->w.rows == ws[0]->w.rows, "aq_matmul_time: weights of different shapes");
+    }
+    AQ_HIP(hipSetDevice(ctx->device));
+    AQ_HIP(hipEventRecord(ctx->ev0, ctx->stream));
+    for (int i = 0; i < iters; i++) {
+        int rc = launch_matmul(ws[i % nw]->w, x->a, ncols, y_dev, nullptr, ctx->stream);
+        if (rc) return rc;
+    }
+    AQ_HIP(hipEventRecord(ctx->ev1, ctx->stream));
+    AQ_HIP(hipEventSynchronize(ctx->ev1));
+    float ms = 0.0f;
+    AQ_HIP(hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
+    *us_per_launch = (double)ms * 1000.0 / iters;
+    return 0;
+}
+
+} // extern "C"
