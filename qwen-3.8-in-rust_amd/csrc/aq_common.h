@@ -49,18 +49,21 @@ inline int block_bytes(int t) {
 }
 inline bool is_kquant(int t) { return t == AQ_TYPE_Q4_K || t == AQ_TYPE_Q5_K || t == AQ_TYPE_Q6_K; }
 
+// Lane l (0..7) of a super-block owns elements 32s + 4l + b (s = sub-block 0..7, b = 0..3): the lane of the
+// reference's 8 exact i32 partial sums (kdot.rs:1-18). Lanes are stored in slot order slot(l) = 2*(l&3) + (l>>2)
+// (0,4,1,5,2,6,3,7), so lanes j and j+4, the pair one kernel thread owns, are adjacent.
+__host__ __device__ inline int lane_slot(int l) { return 2 * (l & 3) + (l >> 2); }
+
 // Device weight planes. A ggml row of `nb` blocks is split into planes so that every kernel load is an
 // aligned vector load; the integer math is unchanged (the GGUF bytes are the source of truth and
 // aq_weight_download restores them exactly). Per super-block (K-quants):
-//   Q4_K: qa 128 B  lane-permuted nibbles: qa[l*16 + j*4 + b] = qs[32j + 4l + b]
-//         sc  12 B  packed 6-bit scales/mins (as stored)      dm 4 B  f16 d, f16 dmin
-//   Q5_K: as Q4_K plus qb 32 B = qh (already lane-contiguous: lane l reads qh[4l..4l+3])
-//   Q6_K: qa 128 B  ql lane-permuted: qa[l*16 + (h*2 + jj)*4 + b] = ql[h*64 + jj*32 + 4l + b]
-//         qb  64 B  qh lane-permuted: qb[l*8 + h*4 + b] = qh[h*32 + 4l + b]
+//   Q4_K: qa 128 B  nibbles by lane: qa[slot(l)*16 + q*4 + b] = qs[32q + 4l + b] (q = sub-block pair)
+//         sc  16 B  f16 d, f16 dmin, then the 12 packed 6-bit scale/min bytes (as stored)
+//   Q5_K: as Q4_K plus qb 32 B: qb[slot(l)*4 + b] = qh[4l + b]
+//   Q6_K: qa 128 B  ql by lane: qa[slot(l)*16 + (h*2 + jj)*4 + b] = ql[h*64 + jj*32 + 4l + b]
+//         qb  64 B  qh by lane: qb[slot(l)*8 + h*4 + b] = qh[h*32 + 4l + b]
 //         sc  16 B  int8 group scales                        dm 2 B  f16 d
 // Per 32-block (Q8_0 / Q4_0): qa 32 B / 16 B codes (as stored), dm 2 B f16 d. F32: qa = the rows.
-// Lane l (0..7) of a super-block owns elements 32s + 4l + j (s = sub-block 0..7, j = 0..3): the lane of the
-// reference's 8 exact i32 partial sums (kdot.rs:1-18).
 struct Weight {
     int type = 0;
     size_t rows = 0, cols = 0, nb = 0; // nb: blocks per row
@@ -73,7 +76,7 @@ struct Weight {
 
 // Device activation buffer: `ncols` rows of `n` values.
 //   f32   : ncols x n
-//   Q8_K  : qs  ncols x n int8, lane-permuted per 256-block: qs[b*256 + l*32 + s*4 + j] = q[b*256 + 32s + 4l + j]
+//   Q8_K  : qs  ncols x n int8, by lane per 256-block: qs[blk*256 + slot(l)*32 + s*4 + b] = q[blk*256 + 32s + 4l + b]
 //           d   ncols x nb f32; bs ncols x nb x 16 i16 (group sums); q8s ncols x nb x 8 i16 (sub-block sums)
 //   Q8_0  : q0  ncols x n int8 (natural order); d0 ncols x n/32 f32 (the f16 scale widened); h0 the f16 bits;
 //           s0  ncols x n/32 i32 (sum of the block's codes, for the Q4_0 -8 offset)
@@ -97,6 +100,10 @@ int launch_q8k_quantize(const Act &a, size_t ncols, const float *src, size_t src
 int launch_q8_0_quantize(const Act &a, size_t ncols, const float *src, size_t src_stride, hipStream_t stream);
 int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
 int launch_kq_isums(const Weight &w, const Act &x, int32_t *lanes, int32_t *mins, hipStream_t stream);
+// The matrix-core K-quant kernel (kq_mfma.hip); launch_matmul routes K-quant weights here.
+int launch_kq_mfma(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
+// The v_dot4 K-quant kernel (matmul.hip), kept as the second implementation the tests compare against.
+int launch_kq_dot4(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
 int launch_repack(Weight &w, const uint8_t *ggml_dev, bool to_planes, hipStream_t stream);
 
 } // namespace aq

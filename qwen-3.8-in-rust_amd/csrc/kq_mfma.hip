@@ -1,0 +1,440 @@
+// kq_mfma.hip — the K-quant x Q8_K matmul (N = 1 matvec and the N = k+1 verify batch) on gfx950 matrix cores.
+//
+// Same integers and floats as the reference (kdot.rs:37-140 and the blocked kdot.rs:176-333): per super-block the
+// 8 exact i32 lane sums (lane l = elements 4l..4l+3 of each 32-element sub-block, the scale multiplied in as an
+// integer), the 4 Q4_K/Q5_K min lanes, the Q6_K -32 fold; then acc[l] += (dx*dw) * float(sum) super-block by
+// super-block without FMA, and the ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) [+ (m0+m2)+(m1+m3)] reduction. Only how
+// the exact integers are produced is new:
+//
+//  * v_mfma_i32_4x4x4_16b_i8 computes 16 independent 4x4x4 int8 products. Block b of one instruction is
+//    (row group g, lane j): its K = 4 elements are lane j's 4 positions of one sub-block, so it yields the lane-j
+//    partial of that sub-block for 4 weight rows x 4 activation columns, exactly (int32). A = activations (A row i
+//    = column c), B = weight codes (B column = weight row). Register layout, measured on the device: A and B of
+//    block b at lanes 4b+i / 4b+j, D[i][j] at lane 4b+j, VGPR i.
+//  * Thread t = 16g + 4j + r of a wave owns weight row 4g + r (16 rows per wave) and the two reference lanes j and
+//    j+4: one instruction set with blocks (g, j) computes lane j, a second one lane j+4. Per-row work (scale
+//    decode, the min lanes) is shared by the row's 4 threads instead of 8, and every min lane j (0..3) is a thread.
+//  * The integer scale of each sub-block multiplies the MFMA partial with a full-rate 24-bit integer mad.
+//  * Activations are staged in LDS per chunk of super-blocks, double-buffered (chunk k+1 is fetched into registers
+//    while chunk k is computed); weights stream from HBM as 16-byte loads, prefetched PF super-blocks ahead.
+//  * Matrices with few rows split K across KS waves of the work-group: wave w takes super-blocks w, w+KS, ...;
+//    after every round the waves exchange their f32 products through LDS and each adds them to its copy of the
+//    chain in super-block order, which keeps the chain the reference's sequential sum bit for bit.
+#include "aq_common.h"
+
+namespace aq {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct MfArgs {
+    const uint8_t *qa, *qb, *sc, *dm;
+    int rows, nb;
+    const int8_t *xqs;   // ncols x n, by lane slot
+    const float *xd;     // ncols x nb
+    const int16_t *xbs;  // ncols x nb x 16
+    const int16_t *xq8s; // ncols x nb x 8
+    size_t xcol;
+    float *y;
+    const float *resid;
+};
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    _Float16 f;
+    const uint16_t h = (uint16_t)bits16;
+    __builtin_memcpy(&f, &h, 2);
+    return (float)f;
+}
+
+__device__ __forceinline__ v4i mfma(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_mfma_i32_4x4x4i8((int)a, (int)b, (v4i){0, 0, 0, 0}, 0, 0, 0);
+}
+
+__device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
+__device__ __forceinline__ int ubyte(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xFF); }
+
+// The weight bytes of one super-block one thread needs (lanes j and j+4 of its row).
+template <int TYPE>
+struct WRegs {
+    uint4 qa0, qa1; // codes of lane j, lane j+4
+    uint4 sc;       // Q4_K/Q5_K: d, dmin, 12 scale bytes; Q6_K: 16 int8 scales
+    uint4 qb;       // Q5_K: .x, .y = qh of lanes j, j+4; Q6_K: .x,.y lane j (h 0,1), .z,.w lane j+4
+    uint32_t d6;    // Q6_K: f16 d
+};
+
+template <int TYPE>
+__device__ __forceinline__ void load_w(WRegs<TYPE> &w, const MfArgs &a, size_t wsb, int j) {
+    const uint4 *q = reinterpret_cast<const uint4 *>(a.qa + wsb * 128 + j * 32);
+    w.qa0 = q[0];
+    w.qa1 = q[1];
+    w.sc = *reinterpret_cast<const uint4 *>(a.sc + wsb * 16);
+    if constexpr (TYPE == AQ_TYPE_Q5_K) {
+        const uint2 h = *reinterpret_cast<const uint2 *>(a.qb + wsb * 32 + j * 8);
+        w.qb = make_uint4(h.x, h.y, 0, 0);
+    } else if constexpr (TYPE == AQ_TYPE_Q6_K) {
+        w.qb = *reinterpret_cast<const uint4 *>(a.qb + wsb * 64 + j * 16);
+        w.d6 = *reinterpret_cast<const uint16_t *>(a.dm + wsb * 2);
+    }
+}
+
+// LDS chunk (per super-block of the chunk): codes xq[CH][NC][256] (by lane slot), f32 scales xd[CH][NCP] and
+// activation-sum pairs xm[CH][8][NCP] (pair i = sums 2i, 2i+1: Q4_K/Q5_K sub-block sums (i < 4), Q6_K group sums),
+// NCP = NC rounded up to 4 so a thread reads its 4 columns with one 16-byte load.
+template <int NC, int CH>
+struct Lds {
+    static constexpr int NCP = (NC + 3) / 4 * 4;
+    int8_t xq[CH][NC][256];
+    float xd[CH][NCP];
+    uint32_t xm[CH][8][NCP];
+};
+
+template <int TYPE, int NC, int KS, int PF, int CH>
+__global__ void __launch_bounds__(256) kq_mfma_kernel(MfArgs a) {
+    static_assert(CH % (KS * PF) == 0, "a chunk must hold whole prefetch rounds");
+    constexpr int RG = 4 / KS;                      // row groups (16 rows each) per work-group
+    constexpr int NCG = (NC + 3) / 4;               // column groups of 4
+    constexpr int NCP = Lds<NC, CH>::NCP;
+    constexpr int NV = (CH * NC * 16 + 255) / 256;  // 16-byte code vectors per thread per chunk
+    constexpr int NM = CH * NC;                     // (super-block, column) meta entries per chunk
+    static_assert(NV <= 4 && NM <= 256, "staging shape");
+    constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
+    __shared__ Lds<NC, CH> lds_buf[2];
+    __shared__ float xch[KS > 1 ? RG : 1][KS > 1 ? 2 : 1][KS][3 * NC][64];
+
+    const int t = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int rg = wid / KS, w = wid % KS;
+    const int g = t >> 4, j = (t >> 2) & 3, r = t & 3;
+    int row = ((int)blockIdx.x * RG + rg) * 16 + 4 * g + r;
+    const bool valid = row < a.rows;
+    if (!valid) row = a.rows - 1;
+    const int nb = a.nb;
+    const int nchunks = (nb + CH - 1) / CH;
+    const size_t rowsb = (size_t)row * nb;
+
+    float acc0[NC], acc1[NC], accm[NC]; // lane j, lane j+4, min lane j
+#pragma unroll
+    for (int i = 0; i < NC; i++) acc0[i] = acc1[i] = accm[i] = 0.0f;
+
+    WRegs<TYPE> wr[PF];
+#pragma unroll
+    for (int p = 0; p < PF; p++) load_w<TYPE>(wr[p], a, rowsb + min(w + p * KS, nb - 1), j);
+    int parity = 0;
+
+    // ---- activation chunk staging (named registers, never an array: arrays here get demoted to scratch)
+    uint4 sv0 = make_uint4(0, 0, 0, 0), sv1 = sv0, sv2 = sv0, sv3 = sv0, sm0 = sv0, sm1 = sv0;
+    float sd = 0.0f;
+#define AQ_STAGE_VEC(I, SV, BODY)                                                                             \
+    if constexpr (I < NV) {                                                                                   \
+        const int v = (int)threadIdx.x + I * 256;                                                             \
+        const int c = v / (CH * 16), rem = v % (CH * 16), sbi = rem / 16, o = (rem % 16) * 16;                \
+        BODY(SV)                                                                                              \
+    }
+    auto stage_load = [&](int k) {
+        const int c0 = k * CH, ch = nb - c0 < CH ? nb - c0 : CH;
+#define AQ_LOAD_BODY(SV)                                                                                      \
+    if (c < NC && sbi < ch)                                                                                   \
+        SV = *reinterpret_cast<const uint4 *>(a.xqs + (size_t)c * a.xcol + (size_t)(c0 + sbi) * 256 + o);
+        AQ_STAGE_VEC(0, sv0, AQ_LOAD_BODY)
+        AQ_STAGE_VEC(1, sv1, AQ_LOAD_BODY)
+        AQ_STAGE_VEC(2, sv2, AQ_LOAD_BODY)
+        AQ_STAGE_VEC(3, sv3, AQ_LOAD_BODY)
+#undef AQ_LOAD_BODY
+        const int e = (int)threadIdx.x;
+        if (e < NM) {
+            const int c = e / CH, sbi = e % CH;
+            if (sbi < ch) {
+                const size_t xm = (size_t)c * nb + c0 + sbi;
+                sd = a.xd[xm];
+                if constexpr (Q6) {
+                    sm0 = reinterpret_cast<const uint4 *>(a.xbs + xm * 16)[0];
+                    sm1 = reinterpret_cast<const uint4 *>(a.xbs + xm * 16)[1];
+                } else {
+                    sm0 = *reinterpret_cast<const uint4 *>(a.xq8s + xm * 8);
+                }
+            }
+        }
+    };
+    auto stage_store = [&](int buf) {
+        Lds<NC, CH> &L = lds_buf[buf];
+#define AQ_STORE_BODY(SV)                                                                                     \
+    if (c < NC) *reinterpret_cast<uint4 *>(&L.xq[sbi][c][o]) = SV;
+        AQ_STAGE_VEC(0, sv0, AQ_STORE_BODY)
+        AQ_STAGE_VEC(1, sv1, AQ_STORE_BODY)
+        AQ_STAGE_VEC(2, sv2, AQ_STORE_BODY)
+        AQ_STAGE_VEC(3, sv3, AQ_STORE_BODY)
+#undef AQ_STORE_BODY
+        const int e = (int)threadIdx.x;
+        if (e < NM) {
+            const int c = e / CH, sbi = e % CH;
+            L.xd[sbi][c] = sd;
+            L.xm[sbi][0][c] = sm0.x;
+            L.xm[sbi][1][c] = sm0.y;
+            L.xm[sbi][2][c] = sm0.z;
+            L.xm[sbi][3][c] = sm0.w;
+            if constexpr (Q6) {
+                L.xm[sbi][4][c] = sm1.x;
+                L.xm[sbi][5][c] = sm1.y;
+                L.xm[sbi][6][c] = sm1.z;
+                L.xm[sbi][7][c] = sm1.w;
+            }
+        }
+    };
+#undef AQ_STAGE_VEC
+    stage_load(0);
+    stage_store(0);
+    if (nchunks > 1) stage_load(1);
+    __syncthreads();
+
+    for (int k = 0; k < nchunks; k++) {
+        const int c0 = k * CH;
+        const int ch = nb - c0 < CH ? nb - c0 : CH;
+        const Lds<NC, CH> &L = lds_buf[k & 1];
+
+        // Products of one super-block: pr0/pr1 (lanes j, j+4) and pm (min lane j), per column.
+        auto process = [&](const WRegs<TYPE> &wv, const int sbi, float *pr0, float *pr1, float *pm) {
+            uint32_t code0[8], code1[8]; // 4 unsigned codes per sub-block, lanes j and j+4
+            int scl0[8], scl1[8];        // integer scale per sub-block, lanes j and j+4
+            int mn0 = 0, mn1 = 0;        // Q4_K/Q5_K mins of sub-blocks 2j, 2j+1 (min lane j)
+            int os00 = 0, os01 = 0, os10 = 0, os11 = 0; // Q6_K -32 fold scales: groups 2l, 2l+1 of l = j, j+4
+            float dw, dminw = 0.0f;
+            if constexpr (Q6) {
+                const uint32_t ql0[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w};
+                const uint32_t ql1[4] = {wv.qa1.x, wv.qa1.y, wv.qa1.z, wv.qa1.w};
+                const uint32_t qh0[2] = {wv.qb.x, wv.qb.y}, qh1[2] = {wv.qb.z, wv.qb.w};
+                const uint32_t sw[4] = {wv.sc.x, wv.sc.y, wv.sc.z, wv.sc.w};
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                    for (int kk = 0; kk < 4; kk++) {
+                        const int s = hh * 4 + kk;
+                        const int li = kk < 2 ? hh * 2 + kk : hh * 2 + kk - 2, sh = kk < 2 ? 0 : 4;
+                        code0[s] = ((ql0[li] >> sh) & 0x0F0F0F0Fu) | (((qh0[hh] >> (2 * kk)) & 0x03030303u) << 4);
+                        code1[s] = ((ql1[li] >> sh) & 0x0F0F0F0Fu) | (((qh1[hh] >> (2 * kk)) & 0x03030303u) << 4);
+                        const int gi = hh * 8 + 2 * kk; // lane j (< 4) uses group gi, lane j+4 group gi+1
+                        scl0[s] = sbyte(sw[gi >> 2], gi & 3);
+                        scl1[s] = sbyte(sw[(gi + 1) >> 2], (gi + 1) & 3);
+                    }
+                // groups 2l, 2l+1: l = j -> bytes 2j, 2j+1 of word j/2; l = j+4 -> word 2 + j/2
+                os00 = sbyte(sw[j >> 1], 2 * (j & 1));
+                os01 = sbyte(sw[j >> 1], 2 * (j & 1) + 1);
+                os10 = sbyte(sw[2 + (j >> 1)], 2 * (j & 1));
+                os11 = sbyte(sw[2 + (j >> 1)], 2 * (j & 1) + 1);
+                dw = h2f(wv.d6);
+            } else {
+                const uint32_t q0 = wv.sc.y, q1 = wv.sc.z, q2 = wv.sc.w;
+                const uint32_t sc_lo = q0 & 0x3F3F3F3Fu, mn_lo = q1 & 0x3F3F3F3Fu;
+                const uint32_t sc_hi = (q2 & 0x0F0F0F0Fu) | ((q0 >> 2) & 0x30303030u);
+                const uint32_t mn_hi = ((q2 >> 4) & 0x0F0F0F0Fu) | ((q1 >> 2) & 0x30303030u);
+                const uint32_t mnw = j < 2 ? mn_lo : mn_hi;
+                mn0 = ubyte(mnw, 2 * (j & 1));
+                mn1 = ubyte(mnw, 2 * (j & 1) + 1);
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    scl0[s] = scl1[s] = ubyte(sc_lo, s);
+                    scl0[s + 4] = scl1[s + 4] = ubyte(sc_hi, s);
+                }
+                const uint32_t w0[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w};
+                const uint32_t w1[4] = {wv.qa1.x, wv.qa1.y, wv.qa1.z, wv.qa1.w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    code0[2 * q] = w0[q] & 0x0F0F0F0Fu;
+                    code0[2 * q + 1] = (w0[q] >> 4) & 0x0F0F0F0Fu;
+                    code1[2 * q] = w1[q] & 0x0F0F0F0Fu;
+                    code1[2 * q + 1] = (w1[q] >> 4) & 0x0F0F0F0Fu;
+                }
+                if constexpr (TYPE == AQ_TYPE_Q5_K) {
+#pragma unroll
+                    for (int s = 0; s < 8; s++) {
+                        code0[s] |= ((wv.qb.x >> s) & 0x01010101u) << 4;
+                        code1[s] |= ((wv.qb.y >> s) & 0x01010101u) << 4;
+                    }
+                }
+                dw = h2f(wv.sc.x & 0xFFFF);
+                dminw = h2f(wv.sc.x >> 16);
+            }
+#pragma unroll
+            for (int cg = 0; cg < NCG; cg++) {
+                const int cA = cg * 4 + r < NC ? cg * 4 + r : 0; // this thread's A-operand column
+                const uint4 *xp = reinterpret_cast<const uint4 *>(&L.xq[sbi][cA][j * 64]);
+                const uint4 xa = xp[0], xb = xp[1], xc = xp[2], xd = xp[3];
+                const uint32_t x0[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w}; // lane j
+                const uint32_t x1[8] = {xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w}; // lane j+4
+                int s0[4] = {0, 0, 0, 0}, s1[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int s = 0; s < 8; s++) {
+                    const v4i d0 = mfma(x0[s], code0[s]);
+                    const v4i d1 = mfma(x1[s], code1[s]);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        if (cg * 4 + c < NC) { // the block's columns past NC are padding
+                            s0[c] += scl0[s] * d0[c];
+                            s1[c] += scl1[s] * d1[c];
+                        }
+                    }
+                }
+                const float4 dx4 = *reinterpret_cast<const float4 *>(&L.xd[sbi][cg * 4]);
+                const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+                const uint4 m0 = *reinterpret_cast<const uint4 *>(&L.xm[sbi][j][cg * 4]);
+                const uint32_t mw0[4] = {m0.x, m0.y, m0.z, m0.w};
+                uint32_t mw1[4] = {0, 0, 0, 0};
+                if constexpr (Q6) {
+                    const uint4 m1 = *reinterpret_cast<const uint4 *>(&L.xm[sbi][j + 4][cg * 4]);
+                    mw1[0] = m1.x;
+                    mw1[1] = m1.y;
+                    mw1[2] = m1.z;
+                    mw1[3] = m1.w;
+                }
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int col = cg * 4 + c;
+                    if (col < NC) {
+                        const float dd = dxs[c] * dw;
+                        const int lo0 = (int)(int16_t)(mw0[c] & 0xFFFF), hi0 = (int)(int16_t)(mw0[c] >> 16);
+                        if constexpr (Q6) {
+                            const int lo1 = (int)(int16_t)(mw1[c] & 0xFFFF), hi1 = (int)(int16_t)(mw1[c] >> 16);
+                            pr0[col] = dd * (float)(s0[c] - 32 * (lo0 * os00 + hi0 * os01));
+                            pr1[col] = dd * (float)(s1[c] - 32 * (lo1 * os10 + hi1 * os11));
+                        } else {
+                            pr0[col] = dd * (float)s0[c];
+                            pr1[col] = dd * (float)s1[c];
+                            pm[col] = (-dxs[c] * dminw) * (float)(mn0 * lo0 + mn1 * hi0);
+                        }
+                    }
+                }
+            }
+        };
+
+        for (int rb = 0; rb < ch; rb += KS * PF) {
+#pragma unroll
+            for (int p = 0; p < PF; p++) {
+                const int round0 = rb + p * KS; // first super-block (chunk-relative) of this round
+                if (round0 < ch) {              // uniform across the work-group
+                    const int sbi = round0 + w;
+                    float pr0[NC], pr1[NC], pm[NC];
+#pragma unroll
+                    for (int c = 0; c < NC; c++) pr0[c] = pr1[c] = pm[c] = 0.0f;
+                    if (sbi < ch) {
+                        process(wr[p], sbi, pr0, pr1, pm);
+                        load_w<TYPE>(wr[p], a, rowsb + min(c0 + sbi + PF * KS, nb - 1), j);
+                    }
+                    if constexpr (KS == 1) {
+#pragma unroll
+                        for (int c = 0; c < NC; c++) {
+                            acc0[c] += pr0[c];
+                            acc1[c] += pr1[c];
+                            if constexpr (!Q6) accm[c] += pm[c];
+                        }
+                    } else {
+                        float(*x)[3 * NC][64] = xch[rg][parity];
+#pragma unroll
+                        for (int c = 0; c < NC; c++) {
+                            x[w][c][t] = pr0[c];
+                            x[w][NC + c][t] = pr1[c];
+                            x[w][2 * NC + c][t] = pm[c];
+                        }
+                        __syncthreads();
+                        const int live = ch - round0 < KS ? ch - round0 : KS; // super-blocks in this round
+#pragma unroll
+                        for (int w2 = 0; w2 < KS; w2++) {
+                            if (w2 < live) {
+#pragma unroll
+                                for (int c = 0; c < NC; c++) {
+                                    acc0[c] += x[w2][c][t];
+                                    acc1[c] += x[w2][NC + c][t];
+                                    if constexpr (!Q6) accm[c] += x[w2][2 * NC + c][t];
+                                }
+                            }
+                        }
+                        parity ^= 1;
+                    }
+                }
+            }
+        }
+        if (k + 1 < nchunks) {
+            stage_store((k + 1) & 1);
+            if (k + 2 < nchunks) stage_load(k + 2);
+        }
+        __syncthreads();
+    }
+    // ---------------------------------------------------------------- reduce the 8 lanes of each row
+    // lanes j and j+4 are in one thread; j sits at t = 16g + 4j + r: xor 8 pairs j with j^2, xor 4 with j^1.
+    if (w != 0) return; // every wave of a row group holds the same chain; wave 0 writes
+#pragma unroll
+    for (int col = 0; col < NC; col++) {
+        float v = acc0[col] + acc1[col]; // l_j + l_{j+4}
+        v = v + __shfl_xor(v, 8);
+        v = v + __shfl_xor(v, 4);
+        if constexpr (!Q6) {
+            float m = accm[col];
+            m = m + __shfl_xor(m, 8); // m0+m2, m1+m3
+            m = m + __shfl_xor(m, 4);
+            v = v + m;
+        }
+        if (j == 0 && valid) {
+            const size_t o = (size_t)col * a.rows + row;
+            a.y[o] = a.resid ? a.resid[o] + v : v;
+        }
+    }
+}
+
+template <int TYPE, int NC, int KS>
+int launch_ks(const MfArgs &args, hipStream_t stream) {
+    // prefetch depth and chunk (CH a multiple of KS * PF); two chunk buffers in LDS
+    constexpr int PF = NC <= 4 ? 4 : 2;
+    constexpr int CH = KS * PF * (NC <= 2 ? 2 : 1);
+    constexpr int ROWS = 64 / KS;
+    const dim3 grid((unsigned)((args.rows + ROWS - 1) / ROWS)), block(256);
+    hipLaunchKernelGGL((kq_mfma_kernel<TYPE, NC, KS, PF, CH>), grid, block, 0, stream, args);
+    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_mfma launch");
+}
+
+// Split K across waves when the rows alone give too few waves to keep HBM busy (256 CUs want >= ~8 each).
+template <int TYPE, int NC>
+int launch_nc(const MfArgs &args, hipStream_t stream) {
+    const int waves = (args.rows + 15) / 16;
+    if (waves >= 2048 || args.nb < 8) return launch_ks<TYPE, NC, 1>(args, stream);
+    if (waves >= 1024) return launch_ks<TYPE, NC, 2>(args, stream);
+    return launch_ks<TYPE, NC, 4>(args, stream);
+}
+
+template <int TYPE>
+int launch_type(const MfArgs &args, size_t ncols, hipStream_t stream) {
+    switch (ncols) {
+    case 1: return launch_nc<TYPE, 1>(args, stream);
+    case 2: return launch_nc<TYPE, 2>(args, stream);
+    case 3: return launch_nc<TYPE, 3>(args, stream);
+    case 4: return launch_nc<TYPE, 4>(args, stream);
+    case 5: return launch_nc<TYPE, 5>(args, stream);
+    case 6: return launch_nc<TYPE, 6>(args, stream);
+    case 7: return launch_nc<TYPE, 7>(args, stream);
+    case 8: return launch_nc<TYPE, 8>(args, stream);
+    default: return fail(AQ_EINVAL, "kq_mfma: ncols must be 1..8");
+    }
+}
+
+} // namespace
+
+int launch_kq_mfma(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream) {
+    MfArgs args{};
+    args.qa = w.qa;
+    args.qb = w.qb;
+    args.sc = w.sc;
+    args.dm = w.dm;
+    args.rows = (int)w.rows;
+    args.nb = (int)w.nb;
+    args.xqs = x.qs;
+    args.xd = x.d;
+    args.xbs = x.bs;
+    args.xq8s = x.q8s;
+    args.xcol = x.n;
+    args.y = y;
+    args.resid = resid;
+    switch (w.type) {
+    case AQ_TYPE_Q4_K: return launch_type<AQ_TYPE_Q4_K>(args, ncols, stream);
+    case AQ_TYPE_Q5_K: return launch_type<AQ_TYPE_Q5_K>(args, ncols, stream);
+    case AQ_TYPE_Q6_K: return launch_type<AQ_TYPE_Q6_K>(args, ncols, stream);
+    default: return fail(AQ_EUNSUP, "kq_mfma: not a K-quant type");
+    }
+}
+
+} // namespace aq

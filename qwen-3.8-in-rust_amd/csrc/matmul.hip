@@ -55,14 +55,14 @@ __global__ void __launch_bounds__(256) kq_matmul_kernel(KqArgs a) {
     for (int sb = 0; sb < nb; sb++) {
         const size_t wsb = (size_t)row * nb + sb;
         // ---------------------------------------------------------------- weights of this super-block
-        const uint4 qa = *reinterpret_cast<const uint4 *>(a.qa + wsb * 128 + l * 16);
+        const uint4 qa = *reinterpret_cast<const uint4 *>(a.qa + wsb * 128 + lane_slot(l) * 16);
         uint32_t code[8]; // 4 unsigned codes per sub-block s, lane l's positions
         int scl[8];       // the integer scale of each of lane l's 8 sub-blocks
         int mn0 = 0, mn1 = 0;
         int off_sc0 = 0, off_sc1 = 0; // Q6_K: scales of groups 2l, 2l+1 (the -32 fold)
         float dw, dminw = 0.0f;
         if constexpr (TYPE == AQ_TYPE_Q4_K || TYPE == AQ_TYPE_Q5_K) {
-            const uint32_t *s12 = reinterpret_cast<const uint32_t *>(a.sc + wsb * 12);
+            const uint32_t *s12 = reinterpret_cast<const uint32_t *>(a.sc + wsb * 16 + 4);
             const uint32_t q0 = s12[0], q1 = s12[1], q2 = s12[2];
             const uint32_t sc_lo = q0 & 0x3F3F3F3Fu;                                  // sc[0..3]
             const uint32_t mn_lo = q1 & 0x3F3F3F3Fu;                                  // mn[0..3]
@@ -79,7 +79,7 @@ __global__ void __launch_bounds__(256) kq_matmul_kernel(KqArgs a) {
             mn1 = (mnw >> (16 * (l & 1) + 8)) & 0xFF;
             const uint32_t w4[4] = {qa.x, qa.y, qa.z, qa.w};
             uint32_t qh = 0;
-            if constexpr (TYPE == AQ_TYPE_Q5_K) qh = *reinterpret_cast<const uint32_t *>(a.qb + wsb * 32 + l * 4);
+            if constexpr (TYPE == AQ_TYPE_Q5_K) qh = *reinterpret_cast<const uint32_t *>(a.qb + wsb * 32 + lane_slot(l) * 4);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 code[2 * j] = w4[j] & 0x0F0F0F0Fu;
@@ -89,11 +89,11 @@ __global__ void __launch_bounds__(256) kq_matmul_kernel(KqArgs a) {
                     code[2 * j + 1] |= ((qh >> (2 * j + 1)) & 0x01010101u) << 4;
                 }
             }
-            const uint32_t dmw = *reinterpret_cast<const uint32_t *>(a.dm + wsb * 4);
+            const uint32_t dmw = *reinterpret_cast<const uint32_t *>(a.sc + wsb * 16);
             dw = half_bits_to_float((uint16_t)(dmw & 0xFFFF));
             dminw = half_bits_to_float((uint16_t)(dmw >> 16));
         } else { // Q6_K
-            const uint2 qh2 = *reinterpret_cast<const uint2 *>(a.qb + wsb * 64 + l * 8);
+            const uint2 qh2 = *reinterpret_cast<const uint2 *>(a.qb + wsb * 64 + lane_slot(l) * 8);
             const uint4 s16 = *reinterpret_cast<const uint4 *>(a.sc + wsb * 16);
             const uint32_t sw[4] = {s16.x, s16.y, s16.z, s16.w};
             const uint32_t ql[4] = {qa.x, qa.y, qa.z, qa.w}; // (h, jj) = 0:(0,0) 1:(0,1) 2:(1,0) 3:(1,1)
@@ -117,7 +117,7 @@ __global__ void __launch_bounds__(256) kq_matmul_kernel(KqArgs a) {
         // ---------------------------------------------------------------- every activation column
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            const size_t xb = (size_t)c * a.xcol + (size_t)sb * 256 + l * 32;
+            const size_t xb = (size_t)c * a.xcol + (size_t)sb * 256 + lane_slot(l) * 32;
             const uint4 x0 = *reinterpret_cast<const uint4 *>(a.xqs + xb);
             const uint4 x1 = *reinterpret_cast<const uint4 *>(a.xqs + xb + 16);
             const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -274,23 +274,24 @@ __global__ void repack_kernel(int type, size_t nblocks, uint8_t *ggml, uint8_t *
     case AQ_TYPE_Q5_K: {
         const bool q5 = type == AQ_TYPE_Q5_K;
         uint8_t *g = ggml + i * (q5 ? 176 : 144);
-        for (int b = 0; b < 4; b++) mv(dm + i * 4 + b, g + b);
-        for (int b = 0; b < 12; b++) mv(sc + i * 12 + b, g + 4 + b);
+        for (int b = 0; b < 16; b++) mv(sc + i * 16 + b, g + b); // d, dmin, 12 scale bytes
         if (q5)
-            for (int b = 0; b < 32; b++) mv(qb + i * 32 + b, g + 16 + b);
+            for (int l = 0; l < 8; l++)
+                for (int b = 0; b < 4; b++) mv(qb + i * 32 + lane_slot(l) * 4 + b, g + 16 + 4 * l + b);
         uint8_t *qs = g + (q5 ? 48 : 16);
         for (int l = 0; l < 8; l++)
             for (int j = 0; j < 4; j++)
-                for (int b = 0; b < 4; b++) mv(qa + i * 128 + l * 16 + j * 4 + b, qs + 32 * j + 4 * l + b);
+                for (int b = 0; b < 4; b++) mv(qa + i * 128 + lane_slot(l) * 16 + j * 4 + b, qs + 32 * j + 4 * l + b);
         break;
     }
     case AQ_TYPE_Q6_K: {
         uint8_t *g = ggml + i * 210;
         for (int l = 0; l < 8; l++)
             for (int h = 0; h < 2; h++) {
+                const int sl = lane_slot(l);
                 for (int jj = 0; jj < 2; jj++)
-                    for (int b = 0; b < 4; b++) mv(qa + i * 128 + l * 16 + (h * 2 + jj) * 4 + b, g + h * 64 + jj * 32 + 4 * l + b);
-                for (int b = 0; b < 4; b++) mv(qb + i * 64 + l * 8 + h * 4 + b, g + 128 + h * 32 + 4 * l + b);
+                    for (int b = 0; b < 4; b++) mv(qa + i * 128 + sl * 16 + (h * 2 + jj) * 4 + b, g + h * 64 + jj * 32 + 4 * l + b);
+                for (int b = 0; b < 4; b++) mv(qb + i * 64 + sl * 8 + h * 4 + b, g + 128 + h * 32 + 4 * l + b);
             }
         for (int b = 0; b < 16; b++) mv(sc + i * 16 + b, g + 192 + b);
         for (int b = 0; b < 2; b++) mv(dm + i * 2 + b, g + 208 + b);
@@ -379,7 +380,7 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
 } // namespace
 
 int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream) {
-    if (is_kquant(w.type)) return launch_kq<false>(w, x, ncols, y, resid, nullptr, nullptr, stream);
+    if (is_kquant(w.type)) return launch_kq_mfma(w, x, ncols, y, resid, stream);
     Q8Args args{};
     args.type = w.type;
     args.qa = w.qa;
@@ -404,6 +405,10 @@ int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const f
     case 8: return launch_q8_nc<8>(args, stream);
     default: return fail(AQ_EINVAL, "matmul: ncols must be 1..8 for Q8_0/Q4_0/F32 weights in this build");
     }
+}
+
+int launch_kq_dot4(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream) {
+    return launch_kq<false>(w, x, ncols, y, resid, nullptr, nullptr, stream);
 }
 
 int launch_kq_isums(const Weight &w, const Act &x, int32_t *lanes, int32_t *mins, hipStream_t stream) {

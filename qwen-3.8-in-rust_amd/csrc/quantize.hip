@@ -58,7 +58,7 @@ __global__ void __launch_bounds__(256) q8k_quantize_kernel(const float *__restri
     const int s = lane >> 3, l = lane & 7;
     const uint32_t packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) | ((uint32_t)(uint8_t)q[2] << 16) |
                             ((uint32_t)(uint8_t)q[3] << 24);
-    *reinterpret_cast<uint32_t *>(qs + qbase + l * 32 + s * 4) = packed;
+    *reinterpret_cast<uint32_t *>(qs + qbase + lane_slot(l) * 32 + s * 4) = packed;
     int sum = q[0] + q[1] + q[2] + q[3];
     sum += __shfl_xor(sum, 1);
     sum += __shfl_xor(sum, 2); // group of 16 = 4 lanes

@@ -32,8 +32,8 @@ static int alloc_weight(Weight &w, int type, size_t rows, size_t cols, int devic
     w.nb = cols / be;
     w.device = device;
     switch (type) {
-    case AQ_TYPE_Q4_K: w.qa_bytes = 128; w.qb_bytes = 0; w.sc_bytes = 12; w.dm_bytes = 4; break;
-    case AQ_TYPE_Q5_K: w.qa_bytes = 128; w.qb_bytes = 32; w.sc_bytes = 12; w.dm_bytes = 4; break;
+    case AQ_TYPE_Q4_K: w.qa_bytes = 128; w.qb_bytes = 0; w.sc_bytes = 16; w.dm_bytes = 0; break;
+    case AQ_TYPE_Q5_K: w.qa_bytes = 128; w.qb_bytes = 32; w.sc_bytes = 16; w.dm_bytes = 0; break;
     case AQ_TYPE_Q6_K: w.qa_bytes = 128; w.qb_bytes = 64; w.sc_bytes = 16; w.dm_bytes = 2; break;
     case AQ_TYPE_Q8_0: w.qa_bytes = 32; w.qb_bytes = 0; w.sc_bytes = 0; w.dm_bytes = 2; break;
     case AQ_TYPE_Q4_0: w.qa_bytes = 16; w.qb_bytes = 0; w.sc_bytes = 0; w.dm_bytes = 2; break;
@@ -310,7 +310,7 @@ int aq_act_get_q8k(const aq_act *a, void *ggml_out, size_t ncols) {
             const int8_t *src = qs.data() + c * x.n + b * 256;
             for (int s = 0; s < 8; s++)
                 for (int l = 0; l < 8; l++)
-                    for (int j = 0; j < 4; j++) blk[4 + 32 * s + 4 * l + j] = (uint8_t)src[l * 32 + s * 4 + j];
+                    for (int j = 0; j < 4; j++) blk[4 + 32 * s + 4 * l + j] = (uint8_t)src[lane_slot(l) * 32 + s * 4 + j];
             std::memcpy(blk + 260, &bs[(c * x.nb + b) * 16], 32);
         }
     return 0;

@@ -169,6 +169,8 @@ def test_q8_weight_dots_bit_exact_on_fixture_rows(ctx):
 
 
 @pytest.mark.parametrize("t,rows,cols", [(aq.Q4_K, 17408, 5120), (aq.Q6_K, 5120, 17408), (aq.Q5_K, 1024, 5120),
+                                         (aq.Q4_K, 12288, 5120), (aq.Q4_K, 5120, 6144), (aq.Q6_K, 10240, 5120),
+                                         (aq.Q5_K, 5120, 6144), (aq.Q4_K, 1000, 512),
                                          (aq.Q8_0, 5120, 6144), (aq.Q4_0, 1024, 5120), (aq.Q4_0, 512, 17408),
                                          (aq.F32, 48, 5120)])
 def test_matmul_full_shapes_bit_exact_and_column_identity(ctx, t, rows, cols):
