@@ -161,6 +161,85 @@ int aq_weight_synth(aq_ctx *ctx, const aq_synth_spec *spec, aq_weight **out);
 int aq_matmul_time(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_act *x, size_t ncols,
                    float *y_dev, int iters, double *us_per_launch);
 
+/* ------------------------------------------------------------------------------------------- model level */
+
+/* Type mixes of the synthetic models. AQ_MIX_Q4_K_M: the per-tensor type table of a llama.cpp Q4_K_M file of
+ * the 27B hybrid (docs/data/q4km_type_breakdown.txt, docs/data/gguf_layout.txt); AQ_MIX_TINY: Q4_K for every
+ * matrix except ffn_down and output (Q6_K), F32 ssm_alpha/ssm_beta. */
+#define AQ_MIX_Q4_K_M 0
+#define AQ_MIX_TINY 1
+
+/* One tensor of a synthetic model: its GGUF name and how to generate it. */
+typedef struct aq_tensor_plan {
+    char name[64];
+    aq_synth_spec spec;
+} aq_tensor_plan;
+
+/* The tensor list of a synthetic model (GGUF names, shapes as the loader checks them, types from `mix`,
+ * weights ~N(0, 0.02), norm weights 1, ssm_a ~ -U(0, 16), ssm_dt.bias 1). With out == NULL only *n_out is set.
+ * Replaces the reference's checkpoint builders (tools/make_tiny_checkpoint.py) for random-init models. */
+int aq_model_plan(const aq_model_config *cfg, int mix, uint64_t seed, aq_tensor_plan *out, size_t cap,
+                  size_t *n_out);
+
+/* Whole model resident in device memory, from ggml tensors on the host (what a GGUF reader hands over;
+ * `Model::load` model.rs:140-356 + `WeightMat::new` matvec.rs:59-63) or generated on the device from the plan
+ * (same bytes as aq_synth_host of each plan entry). Matrices: Q4_K/Q5_K/Q6_K/Q8_0/Q4_0/F32; vectors F32. */
+int aq_model_load(aq_ctx *ctx, const aq_model_config *cfg, const aq_tensor *tensors, size_t n, aq_model **out);
+int aq_model_synth(aq_ctx *ctx, const aq_model_config *cfg, int mix, uint64_t seed, aq_model **out);
+int aq_model_free(aq_model *m);
+
+/* Bytes of the weights one pass reads: the decoder layers + output norm + lm_head (`main`), the MTP block with
+ * eh_proj and its norms (`mtp_block`), the lm_head alone (`lm_head`). */
+typedef struct aq_model_bytes {
+    uint64_t main, mtp_block, lm_head, embed_row;
+} aq_model_bytes;
+int aq_model_get_bytes(const aq_model *m, aq_model_bytes *out);
+
+/* Per-sequence state: DeltaNet conv/recurrent state, KV caches, the speculative buffers (spec_k drafts,
+ * 0 = plain decode only) for positions < max_pos. `Model::new_state_spec` spec.rs:184 + `State::reserve`
+ * model.rs:123. spec_k <= 7. */
+int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out);
+int aq_state_free(aq_state *s);
+
+/* `Model::prefill` (model.rs:443-461): the prompt through every layer; logits of the last row (nullable, vocab
+ * floats) and their argmax. */
+int aq_prefill(aq_state *s, const uint32_t *ids, size_t n, float *logits_last_host, uint32_t *argmax_out);
+/* `Model::forward_token` (model.rs:486-490) + `argmax` (505-513). */
+int aq_forward_token(aq_state *s, uint32_t id, float *logits_host, uint32_t *argmax_out);
+/* `Model::spec_prefill` (spec.rs:229-272): the prompt, x_T = argmax of the last row, the MTP over the prompt and
+ * the first k drafts. */
+int aq_spec_prefill(aq_state *s, const uint32_t *ids, size_t n, uint32_t *x_t);
+/* `Model::spec_round` (spec.rs:326-433), greedy: verify [x_p, d_1..d_k] in one batch, accept on the device,
+ * commit the DeltaNet state of the accepted rows, truncate the KV caches, re-feed the MTP and draft the next k.
+ * emitted: capacity k+1; *m = accepted drafts; *n_emitted = m+1. */
+int aq_spec_round(aq_state *s, uint32_t x_p, uint32_t *emitted, uint32_t *n_emitted, uint32_t *m);
+/* `Model::spec_set_drafts` (spec.rs:436) test hook, and the current drafts. */
+int aq_spec_set_drafts(aq_state *s, const uint32_t *d, size_t k);
+int aq_spec_get_drafts(aq_state *s, uint32_t *d, size_t k);
+/* Row i (< k+1) of the last verify batch's logits. */
+int aq_spec_logits_row(aq_state *s, size_t i, float *host_out);
+int aq_spec_get_stats(aq_state *s, aq_spec_stats *out);
+int aq_state_pos(const aq_state *s, uint32_t *pos);
+/* The state as f32, in this order: per layer, attention: K then V rows [0, len); DeltaNet: the recurrent
+ * state then the conv window; then the MTP K and V rows. With out == NULL only *n_out is set. */
+int aq_state_export(aq_state *s, float *out, size_t cap, size_t *n_out);
+
+/* One decoder piece on its own (the reference's layer tests, tests/layers.rs:109-271): kind 0 DeltaNet mixer,
+ * 1 attention mixer, 2 MLP, 3 decoder layer with DeltaNet, 4 with attention; tensors "blk.0.*". x: t rows of
+ * hidden (host); conv/rec (DeltaNet) and k_cache/v_cache (kv_cap rows of n_head_kv*head_dim, *kv_len used) are
+ * read and updated on the host; y: t rows of hidden. */
+int aq_layer_run(aq_ctx *ctx, const aq_model_config *cfg, const aq_tensor *tensors, size_t n, int kind,
+                 const float *x, size_t t, uint32_t start_pos, float *conv, float *rec, float *k_cache,
+                 float *v_cache, uint32_t *kv_len, uint32_t kv_cap, float *y);
+
+/* The Gated-DeltaNet recurrence alone (deltanet.rs:43-86), with speculative rollback: from `state_dev`
+ * (nv x dk x dv f32, device), t rows of q, k (t x nk*dk, already normalised), v (t x nv*dv), g and beta
+ * (t x nv) give out (t x nv*dv); the state is then advanced by the first `keep` rows only (keep <= t),
+ * as the reference's snapshot / restore / replay leaves it (spec.rs:154-179, 396-415). Host arrays. */
+int aq_deltanet_verify_commit(aq_ctx *ctx, uint32_t nk, uint32_t nv, uint32_t dk, uint32_t dv, size_t t, size_t keep,
+                              const float *q, const float *k, const float *v, const float *g, const float *beta,
+                              float *state_dev, float *out);
+
 #ifdef __cplusplus
 }
 #endif

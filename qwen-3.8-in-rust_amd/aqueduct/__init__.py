@@ -78,6 +78,26 @@ def lib():
         "aq_matmul_time": (i, [P, P, sz, P, sz, P, i, C.POINTER(C.c_double)]),
         "aq_synth_host": (i, [P, P, i]),
         "aq_weight_synth": (i, [P, P, C.POINTER(P)]),
+        "aq_model_plan": (i, [P, i, C.c_uint64, P, sz, C.POINTER(sz)]),
+        "aq_model_load": (i, [P, P, P, sz, C.POINTER(P)]),
+        "aq_model_synth": (i, [P, P, i, C.c_uint64, C.POINTER(P)]),
+        "aq_model_free": (i, [P]),
+        "aq_model_get_bytes": (i, [P, P]),
+        "aq_state_new": (i, [P, C.c_uint32, C.c_uint32, C.POINTER(P)]),
+        "aq_state_free": (i, [P]),
+        "aq_prefill": (i, [P, P, sz, P, P]),
+        "aq_forward_token": (i, [P, C.c_uint32, P, P]),
+        "aq_spec_prefill": (i, [P, P, sz, P]),
+        "aq_spec_round": (i, [P, C.c_uint32, P, P, P]),
+        "aq_spec_set_drafts": (i, [P, P, sz]),
+        "aq_spec_get_drafts": (i, [P, P, sz]),
+        "aq_spec_logits_row": (i, [P, sz, P]),
+        "aq_spec_get_stats": (i, [P, P]),
+        "aq_state_pos": (i, [P, P]),
+        "aq_state_export": (i, [P, P, sz, C.POINTER(sz)]),
+        "aq_layer_run": (i, [P, P, P, sz, i, P, sz, C.c_uint32, P, P, P, P, P, C.c_uint32, P]),
+        "aq_deltanet_verify_commit": (i, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, sz, sz, P, P, P, P, P,
+                                          P, P]),
     }
     for name, (res, args) in sigs.items():
         f = getattr(L, name)
@@ -267,3 +287,189 @@ def device_count():
     n = C.c_int()
     check(lib().aq_device_count(C.byref(n)))
     return n.value
+
+
+# ------------------------------------------------------------------------------------------------ model level
+MIX_Q4_K_M, MIX_TINY = 0, 1
+
+
+class AqTensorPlan(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("spec", AqSynthSpec)]
+
+
+class AqModelBytes(C.Structure):
+    _fields_ = [("main", C.c_uint64), ("mtp_block", C.c_uint64), ("lm_head", C.c_uint64), ("embed_row", C.c_uint64)]
+
+
+def config(**kw):
+    c = AqModelConfig()
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+def tiny_config():
+    """The tiny hybrid of the correctness config: 3 DeltaNet layers + 1 attention layer + the MTP block."""
+    return config(n_layer=4, hidden=256, ffn=768, vocab=4096, n_head=4, n_head_kv=2, head_dim=64, rope_dim=16,
+                  rope_theta=1e7, rms_eps=1e-6, full_attention_interval=4, dn_n_k_heads=2, dn_n_v_heads=4,
+                  dn_head_dim_k=64, dn_head_dim_v=64, dn_conv_kernel=4, has_mtp=1)
+
+
+def config_27b():
+    """The 27B hybrid's shapes (docs/model-facts.md:22-123 of the reference)."""
+    return config(n_layer=64, hidden=5120, ffn=17408, vocab=248320, n_head=24, n_head_kv=4, head_dim=256,
+                  rope_dim=64, rope_theta=1e7, rms_eps=1e-6, full_attention_interval=4, dn_n_k_heads=16,
+                  dn_n_v_heads=48, dn_head_dim_k=128, dn_head_dim_v=128, dn_conv_kernel=4, has_mtp=1)
+
+
+def model_plan(cfg, mix, seed):
+    """[(name, AqSynthSpec)] of a synthetic model (aq_model_plan)."""
+    n = C.c_size_t()
+    check(lib().aq_model_plan(C.byref(cfg), mix, seed, None, 0, C.byref(n)))
+    arr = (AqTensorPlan * n.value)()
+    check(lib().aq_model_plan(C.byref(cfg), mix, seed, arr, n.value, C.byref(n)))
+    return [(e.name.decode(), AqSynthSpec(e.spec.ggml_type, e.spec.rows, e.spec.cols, e.spec.seed, e.spec.dist,
+                                          e.spec.a, e.spec.b)) for e in arr]
+
+
+def plan_tensors(plan, threads=0):
+    """Host ggml bytes of every plan entry: [(name, type, rows, cols, data)]."""
+    return [(name, sp.ggml_type, sp.rows, sp.cols, synth_host(sp, threads)) for name, sp in plan]
+
+
+def tensor_table(tensors):
+    arr = (AqTensor * len(tensors))()
+    keep = []
+    for i, (name, t, rows, cols, data) in enumerate(tensors):
+        data = np.ascontiguousarray(data)
+        nb = name.encode()
+        keep += [nb, data]
+        arr[i] = AqTensor(nb, t, rows, cols, data.ctypes.data, data.nbytes)
+    return arr, keep
+
+
+class Model:
+    """aq_model: the whole model resident in device memory (the reference's Model, model.rs)."""
+
+    def __init__(self, ctx: Context, cfg, tensors=None, mix=None, seed=None):
+        self.ctx, self.cfg = ctx, cfg
+        h = C.c_void_p()
+        if tensors is not None:
+            table, keep = tensor_table(tensors)
+            check(lib().aq_model_load(ctx.h, C.byref(cfg), table, len(tensors), C.byref(h)))
+        else:
+            check(lib().aq_model_synth(ctx.h, C.byref(cfg), mix, seed, C.byref(h)))
+        self.h = h
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().aq_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()
+
+    def bytes(self):
+        b = AqModelBytes()
+        check(lib().aq_model_get_bytes(self.h, C.byref(b)))
+        return {"main": b.main, "mtp_block": b.mtp_block, "lm_head": b.lm_head, "embed_row": b.embed_row}
+
+
+class State:
+    """aq_state: one sequence (the reference's State + spec buffers, model.rs / spec.rs)."""
+
+    def __init__(self, model: Model, spec_k=0, max_pos=512):
+        self.model, self.k = model, spec_k
+        h = C.c_void_p()
+        check(lib().aq_state_new(model.h, spec_k, max_pos, C.byref(h)))
+        self.h = h
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().aq_state_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()
+
+    @property
+    def pos(self):
+        p = C.c_uint32()
+        check(lib().aq_state_pos(self.h, C.byref(p)))
+        return p.value
+
+    def forward_token(self, tok, want_logits=False):
+        lg = np.zeros(self.model.cfg.vocab, np.float32) if want_logits else None
+        a = C.c_uint32()
+        check(lib().aq_forward_token(self.h, tok, ptr(lg), C.byref(a)))
+        return (a.value, lg) if want_logits else a.value
+
+    def prefill(self, ids, want_logits=False):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        lg = np.zeros(self.model.cfg.vocab, np.float32) if want_logits else None
+        a = C.c_uint32()
+        check(lib().aq_prefill(self.h, ptr(ids), ids.size, ptr(lg), C.byref(a)))
+        return (a.value, lg) if want_logits else a.value
+
+    def spec_prefill(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        x = C.c_uint32()
+        check(lib().aq_spec_prefill(self.h, ptr(ids), ids.size, C.byref(x)))
+        return x.value
+
+    def spec_round(self, x_p):
+        em = np.zeros(self.k + 1, np.uint32)
+        n, m = C.c_uint32(), C.c_uint32()
+        check(lib().aq_spec_round(self.h, x_p, ptr(em), C.byref(n), C.byref(m)))
+        return m.value, em[: n.value].tolist()
+
+    def set_drafts(self, d):
+        d = np.ascontiguousarray(d, dtype=np.uint32)
+        check(lib().aq_spec_set_drafts(self.h, ptr(d), d.size))
+
+    def drafts(self):
+        d = np.zeros(self.k, np.uint32)
+        check(lib().aq_spec_get_drafts(self.h, ptr(d), self.k))
+        return d.tolist()
+
+    def logits_row(self, i):
+        out = np.zeros(self.model.cfg.vocab, np.float32)
+        check(lib().aq_spec_logits_row(self.h, i, ptr(out)))
+        return out
+
+    def stats(self):
+        st = AqSpecStats()
+        check(lib().aq_spec_get_stats(self.h, C.byref(st)))
+        return {"rounds": st.rounds, "drafted": st.drafted, "accepted": st.accepted, "emitted": st.emitted,
+                "hist": list(st.hist), "verify_ms": st.verify_ms, "commit_ms": st.commit_ms,
+                "refeed_ms": st.refeed_ms, "chain_ms": st.chain_ms}
+
+    def export(self):
+        n = C.c_size_t()
+        check(lib().aq_state_export(self.h, None, 0, C.byref(n)))
+        out = np.zeros(n.value, np.float32)
+        check(lib().aq_state_export(self.h, ptr(out), out.size, C.byref(n)))
+        return out
+
+
+def layer_run(ctx: Context, cfg, tensors, kind, x, start_pos, conv=None, rec=None, k_cache=None, v_cache=None,
+              kv_len=0, kv_cap=0):
+    """One decoder piece (aq_layer_run); conv/rec/k_cache/v_cache are updated in place. Returns (y, kv_len)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    t = x.shape[0]
+    y = np.zeros_like(x)
+    table, keep = tensor_table(tensors)
+    kl = C.c_uint32(kv_len)
+    check(lib().aq_layer_run(ctx.h, C.byref(cfg), table, len(tensors), kind, ptr(x), t, start_pos, ptr(conv),
+                             ptr(rec), ptr(k_cache), ptr(v_cache), C.byref(kl), kv_cap, ptr(y)))
+    return y, kl.value
+
+
+def deltanet_verify_commit(ctx: Context, nk, nv, dk, dv, keep, q, k, v, g, beta, state: DeviceBuffer):
+    """The isolated recurrence with rollback (aq_deltanet_verify_commit): returns out [t, nv*dv]."""
+    q, k, v, g, beta = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v, g, beta))
+    t = q.shape[0]
+    out = np.zeros((t, nv * dv), np.float32)
+    check(lib().aq_deltanet_verify_commit(ctx.h, nk, nv, dk, dv, t, keep, ptr(q), ptr(k), ptr(v), ptr(g), ptr(beta),
+                                          state.p, ptr(out)))
+    return out

@@ -196,13 +196,14 @@ __global__ void __launch_bounds__(256) q8_matmul_kernel(Q8Args a) {
     if (row < a.rows) {
         for (int b = j; b < nb; b += TPR) {
             const size_t wb = (size_t)row * nb + b;
-            if (a.type == AQ_TYPE_F32) {
+            if (a.type == AQ_TYPE_F32) { // the last block may be the reference's short tail
                 const float *w = reinterpret_cast<const float *>(a.qa) + (size_t)row * a.n + (size_t)b * 32;
+                const int ne = a.n - (size_t)b * 32 < 32 ? (int)(a.n - (size_t)b * 32) : 32;
 #pragma unroll
                 for (int c = 0; c < NC; c++) {
                     const float *x = a.xf + (size_t)c * a.n + (size_t)b * 32;
                     float part = 0.0f;
-                    for (int e = 0; e < 32; e++) part += w[e] * x[e];
+                    for (int e = 0; e < ne; e++) part += w[e] * x[e];
                     prods[(r_loc * nb + b) * NC + c] = part;
                 }
                 continue;
@@ -246,8 +247,9 @@ __global__ void __launch_bounds__(256) q8_matmul_kernel(Q8Args a) {
         if (orow < a.rows) {
             float acc = 0.0f;
             if (a.type == AQ_TYPE_F32) {
+                // dot.rs:180-200: full blocks, then `acc + part` with the tail's partial (0.0f when there is none)
                 for (int b = 0; b < nb; b++) acc += prods[(rr * nb + b) * NC + c];
-                acc = acc + 0.0f; // dot.rs:199 `acc + part` with an empty tail
+                if (a.n % 32 == 0) acc = acc + 0.0f;
             } else {
                 for (int b = 0; b < nb; b++) acc += prods[(rr * nb + b) * NC + c];
             }
@@ -386,7 +388,7 @@ int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const f
     args.qa = w.qa;
     args.dm = w.dm;
     args.rows = (int)w.rows;
-    args.nb32 = (int)(w.type == AQ_TYPE_F32 ? w.cols / 32 : w.nb);
+    args.nb32 = (int)(w.type == AQ_TYPE_F32 ? (w.cols + 31) / 32 : w.nb);
     args.xq = x.q0;
     args.xd = x.d0;
     args.xs = x.s0;

@@ -1,0 +1,89 @@
+// ops.h — launchers of the model-level kernels (ops.hip): embedding rows, RMSNorm with the fused activation
+// quantiser, SwiGLU with the fused quantiser, the Gated-DeltaNet head kernel (conv + recurrence + gated norm),
+// the attention prologue and decode kernels, argmax and the greedy acceptance. Every launcher returns 0 or an
+// AQ_E* code and runs on `stream`.
+#pragma once
+
+#include "aq_common.h"
+
+namespace aq {
+
+// What a row kernel writes besides (optionally) f32: nothing, Q8_K (for K-quant weights) or Q8_0 (for Q8_0 /
+// Q4_0 weights). F32 weights read the f32 rows.
+enum QuantKind { QK_NONE = 0, QK_Q8K = 1, QK_Q80 = 2 };
+inline QuantKind quant_kind_for(int weight_type) {
+    if (is_kquant(weight_type)) return QK_Q8K;
+    if (weight_type == AQ_TYPE_Q8_0 || weight_type == AQ_TYPE_Q4_0) return QK_Q80;
+    return QK_NONE;
+}
+
+// Where a row kernel puts the quantised form: column `col0 + row` of `act`, starting at element `elem_off`
+// (a multiple of 256 for Q8_K, of 32 for Q8_0). Also writes act.f32 there when `f32` is set.
+struct QuantOut {
+    const Act *act = nullptr;
+    QuantKind kind = QK_NONE;
+    size_t col0 = 0, elem_off = 0;
+    bool f32 = false;
+};
+
+// out[i * out_stride + e] = dequantised row ids[i] of `w` (model.rs:364-368; Q4_K only).
+int launch_embed(const Weight &w, const uint32_t *ids, size_t t, float *out, size_t out_stride, hipStream_t stream);
+
+// y = (x * inv_rms(x)) * w per row (rmsnorm.rs:14-76), t rows of n; y_f32 optional (row stride y_stride).
+int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t, float *y_f32,
+                   size_t y_stride, const QuantOut &q, hipStream_t stream);
+
+// h = silu(g) * u elementwise over t rows of n (act.rs:24-30), into the quantised form (and h_f32 if set).
+int launch_swiglu(const float *g, const float *u, size_t n, size_t t, float *h_f32, const QuantOut &q,
+                  hipStream_t stream);
+
+struct DnArgs {
+    const float *mixed = nullptr; // t x cd conv inputs (the qkv projection)
+    const float *z = nullptr;     // t x vd output gate (null: no output)
+    const float *a = nullptr, *b = nullptr; // t x nv gate pre-activations
+    const float *conv_src = nullptr;        // cd x (K-1) window
+    float *conv_dst = nullptr;              // null: window not written
+    const float *conv_w = nullptr;          // cd x K
+    const float *ssm_a = nullptr, *dt_bias = nullptr, *ssm_norm = nullptr;
+    float eps = 0.0f, qscale = 0.0f;
+    float *rec = nullptr; // nv x dk x dv recurrent state
+    int write_state = 0;
+    float *out = nullptr; // t x vd gated-norm output (null: none)
+    int t = 0, nk = 0, nv = 0, dk = 0, dv = 0, kernel = 0;
+    // raw mode (the isolated recurrence): q, k (t x nk*dk), v (t x nv*dv), g, beta (t x nv) used as given
+    int raw = 0;
+    const float *rq = nullptr, *rk = nullptr, *rv = nullptr, *rg = nullptr, *rbeta = nullptr;
+};
+int launch_dn_core(const DnArgs &a, hipStream_t stream);
+
+struct AttnArgs {
+    const float *qg = nullptr;          // t x (2*nh*hd): per head [q | gate]
+    const float *kk = nullptr, *vv = nullptr; // t x nkv*hd
+    const float *q_norm = nullptr, *k_norm = nullptr;
+    float eps = 0.0f, scaling = 0.0f;
+    const float *cos_tab = nullptr, *sin_tab = nullptr; // per position: rope_dim/2 values
+    size_t start_pos = 0;        // position of row 0 (rope)
+    float *q = nullptr;          // t x nh*hd scratch (post norm + rope)
+    float *kcache = nullptr, *vcache = nullptr;
+    size_t base = 0;             // cache rows before row 0
+    size_t stride = 0;           // nkv*hd
+    float *out = nullptr;        // t x nh*hd
+    int t = 0, nh = 0, nkv = 0, hd = 0, rd = 0;
+};
+// Norm + RoPE of q and k, K/V appended at cache rows base..base+t, then per (head, row) softmax attention over
+// base + row + 1 positions with the sigmoid output gate (gqa_attention.rs:327-418).
+int launch_attention(const AttnArgs &a, hipStream_t stream);
+
+// ids[r] = argmax of row r of x (t rows of n, row stride `stride`), first maximum wins (model.rs:505-513).
+// `scratch` holds at least argmax_scratch_bytes(n, t).
+size_t argmax_scratch_bytes(size_t n, size_t t);
+int launch_argmax(const float *x, size_t n, size_t stride, size_t t, uint32_t *ids, void *scratch, hipStream_t stream);
+
+// Greedy acceptance (spec.rs:355-366): info = {m, n_emitted, keep}, emitted[0..n_emitted).
+int launch_accept(const uint32_t *argmax_ids, const uint32_t *drafts, int k, uint32_t *emitted, uint32_t *info,
+                  hipStream_t stream);
+
+// batch = [x_p, drafts[0..k)]
+int launch_make_batch(uint32_t x_p, const uint32_t *drafts, int k, uint32_t *batch, hipStream_t stream);
+
+} // namespace aq

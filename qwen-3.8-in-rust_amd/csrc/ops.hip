@@ -1,0 +1,567 @@
+// ops.hip — the model-level kernels around the matmuls: embedding rows, RMSNorm + activation quantiser, SwiGLU +
+// quantiser, the Gated-DeltaNet head kernel, attention, argmax and greedy acceptance.
+//
+// Every kernel reproduces the reference's scalar arithmetic in the reference's order (products and sums rounded
+// one by one, no FMA; sequential sums stay sequential, in one thread), so its outputs equal the CPU path's bit
+// for bit wherever the reference is exact IEEE arithmetic; exp and log1p are evaluated in double and rounded
+// once (quant_dev.h).
+#include <cmath>
+
+#include "ops.h"
+#include "quant_dev.h"
+
+namespace aq {
+namespace {
+
+// ------------------------------------------------------------------------------------------------ embedding
+// model.rs:364-368 `embed_token_into` -> quant.rs:102-133 `dequant_q4_k`: y = (d*sc)*q - (dmin*m) per element,
+// read from the Q4_K planes (sub-block s, position p = 4l + b: nibble of qa[slot(l)*16 + (s/2)*4 + b]).
+__global__ void __launch_bounds__(256) embed_q4k_kernel(Weight w, const uint32_t *ids, float *out, size_t out_stride) {
+    const size_t i = blockIdx.y, sb = blockIdx.x;
+    size_t row = ids[i];
+    if (row >= w.rows) row = w.rows - 1; // ids are validated by the host; keep every access in bounds regardless
+    const size_t wsb = row * w.nb + sb;
+    const int e = threadIdx.x, s = e >> 5, p = e & 31, l = p >> 2, b = p & 3;
+    const uint8_t byte = w.qa[wsb * 128 + lane_slot(l) * 16 + (s >> 1) * 4 + b];
+    const int q = (s & 1) ? (byte >> 4) : (byte & 0xF);
+    const uint8_t *rec = w.sc + wsb * 16;
+    const float d = f16_to_f32((uint16_t)(rec[0] | (rec[1] << 8)));
+    const float dmin = f16_to_f32((uint16_t)(rec[2] | (rec[3] << 8)));
+    const uint8_t *sc12 = rec + 4;
+    int sc, m;
+    if (s < 4) { // quant.rs:45-51 get_scale_min_k4
+        sc = sc12[s] & 63;
+        m = sc12[s + 4] & 63;
+    } else {
+        sc = (sc12[s + 4] & 0xF) | ((sc12[s - 4] >> 6) << 4);
+        m = (sc12[s + 4] >> 4) | ((sc12[s] >> 6) << 4);
+    }
+    const float d1 = d * (float)sc, m1 = dmin * (float)m;
+    out[i * out_stride + sb * 256 + e] = d1 * (float)q - m1;
+}
+
+// -------------------------------------------------------------------------------------------------- rmsnorm
+// rmsnorm.rs:25-76: ss = reduce8 of 8 interleaved sequential lanes (+ sequential tail), mean = ss/n,
+// inv = 1/sqrt(mean + eps), y = (x*inv)*w. One work-group per row; the row sits in LDS; 8 threads run the
+// 8 lane chains. Then the quantised form is written from LDS.
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const float *x, size_t x_stride, const float *w, float eps, int n,
+                                                      float *y, size_t y_stride, Act qa, int kind, size_t col0,
+                                                      size_t eoff, int act_f32) {
+    extern __shared__ float xs[]; // n + 16
+    float *red = xs + n;
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *xr = x + (size_t)row * x_stride;
+    for (int i = tid; i < n; i += 256) xs[i] = xr[i];
+    __syncthreads();
+    const int n8 = n / 8 * 8;
+    if (tid < 8) {
+        float acc = 0.0f;
+        for (int i = tid; i < n8; i += 8) acc += xs[i] * xs[i];
+        red[tid] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float ss = reduce8_f(red);
+        for (int i = n8; i < n; i++) ss += xs[i] * xs[i];
+        const float mean = ss / (float)n;
+        red[8] = 1.0f / sqrtf(mean + eps);
+    }
+    __syncthreads();
+    const float inv = red[8];
+    for (int i = tid; i < n; i += 256) {
+        const float v = (xs[i] * inv) * w[i];
+        xs[i] = v;
+        if (y) y[(size_t)row * y_stride + i] = v;
+        if (act_f32) qa.f32[(col0 + row) * qa.n + eoff + i] = v;
+    }
+    __syncthreads();
+    if (kind == QK_Q8K) {
+        const int wave = tid >> 6, lane = tid & 63;
+        for (int blk = wave; blk < n / 256; blk += 4) {
+            const float v4[4] = {xs[blk * 256 + lane * 4], xs[blk * 256 + lane * 4 + 1], xs[blk * 256 + lane * 4 + 2],
+                                 xs[blk * 256 + lane * 4 + 3]};
+            q8k_block_store(qa, col0 + row, eoff / 256 + blk, v4, lane);
+        }
+    } else if (kind == QK_Q80) {
+        for (int blk = tid; blk < n / 32; blk += 256) q8_0_block_store(qa, col0 + row, eoff / 32 + blk, xs + blk * 32);
+    }
+}
+
+// --------------------------------------------------------------------------------------------------- swiglu
+// act.rs:24-30: h = silu(g) * u. Q8_K: one wave per 256-block; Q8_0 / none: one lane per 32-block.
+__global__ void __launch_bounds__(256) swiglu_q8k_kernel(const float *g, const float *u, size_t n, size_t total,
+                                                         float *h, Act qa, size_t col0) {
+    const int lane = threadIdx.x & 63;
+    const size_t blk = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= total) return;
+    const size_t nb = n / 256, row = blk / nb, b = blk % nb;
+    const size_t e = row * n + b * 256 + lane * 4;
+    const float4 gv = *reinterpret_cast<const float4 *>(g + e), uv = *reinterpret_cast<const float4 *>(u + e);
+    const float v[4] = {silu_f(gv.x) * uv.x, silu_f(gv.y) * uv.y, silu_f(gv.z) * uv.z, silu_f(gv.w) * uv.w};
+    if (h) *reinterpret_cast<float4 *>(h + e) = make_float4(v[0], v[1], v[2], v[3]);
+    q8k_block_store(qa, col0 + row, b, v, lane);
+}
+
+__global__ void __launch_bounds__(256) swiglu_q80_kernel(const float *g, const float *u, size_t n, size_t total,
+                                                         float *h, Act qa, size_t col0, int quant) {
+    const size_t blk = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= total) return;
+    const size_t nb = n / 32, row = blk / nb, b = blk % nb;
+    const size_t e = row * n + b * 32;
+    float v[32];
+    for (int i = 0; i < 32; i++) v[i] = silu_f(g[e + i]) * u[e + i];
+    if (h)
+        for (int i = 0; i < 32; i++) h[e + i] = v[i];
+    if (quant) q8_0_block_store(qa, col0 + row, b, v);
+}
+
+// ------------------------------------------------------------------------------------------ Gated DeltaNet
+// One work-group per V head p (K head p % nk, gated_deltanet.rs:172); thread j owns column j of the head's
+// state S[k][v] (row-major, dk x dv) in registers, and the conv windows of channels q_j, k_j, v_j.
+// Per row (gated_deltanet.rs:261-375, deltanet.rs:19-86, conv.rs:11-36):
+//   conv step + SiLU of the head's q/k/v channels; l2norm(q), l2norm(k) (eps 1e-6, sequential sums);
+//   q *= 1/sqrt(dk); g = ssm_a * softplus(a + dt_bias); beta = sigmoid(b);
+//   S *= exp(g); kv = sum_k S[k][v] k[k]; delta = (v - kv) beta; S[k][v] += k[k] delta; o = sum_k S[k][v] q[k];
+//   y = (w * (o * inv_rms(o))) * silu(z)  (rmsnorm.rs:37-46).
+// Each column's sums run in its own thread in the reference's order. The state is written back only when asked
+// (write_state); the conv windows go to conv_dst (a second buffer, so work-groups sharing a K head never read a
+// window another one has already advanced): v channels by every head, q/k channels by head p == kh.
+__device__ __forceinline__ float conv_step(float win[3], const float c[4], float x) {
+    float acc = 0.0f;
+    acc += c[0] * win[0];
+    acc += c[1] * win[1];
+    acc += c[2] * win[2];
+    acc += c[3] * x;
+    win[0] = win[1];
+    win[1] = win[2];
+    win[2] = x;
+    return silu_f(acc);
+}
+
+template <int DK>
+__global__ void __launch_bounds__(256) dn_core_kernel(DnArgs a) {
+    __shared__ float qn[DK], kn[DK], ob[256], red[16];
+    const int p = blockIdx.x, j = threadIdx.x;
+    const int kh = p % a.nk, dv = a.dv;
+    const int kd = a.nk * DK, vd = a.nv * dv, cd = 2 * kd + vd;
+    const bool has_qk = j < DK, has_v = j < dv;
+    float wq[3] = {0, 0, 0}, wk[3] = {0, 0, 0}, wv[3] = {0, 0, 0};
+    float cq[4] = {0, 0, 0, 0}, ck[4] = {0, 0, 0, 0}, cv[4] = {0, 0, 0, 0};
+    const int chq = kh * DK + j, chk = kd + kh * DK + j, chv = 2 * kd + p * dv + j;
+    if (!a.raw) {
+        if (has_qk) {
+            for (int e = 0; e < 3; e++) {
+                wq[e] = a.conv_src[(size_t)chq * 3 + e];
+                wk[e] = a.conv_src[(size_t)chk * 3 + e];
+            }
+            for (int e = 0; e < 4; e++) {
+                cq[e] = a.conv_w[(size_t)chq * 4 + e];
+                ck[e] = a.conv_w[(size_t)chk * 4 + e];
+            }
+        }
+        if (has_v) {
+            for (int e = 0; e < 3; e++) wv[e] = a.conv_src[(size_t)chv * 3 + e];
+            for (int e = 0; e < 4; e++) cv[e] = a.conv_w[(size_t)chv * 4 + e];
+        }
+    }
+    float s[DK];
+    float *srec = a.rec + (size_t)p * DK * dv;
+#pragma unroll
+    for (int k = 0; k < DK; k++) s[k] = has_v ? srec[(size_t)k * dv + j] : 0.0f;
+    const float big_a = a.raw ? 0.0f : a.ssm_a[p], dtb = a.raw ? 0.0f : a.dt_bias[p];
+    const int tk = blockDim.x > 64 ? 64 : 1; // the k-norm chain runs in another wave when there is one
+
+    for (int i = 0; i < a.t; i++) {
+        float vval = 0.0f;
+        if (a.raw) {
+            if (has_qk) {
+                qn[j] = a.rq[(size_t)i * kd + kh * DK + j];
+                kn[j] = a.rk[(size_t)i * kd + kh * DK + j];
+            }
+            if (has_v) vval = a.rv[(size_t)i * vd + p * dv + j];
+        } else {
+            const float *mrow = a.mixed + (size_t)i * cd;
+            if (has_qk) {
+                qn[j] = conv_step(wq, cq, mrow[chq]);
+                kn[j] = conv_step(wk, ck, mrow[chk]);
+            }
+            if (has_v) vval = conv_step(wv, cv, mrow[chv]);
+        }
+        __syncthreads();
+        float g, beta;
+        if (a.raw) {
+            g = a.rg[(size_t)i * a.nv + p];
+            beta = a.rbeta[(size_t)i * a.nv + p];
+        } else {
+            if (j == 0 || j == tk) { // deltanet.rs:19-29 l2norm, eps 1e-6
+                const float *x = j == 0 ? qn : kn;
+                float ss = 0.0f;
+                for (int k = 0; k < DK; k++) ss += x[k] * x[k];
+                red[j == 0 ? 0 : 1] = 1.0f / sqrtf(ss + 1e-6f);
+            }
+            __syncthreads();
+            if (has_qk) {
+                const float qv = qn[j] * red[0];
+                qn[j] = qv * a.qscale;
+                kn[j] = kn[j] * red[1];
+            }
+            __syncthreads();
+            g = big_a * softplus_f(a.a[(size_t)i * a.nv + p] + dtb); // deltanet.rs:32-35 gate_g
+            beta = sigmoid_f(a.b[(size_t)i * a.nv + p]);
+        }
+        float ov = 0.0f;
+        if (has_v) { // deltanet.rs:43-86
+            const float decay = exp_f(g);
+#pragma unroll
+            for (int k = 0; k < DK; k++) s[k] *= decay;
+            float kv = 0.0f;
+#pragma unroll
+            for (int k = 0; k < DK; k++) kv += s[k] * kn[k];
+            const float delta = (vval - kv) * beta;
+#pragma unroll
+            for (int k = 0; k < DK; k++) s[k] += kn[k] * delta;
+#pragma unroll
+            for (int k = 0; k < DK; k++) ov += s[k] * qn[k];
+        }
+        if (a.out) {
+            if (a.raw) {
+                if (has_v) a.out[(size_t)i * vd + p * dv + j] = ov;
+            } else {
+                if (has_v) ob[j] = ov;
+                __syncthreads();
+                const int n8 = dv / 8 * 8;
+                if (j < 8) {
+                    float acc = 0.0f;
+                    for (int e = j; e < n8; e += 8) acc += ob[e] * ob[e];
+                    red[4 + j] = acc;
+                }
+                __syncthreads();
+                if (j == 0) {
+                    float ss = reduce8_f(red + 4);
+                    for (int e = n8; e < dv; e++) ss += ob[e] * ob[e];
+                    red[2] = 1.0f / sqrtf(ss / (float)dv + a.eps);
+                }
+                __syncthreads();
+                if (has_v) {
+                    const size_t o = (size_t)i * vd + p * dv + j;
+                    a.out[o] = (a.ssm_norm[j] * (ov * red[2])) * silu_f(a.z[o]);
+                }
+            }
+        }
+        __syncthreads(); // qn, kn, ob, red are rewritten by the next row
+    }
+    if (a.write_state && has_v) {
+#pragma unroll
+        for (int k = 0; k < DK; k++) srec[(size_t)k * dv + j] = s[k];
+    }
+    if (a.conv_dst && !a.raw) {
+        if (has_v)
+            for (int e = 0; e < 3; e++) a.conv_dst[(size_t)chv * 3 + e] = wv[e];
+        if (has_qk && p == kh)
+            for (int e = 0; e < 3; e++) {
+                a.conv_dst[(size_t)chq * 3 + e] = wq[e];
+                a.conv_dst[(size_t)chk * 3 + e] = wk[e];
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- attention
+// gqa_attention.rs:327-418 per row: q/k per-head RMSNorm (rmsnorm.rs) then RoPE on the first rope_dim dims
+// (rope.rs:31-45: pairs (i, i + rd/2)); K and V appended to the cache. One work-group per (head, row).
+__global__ void __launch_bounds__(256) attn_prep_kernel(AttnArgs a) {
+    __shared__ float xs[256], red[16];
+    const int hh = blockIdx.x, i = blockIdx.y, d = threadIdx.x, hd = a.hd;
+    const bool isq = hh < a.nh;
+    const float *src = isq ? a.qg + (size_t)i * 2 * a.nh * hd + (size_t)hh * 2 * hd
+                           : a.kk + (size_t)i * a.nkv * hd + (size_t)(hh - a.nh) * hd;
+    const float *w = isq ? a.q_norm : a.k_norm;
+    xs[d] = src[d];
+    __syncthreads();
+    const int n8 = hd / 8 * 8;
+    if (d < 8) {
+        float acc = 0.0f;
+        for (int e = d; e < n8; e += 8) acc += xs[e] * xs[e];
+        red[d] = acc;
+    }
+    __syncthreads();
+    if (d == 0) {
+        float ss = reduce8_f(red);
+        for (int e = n8; e < hd; e++) ss += xs[e] * xs[e];
+        red[8] = 1.0f / sqrtf(ss / (float)hd + a.eps);
+    }
+    __syncthreads();
+    const float y = (xs[d] * red[8]) * w[d];
+    __syncthreads();
+    xs[d] = y;
+    __syncthreads();
+    const int half = a.rd / 2;
+    const size_t pos = a.start_pos + i;
+    const float *cs = a.cos_tab + pos * half, *sn = a.sin_tab + pos * half;
+    float r = y;
+    if (d < half) {
+        r = xs[d] * cs[d] - xs[d + half] * sn[d];
+    } else if (d < a.rd) {
+        const int e = d - half;
+        r = xs[d] * cs[e] + xs[e] * sn[e];
+    }
+    if (isq) {
+        a.q[(size_t)i * a.nh * hd + (size_t)hh * hd + d] = r;
+    } else {
+        const int kvh = hh - a.nh;
+        const size_t crow = a.base + i;
+        a.kcache[crow * a.stride + (size_t)kvh * hd + d] = r;
+        a.vcache[crow * a.stride + (size_t)kvh * hd + d] = a.vv[(size_t)i * a.nkv * hd + (size_t)kvh * hd + d];
+    }
+}
+
+// Scores (sequential dot over head_dim, times scaling), softmax (softmax.rs:22-49: max, exp, 8-lane sum, divide),
+// weighted V sum (sequential over positions), times sigmoid(gate).
+__global__ void __launch_bounds__(256) attn_core_kernel(AttnArgs a) {
+    extern __shared__ float sm[]; // hd + (base + t) + 32
+    const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x, hd = a.hd;
+    const int kvh = h / (a.nh / a.nkv);
+    const size_t len = a.base + i + 1;
+    float *qs = sm, *sc = sm + hd, *red = sc + a.base + a.t;
+    for (int d = tid; d < hd; d += 256) qs[d] = a.q[(size_t)i * a.nh * hd + (size_t)h * hd + d];
+    __syncthreads();
+    float mx = -INFINITY;
+    for (size_t tt = tid; tt < len; tt += 256) {
+        const float *kr = a.kcache + tt * a.stride + (size_t)kvh * hd;
+        float acc = 0.0f;
+        for (int d = 0; d < hd; d++) acc += qs[d] * kr[d];
+        const float v = acc * a.scaling;
+        sc[tt] = v;
+        mx = v > mx ? v : mx;
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(mx, off);
+        mx = o > mx ? o : mx;
+    }
+    if ((tid & 63) == 0) red[16 + (tid >> 6)] = mx;
+    __syncthreads();
+    mx = red[16];
+    for (int wv = 1; wv < 4; wv++) mx = red[16 + wv] > mx ? red[16 + wv] : mx;
+    for (size_t tt = tid; tt < len; tt += 256) sc[tt] = exp_f(sc[tt] - mx);
+    __syncthreads();
+    const size_t n8 = len / 8 * 8;
+    if (tid < 8) {
+        float acc = 0.0f;
+        for (size_t e = tid; e < n8; e += 8) acc += sc[e];
+        red[tid] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float s = reduce8_f(red);
+        for (size_t e = n8; e < len; e++) s += sc[e];
+        red[8] = s;
+    }
+    __syncthreads();
+    const float ssum = red[8];
+    for (size_t tt = tid; tt < len; tt += 256) sc[tt] = sc[tt] / ssum;
+    __syncthreads();
+    for (int d = tid; d < hd; d += 256) {
+        float acc = 0.0f;
+        for (size_t tt = 0; tt < len; tt++) acc += sc[tt] * a.vcache[tt * a.stride + (size_t)kvh * hd + d];
+        const float gate = a.qg[(size_t)i * 2 * a.nh * hd + (size_t)h * 2 * hd + hd + d];
+        a.out[(size_t)i * a.nh * hd + (size_t)h * hd + d] = acc * sigmoid_f(gate);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------- argmax
+constexpr size_t ARGMAX_CHUNK = 2048;
+
+__device__ __forceinline__ void amax_merge(float &bv, uint32_t &bi, float ov, uint32_t oi) {
+    if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
+__device__ __forceinline__ void amax_block(float &bv, uint32_t &bi, float *sv, uint32_t *si) {
+    for (int off = 32; off >= 1; off >>= 1) amax_merge(bv, bi, __shfl_xor(bv, off), __shfl_xor(bi, off));
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) amax_merge(bv, bi, sv[w], si[w]);
+    }
+}
+
+__global__ void __launch_bounds__(256) argmax_partial_kernel(const float *x, size_t n, size_t stride, float *pv,
+                                                             uint32_t *pi, int nchunk) {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    const int c = blockIdx.x, r = blockIdx.y;
+    const float *xr = x + (size_t)r * stride;
+    const size_t lo = (size_t)c * ARGMAX_CHUNK, hi = lo + ARGMAX_CHUNK < n ? lo + ARGMAX_CHUNK : n;
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (size_t e = lo + threadIdx.x; e < hi; e += 256) amax_merge(bv, bi, xr[e], (uint32_t)e);
+    amax_block(bv, bi, sv, si);
+    if (threadIdx.x == 0) {
+        pv[(size_t)r * nchunk + c] = bv;
+        pi[(size_t)r * nchunk + c] = bi;
+    }
+}
+
+__global__ void __launch_bounds__(64) argmax_final_kernel(const float *pv, const uint32_t *pi, int nchunk,
+                                                          uint32_t *ids) {
+    __shared__ float sv[1];
+    __shared__ uint32_t si[1];
+    const int r = blockIdx.x;
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (int c = threadIdx.x; c < nchunk; c += 64) amax_merge(bv, bi, pv[(size_t)r * nchunk + c], pi[(size_t)r * nchunk + c]);
+    amax_block(bv, bi, sv, si);
+    if (threadIdx.x == 0) ids[r] = bi == 0xFFFFFFFFu ? 0u : bi;
+}
+
+// -------------------------------------------------------------------------------------------- acceptance
+// spec.rs:355-366: walk the drafts while the verify argmax agrees; emit the verify argmax at each step, plus the
+// bonus token when every draft was accepted.
+__global__ void accept_kernel(const uint32_t *ids, const uint32_t *drafts, int k, uint32_t *emitted, uint32_t *info) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    int m = 0, ne = 0;
+    while (m < k) {
+        const uint32_t a = ids[m];
+        emitted[ne++] = a;
+        if (a != drafts[m]) break;
+        m++;
+    }
+    if (m == k) emitted[ne++] = ids[k];
+    info[0] = (uint32_t)m;
+    info[1] = (uint32_t)ne;
+    info[2] = (uint32_t)(m + 1);
+}
+
+__global__ void make_batch_kernel(uint32_t x_p, const uint32_t *drafts, int k, uint32_t *batch) {
+    const int i = threadIdx.x;
+    if (i == 0) batch[0] = x_p;
+    else if (i <= k) batch[i] = drafts[i - 1];
+}
+
+int launched(const char *what) {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail(AQ_EHIP, std::string(what) + " launch: " + hipGetErrorString(e));
+}
+
+} // namespace
+
+int launch_embed(const Weight &w, const uint32_t *ids, size_t t, float *out, size_t out_stride, hipStream_t stream) {
+    AQ_REQUIRE(w.type == AQ_TYPE_Q4_K, "embed: token_embd must be Q4_K in this build");
+    if (t == 0) return 0;
+    hipLaunchKernelGGL(embed_q4k_kernel, dim3((unsigned)w.nb, (unsigned)t), dim3(256), 0, stream, w, ids, out, out_stride);
+    return launched("embed");
+}
+
+int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t, float *y_f32,
+                   size_t y_stride, const QuantOut &q, hipStream_t stream) {
+    AQ_REQUIRE(n > 0 && n <= 16384, "rmsnorm: row length must be 1..16384");
+    if (t == 0) return 0;
+    Act act{};
+    if (q.act) {
+        act = *q.act;
+        AQ_REQUIRE(q.col0 + t <= act.ncols && q.elem_off + n <= act.n, "rmsnorm: quantised output out of range");
+        AQ_REQUIRE(q.kind != QK_Q8K || (n % 256 == 0 && q.elem_off % 256 == 0), "rmsnorm: Q8_K needs 256-blocks");
+        AQ_REQUIRE(q.kind != QK_Q80 || (n % 32 == 0 && q.elem_off % 32 == 0), "rmsnorm: Q8_0 needs 32-blocks");
+    } else {
+        AQ_REQUIRE(q.kind == QK_NONE && !q.f32, "rmsnorm: quantised output without a buffer");
+    }
+    const size_t shmem = (n + 16) * sizeof(float);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)t), dim3(256), shmem, stream, x, x_stride, w, eps, (int)n, y_f32,
+                       y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0);
+    return launched("rmsnorm");
+}
+
+int launch_swiglu(const float *g, const float *u, size_t n, size_t t, float *h_f32, const QuantOut &q,
+                  hipStream_t stream) {
+    if (t == 0) return 0;
+    Act act{};
+    if (q.act) {
+        act = *q.act;
+        AQ_REQUIRE(q.col0 + t <= act.ncols && q.elem_off == 0 && n == act.n, "swiglu: quantised output shape");
+    }
+    if (q.kind == QK_Q8K) {
+        AQ_REQUIRE(n % 256 == 0, "swiglu: Q8_K needs n % 256 == 0");
+        const size_t total = t * (n / 256);
+        hipLaunchKernelGGL(swiglu_q8k_kernel, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, g, u, n, total,
+                           h_f32, act, q.col0);
+    } else {
+        AQ_REQUIRE(n % 32 == 0, "swiglu: n % 32 != 0");
+        AQ_REQUIRE(q.kind == QK_Q80 || h_f32, "swiglu: no output");
+        const size_t total = t * (n / 32);
+        hipLaunchKernelGGL(swiglu_q80_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, g, u, n,
+                           total, h_f32, act, q.col0, q.kind == QK_Q80 ? 1 : 0);
+    }
+    return launched("swiglu");
+}
+
+int launch_dn_core(const DnArgs &a, hipStream_t stream) {
+    AQ_REQUIRE(a.t >= 1 && a.nk >= 1 && a.nv >= 1 && a.nv % a.nk == 0, "deltanet: head counts");
+    AQ_REQUIRE(a.dv >= 1 && a.dv <= 256, "deltanet: head_dim_v must be 1..256");
+    AQ_REQUIRE(a.rec, "deltanet: no state");
+    if (!a.raw) {
+        AQ_REQUIRE(a.kernel == 4, "deltanet: conv kernel must be 4 in this build");
+        AQ_REQUIRE(a.mixed && a.a && a.b && a.conv_src && a.conv_w && a.ssm_a && a.dt_bias, "deltanet: inputs");
+        AQ_REQUIRE(!a.out || (a.z && a.ssm_norm), "deltanet: output needs z and ssm_norm");
+    } else {
+        AQ_REQUIRE(a.rq && a.rk && a.rv && a.rg && a.rbeta, "deltanet: raw inputs");
+    }
+    const int threads = ((a.dk > a.dv ? a.dk : a.dv) + 63) / 64 * 64;
+    switch (a.dk) {
+#define AQ_DK(D)                                                                                              \
+    case D: hipLaunchKernelGGL(dn_core_kernel<D>, dim3((unsigned)a.nv), dim3(threads), 0, stream, a); break;
+        AQ_DK(8) AQ_DK(16) AQ_DK(32) AQ_DK(64) AQ_DK(128)
+#undef AQ_DK
+    default: return fail(AQ_EUNSUP, "deltanet: head_dim_k must be 8, 16, 32, 64 or 128 in this build");
+    }
+    return launched("deltanet");
+}
+
+int launch_attention(const AttnArgs &a, hipStream_t stream) {
+    AQ_REQUIRE(a.t >= 1 && a.nh >= 1 && a.nkv >= 1 && a.nh % a.nkv == 0, "attention: head counts");
+    AQ_REQUIRE(a.hd >= 8 && a.hd <= 256 && a.hd % 8 == 0, "attention: head_dim must be a multiple of 8, <= 256");
+    AQ_REQUIRE(a.rd >= 2 && a.rd <= a.hd && a.rd % 2 == 0, "attention: rope_dim");
+    hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)(a.nh + a.nkv), (unsigned)a.t), dim3(a.hd), 0, stream, a);
+    int rc = launched("attention prologue");
+    if (rc) return rc;
+    const size_t shmem = (a.hd + a.base + a.t + 32) * sizeof(float);
+    AQ_REQUIRE(shmem <= 160 * 1024, "attention: context too long for one work-group's LDS");
+    hipLaunchKernelGGL(attn_core_kernel, dim3((unsigned)a.nh, (unsigned)a.t), dim3(256), shmem, stream, a);
+    return launched("attention");
+}
+
+size_t argmax_scratch_bytes(size_t n, size_t t) {
+    const size_t nchunk = (n + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
+    return t * nchunk * 8 + 256;
+}
+
+int launch_argmax(const float *x, size_t n, size_t stride, size_t t, uint32_t *ids, void *scratch, hipStream_t stream) {
+    AQ_REQUIRE(n >= 1 && t >= 1, "argmax: empty");
+    const int nchunk = (int)((n + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK);
+    float *pv = (float *)scratch;
+    uint32_t *pi = (uint32_t *)((uint8_t *)scratch + ((t * nchunk * 4 + 255) & ~(size_t)255));
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3((unsigned)nchunk, (unsigned)t), dim3(256), 0, stream, x, n, stride,
+                       pv, pi, nchunk);
+    int rc = launched("argmax");
+    if (rc) return rc;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)t), dim3(64), 0, stream, pv, pi, nchunk, ids);
+    return launched("argmax final");
+}
+
+int launch_accept(const uint32_t *argmax_ids, const uint32_t *drafts, int k, uint32_t *emitted, uint32_t *info,
+                  hipStream_t stream) {
+    hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(64), 0, stream, argmax_ids, drafts, k, emitted, info);
+    return launched("accept");
+}
+
+int launch_make_batch(uint32_t x_p, const uint32_t *drafts, int k, uint32_t *batch, hipStream_t stream) {
+    AQ_REQUIRE(k >= 0 && k < 64, "make_batch: k");
+    hipLaunchKernelGGL(make_batch_kernel, dim3(1), dim3(64), 0, stream, x_p, drafts, k, batch);
+    return launched("make_batch");
+}
+
+} // namespace aq

@@ -1,0 +1,127 @@
+// quant_dev.h — device building blocks shared by the quantise, norm, activation and model kernels: the Q8_K and
+// Q8_0 activation quantisers as device functions, and the reference's scalar activations.
+#pragma once
+
+#include "aq_common.h"
+
+namespace aq {
+
+__device__ __forceinline__ float f16_to_f32(uint16_t bits) {
+    _Float16 f;
+    __builtin_memcpy(&f, &bits, 2);
+    return (float)f;
+}
+
+// f32 exp rounded once from a double evaluation: the correctly rounded value except in vanishingly rare
+// hard cases. The reference calls the platform libm `expf` (act.rs:7-40, softmax.rs:22-49, deltanet.rs:43-86),
+// which is not always correctly rounded; the two agree on all but about 1 in 13,000 inputs (an exhaustive
+// sweep of |x| <= 88), and a disagreement is one ulp.
+__device__ __forceinline__ float exp_f(float x) { return (float)exp((double)x); }
+
+// act.rs:7-9 `silu`, 12-14 `sigmoid`, 33-40 `softplus` (threshold 20), same operation order.
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + exp_f(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + exp_f(-x)); }
+__device__ __forceinline__ float softplus_f(float x) {
+    if (x > 20.0f) return x;
+    const float e = exp_f(x);
+    return (float)log1p((double)e);
+}
+
+// rmsnorm.rs reduce8 / reduce4 pairings.
+__device__ __forceinline__ float reduce8_f(const float *l) {
+    return ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
+}
+
+// One Q8_K block (256 values) quantised by one wave: lane i holds x[4i..4i+3]. Q8KRow::quantize_scalar_into
+// (q8k.rs:76-114): max = the first element with the largest |x|, iscale = -127/max, q = min(127,
+// round_ties_even(iscale*x)), d = 1/iscale (0 for an all-zero block), bsums per 16, q8s per 32. Writes the
+// block at (qs_blk, *d_out, bs_blk[16], q8s_blk[8]) in the kernels' lane-slot code order.
+__device__ __forceinline__ void q8k_block_wave(const float x[4], int lane, int8_t *qs_blk, float *d_out,
+                                               int16_t *bs_blk, int16_t *q8s_blk) {
+    float amax = 0.0f, maxv = 0.0f;
+    int idx = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float a = fabsf(x[j]);
+        if (a > amax) {
+            amax = a;
+            idx = lane * 4 + j;
+            maxv = x[j];
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float oa = __shfl_xor(amax, off);
+        const int oi = __shfl_xor(idx, off);
+        const float om = __shfl_xor(maxv, off);
+        if (oa > amax || (oa == amax && oi < idx)) {
+            amax = oa;
+            idx = oi;
+            maxv = om;
+        }
+    }
+    int q[4] = {0, 0, 0, 0};
+    if (amax != 0.0f) {
+        const float iscale = -127.0f / maxv;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int qi = (int)__builtin_rintf(iscale * x[j]);
+            q[j] = qi < 127 ? qi : 127;
+        }
+        if (lane == 0) *d_out = 1.0f / iscale;
+    } else if (lane == 0) {
+        *d_out = 0.0f;
+    }
+    const int s = lane >> 3, l = lane & 7;
+    const uint32_t packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) | ((uint32_t)(uint8_t)q[2] << 16) |
+                            ((uint32_t)(uint8_t)q[3] << 24);
+    *reinterpret_cast<uint32_t *>(qs_blk + lane_slot(l) * 32 + s * 4) = packed;
+    int sum = q[0] + q[1] + q[2] + q[3];
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    if ((lane & 3) == 0) bs_blk[lane >> 2] = (int16_t)sum;
+    const int s32 = sum + __shfl_xor(sum, 4);
+    if ((lane & 7) == 0) q8s_blk[lane >> 3] = (int16_t)s32;
+}
+
+// Store block `blk` of column `col` of a Q8_K activation.
+__device__ __forceinline__ void q8k_block_store(const Act &a, size_t col, size_t blk, const float x[4], int lane) {
+    const size_t m = col * a.nb + blk;
+    q8k_block_wave(x, lane, a.qs + col * a.n + blk * 256, a.d + m, a.bs + m * 16, a.q8s + m * 8);
+}
+
+// One Q8_0 block (32 values) by one lane. Q8Row::quantize_scalar_into (q8.rs:81-121): d = amax/127 -> f16
+// (round to nearest even), id = d != 0 ? 1/d : 0 from the unrounded d, q = round_half_away(x*id) saturated.
+__device__ __forceinline__ void q8_0_block_store(const Act &a, size_t col, size_t blk, const float *v) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) {
+        const float av = fabsf(v[i]);
+        if (av > amax) amax = av;
+    }
+    const float dd = amax / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    const _Float16 hd = (_Float16)dd;
+    uint16_t hbits;
+    __builtin_memcpy(&hbits, &hd, 2);
+    int sum = 0;
+    uint32_t words[8];
+    for (int i = 0; i < 8; i++) {
+        uint32_t w = 0;
+        for (int j = 0; j < 4; j++) {
+            const float r = roundf(v[4 * i + j] * id);
+            const int qi = r > 127.0f ? 127 : (r < -128.0f ? -128 : (int)r);
+            sum += qi;
+            w |= (uint32_t)(uint8_t)qi << (8 * j);
+        }
+        words[i] = w;
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(a.q0 + col * a.n + blk * 32);
+    dst[0] = make_uint4(words[0], words[1], words[2], words[3]);
+    dst[1] = make_uint4(words[4], words[5], words[6], words[7]);
+    const size_t m = col * a.nb32 + blk;
+    a.d0[m] = (float)hd;
+    a.h0[m] = hbits;
+    a.s0[m] = sum;
+}
+
+} // namespace aq

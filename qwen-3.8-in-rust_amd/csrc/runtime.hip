@@ -25,7 +25,6 @@ static int alloc_weight(Weight &w, int type, size_t rows, size_t cols, int devic
     AQ_REQUIRE(rows > 0 && cols > 0, "weight: empty shape");
     AQ_REQUIRE(cols % be == 0, "weight: cols " + std::to_string(cols) + " is not a multiple of the block size " +
                                    std::to_string(be));
-    if (type == AQ_TYPE_F32) AQ_REQUIRE(cols % 32 == 0, "weight: F32 cols must be a multiple of 32");
     w.type = type;
     w.rows = rows;
     w.cols = cols;
@@ -80,7 +79,6 @@ void free_weight(Weight &w) {
 
 int alloc_act(Act &a, size_t n, size_t ncols, int device) {
     AQ_REQUIRE(n > 0 && ncols > 0, "act: empty shape");
-    AQ_REQUIRE(n % 32 == 0, "act: n must be a multiple of 32");
     a.n = n;
     a.ncols = ncols;
     a.nb = n / 256;
@@ -284,8 +282,10 @@ int aq_act_quantize(aq_act *a, int weight_type, size_t ncols) {
         AQ_REQUIRE(a->a.n % 256 == 0, "aq_act_quantize: Q8_K needs n % 256 == 0 (matvec.rs:73-77)");
         return launch_q8k_quantize(a->a, ncols, a->a.f32, a->a.n, a->ctx->stream);
     }
-    if (weight_type == AQ_TYPE_Q8_0 || weight_type == AQ_TYPE_Q4_0)
+    if (weight_type == AQ_TYPE_Q8_0 || weight_type == AQ_TYPE_Q4_0) {
+        AQ_REQUIRE(a->a.n % 32 == 0, "aq_act_quantize: Q8_0 needs n % 32 == 0");
         return launch_q8_0_quantize(a->a, ncols, a->a.f32, a->a.n, a->ctx->stream);
+    }
     if (weight_type == AQ_TYPE_F32) return 0;
     return fail(AQ_EUNSUP, "aq_act_quantize: unsupported weight type");
 }
@@ -318,7 +318,7 @@ int aq_act_get_q8k(const aq_act *a, void *ggml_out, size_t ncols) {
 
 int aq_act_get_q8_0(const aq_act *a, void *ggml_out, size_t ncols) {
     AQ_REQUIRE(a && ggml_out, "aq_act_get_q8_0: null argument");
-    AQ_REQUIRE(ncols <= a->a.ncols, "aq_act_get_q8_0: shape");
+    AQ_REQUIRE(ncols <= a->a.ncols && a->a.n % 32 == 0, "aq_act_get_q8_0: shape");
     const Act &x = a->a;
     AQ_HIP(hipSetDevice(a->ctx->device));
     std::vector<int8_t> q(ncols * x.n);

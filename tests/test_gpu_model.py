@@ -1,0 +1,318 @@
+"""The device model path against the CPU oracle and the reference's layer fixtures.
+
+* layer pieces (tests/layers.rs:109-271 fixtures, F32 weights): the device layer equals the oracle's and meets the
+  fixture budget;
+* the tiny hybrid (3 DeltaNet + 1 attention layer + MTP, Q4_K/Q6_K): prefill and 32 greedy tokens give the oracle's
+  ids, logits within 1e-3 of the oracle's (relative to the largest |logit|);
+* greedy --spec 3 emits exactly the plain ids (tests/spec_identity.rs:34-119) and matches the oracle round by round
+  (drafts, accepted count);
+* forced drafts: after every round the device state equals the plain path's state at the same position bit for
+  bit, and the oracle's within tolerance (the reference's rollback contract, spec.rs:396-415);
+* the isolated recurrence with rollback (the DeltaNet config: 32 V / 16 K heads x 128): outputs within 1e-4 of the
+  oracle, the committed state bit-identical to a plain sequential run of the kept rows.
+"""
+import ctypes as C
+import json
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "qwen-3.8-in-rust_amd"))
+import aqueduct as aq  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "layers")
+EPS = float(np.finfo(np.float32).eps)
+SEED = 20260905
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    return aq.Context(0)
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+# ------------------------------------------------------------------------------------------ layer fixtures
+with open(os.path.join(DIR, "manifest.json")) as f:
+    M = json.load(f)
+CFG = M["config"]
+K = M["budget_k"]
+
+
+def farr(field):
+    return np.load(os.path.join(DIR, field["file"]), allow_pickle=False).astype(np.float32)
+
+
+def fcase(name):
+    return next(c for c in M["cases"] if c["case"] == name)
+
+
+def fx_config(mod):
+    c = mod.AqModelConfig()
+    c.n_layer, c.hidden, c.ffn, c.vocab = 1, CFG["hidden_size"], CFG["intermediate_size"], CFG["vocab_size"]
+    c.n_head, c.n_head_kv, c.head_dim = CFG["num_attention_heads"], CFG["num_key_value_heads"], CFG["head_dim"]
+    c.rope_dim = int(CFG["head_dim"] * CFG["rope_parameters"]["partial_rotary_factor"])
+    c.rope_theta, c.rms_eps = CFG["rope_parameters"]["rope_theta"], CFG["rms_norm_eps"]
+    c.full_attention_interval = 4
+    c.dn_n_k_heads, c.dn_n_v_heads = CFG["linear_num_key_heads"], CFG["linear_num_value_heads"]
+    c.dn_head_dim_k, c.dn_head_dim_v = CFG["linear_key_head_dim"], CFG["linear_value_head_dim"]
+    c.dn_conv_kernel, c.has_mtp = CFG["linear_conv_kernel_dim"], 0
+    return c
+
+
+def fx_tensors(c):
+    out = []
+    for name, f in c["weights"].items():
+        a = farr(f)
+        rows, cols = (a.shape[0], a.shape[1]) if a.ndim == 2 else (1, a.size)
+        out.append(("blk.0." + name, aq.F32, rows, cols, a))
+    return out
+
+
+class Pair:
+    """The same layer on the device and in the oracle, with their own carried state."""
+
+    def __init__(self, ctx, c, kind):
+        self.ctx, self.kind = ctx, kind
+        self.tensors = fx_tensors(c)
+        self.gcfg, self.ocfg = fx_config(aq), fx_config(O)
+        self.otable, self.okeep = O.tensor_table(self.tensors)
+        cfg = self.gcfg
+        cd = 2 * cfg.dn_n_k_heads * cfg.dn_head_dim_k + cfg.dn_n_v_heads * cfg.dn_head_dim_v
+        self.cap = 16
+        stride = cfg.n_head_kv * cfg.head_dim
+        z = lambda n: np.zeros(n, np.float32)  # noqa: E731
+        self.g = dict(conv=z(cd * 3), rec=z(cfg.dn_n_v_heads * cfg.dn_head_dim_k * cfg.dn_head_dim_v),
+                      kc=z(self.cap * stride), vc=z(self.cap * stride), len=0)
+        self.o = dict(conv=z(cd * 3), rec=z(cfg.dn_n_v_heads * cfg.dn_head_dim_k * cfg.dn_head_dim_v),
+                      kc=z(self.cap * stride), vc=z(self.cap * stride), len=C.c_uint32(0))
+
+    def run(self, x, start):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.gcfg.hidden)
+        g = self.g
+        yg, g["len"] = aq.layer_run(self.ctx, self.gcfg, self.tensors, self.kind, x, start, g["conv"], g["rec"],
+                                    g["kc"], g["vc"], g["len"], self.cap)
+        o = self.o
+        yo = np.zeros_like(x)
+        rc = O.lib().or_layer_run(C.byref(self.ocfg), self.otable, len(self.tensors), self.kind, O.ptr(x), x.shape[0],
+                                  start, O.ptr(o["conv"]), O.ptr(o["rec"]), O.ptr(o["kc"]), O.ptr(o["vc"]),
+                                  C.byref(o["len"]), self.cap, O.ptr(yo))
+        assert rc == 0
+        return yg, yo
+
+
+def budget_check(label, got, want, width):
+    bud = K * math.sqrt(width) * EPS * float(np.abs(want).max())
+    d = float(np.abs(got.astype(np.float64) - want.astype(np.float64)).max())
+    assert d <= bud, f"{label}: {d:e} > {bud:e}"
+
+
+def oracle_check(label, got, want, tol=1e-5):
+    r = rel(got, want)
+    print(f"{label}: device vs oracle rel {r:.3e}, bit-identical {np.array_equal(got, want)}", flush=True)
+    assert r <= tol, f"{label}: device vs oracle {r:e}"
+
+
+@pytest.mark.parametrize("name,kind", [("deltanet_layer", 0), ("attention_layer", 1), ("mlp_layer", 2),
+                                       ("decoder_linear_attention", 3), ("decoder_full_attention", 4)])
+def test_layer_pieces_match_oracle_and_fixtures(ctx, name, kind):
+    print(f"case {name} kind {kind}", flush=True)
+    c = fcase(name)
+    p = Pair(ctx, c, kind)
+    hidden, inter = CFG["hidden_size"], CFG["intermediate_size"]
+    width = max(hidden, inter, 64)
+    x = farr(c["prefill"]["x"])
+    if kind >= 3:  # token by token, as tests/layers.rs:253-257
+        ys = [p.run(x[i], i) for i in range(c["t"])]
+        yg = np.concatenate([a for a, _ in ys])
+        yo = np.concatenate([b for _, b in ys])
+    else:
+        yg, yo = p.run(x, 0)
+    oracle_check(f"{name} prefill", yg, yo)
+    budget_check(f"{name} prefill vs fixture", yg, farr(c["prefill"]["y"]).reshape(yg.shape), width)
+    if kind in (0, 3):
+        oracle_check(f"{name} rec", p.g["rec"], p.o["rec"])
+        oracle_check(f"{name} conv", p.g["conv"], p.o["conv"])
+    if kind in (1, 4):
+        assert p.g["len"] == p.o["len"].value
+        n = p.g["len"] * fx_config(aq).n_head_kv * CFG["head_dim"]
+        oracle_check(f"{name} K cache", p.g["kc"][:n], p.o["kc"][:n])
+        oracle_check(f"{name} V cache", p.g["vc"][:n], p.o["vc"][:n])
+    if "step" in c:
+        pos = c["step"].get("position", c["t"])
+        yg1, yo1 = p.run(farr(c["step"]["x"]), pos)
+        oracle_check(f"{name} step", yg1, yo1)
+        budget_check(f"{name} step vs fixture", yg1, farr(c["step"]["y"]).reshape(yg1.shape), width)
+
+
+# ---------------------------------------------------------------------------------------------- tiny model
+@pytest.fixture(scope="module")
+def tiny(ctx):
+    cfg = aq.tiny_config()
+    plan = aq.model_plan(cfg, aq.MIX_TINY, SEED)
+    tensors = aq.plan_tensors(plan)
+    gm = aq.Model(ctx, cfg, tensors=tensors)
+    ocfg = O.AqModelConfig()
+    for name, _ in O.AqModelConfig._fields_:
+        setattr(ocfg, name, getattr(cfg, name))
+    om = O.Model(ocfg, tensors, threads=8)
+    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, 16).astype(np.uint32)
+    return dict(cfg=cfg, plan=plan, tensors=tensors, gm=gm, om=om, prompt=prompt)
+
+
+def plain_run(state, prompt, n, want_logits=False):
+    tok, lg = state.prefill(prompt, want_logits=True)
+    ids, lgs = [tok], [lg]
+    for _ in range(n - 1):
+        tok, lg = state.forward_token(ids[-1], want_logits=True)
+        ids.append(tok)
+        lgs.append(lg)
+    return ids, lgs
+
+
+def test_tiny_synth_on_device_equals_host_upload(ctx, tiny):
+    print("case tiny synth vs upload", flush=True)
+    gs = aq.Model(ctx, tiny["cfg"], mix=aq.MIX_TINY, seed=SEED)
+    a = aq.State(tiny["gm"], 0, 128)
+    b = aq.State(gs, 0, 128)
+    ta, la = a.prefill(tiny["prompt"], want_logits=True)
+    tb, lb = b.prefill(tiny["prompt"], want_logits=True)
+    assert ta == tb and np.array_equal(la, lb)
+    assert tiny["gm"].bytes() == gs.bytes()
+
+
+def test_tiny_plain_greedy_matches_oracle(ctx, tiny):
+    print("case tiny plain greedy", flush=True)
+    gs = aq.State(tiny["gm"], 0, 128)
+    os_ = O.State(tiny["om"], 0, 128)
+    gids, glg = plain_run(gs, tiny["prompt"], 32)
+    oids, olg = plain_run(os_, tiny["prompt"], 32)
+    worst = max(rel(g, o) for g, o in zip(glg, olg))
+    exact = sum(np.array_equal(g, o) for g, o in zip(glg, olg))
+    print(f"tiny plain: logits max rel {worst:.3e}, {exact}/32 steps bit-identical; ids {gids[:8]}...", flush=True)
+    assert gids == oids
+    assert worst <= 1e-3
+    se, so = gs.export(), os_.export()
+    assert se.size == so.size
+    assert rel(se, so) <= 1e-3
+
+
+def spec_run(state, prompt, n):
+    x = state.spec_prefill(prompt)
+    out, rounds = [x], []
+    while len(out) < n:
+        drafts = state.drafts()
+        m, em = state.spec_round(out[-1])
+        rounds.append((drafts, m, em))
+        out += em
+    return out[:n], rounds
+
+
+def test_tiny_spec3_identity_and_oracle_rounds(ctx, tiny):
+    print("case tiny spec 3", flush=True)
+    gp = aq.State(tiny["gm"], 0, 160)
+    plain, _ = plain_run(gp, tiny["prompt"], 32)
+    gs = aq.State(tiny["gm"], 3, 160)
+    os_ = O.State(tiny["om"], 3, 160)
+    gids, grounds = spec_run(gs, tiny["prompt"], 32)
+    oids, orounds = spec_run(os_, tiny["prompt"], 32)
+    st = gs.stats()
+    print(f"tiny spec: rounds {st['rounds']} accepted {st['accepted']} hist {st['hist'][:4]}", flush=True)
+    assert gids == plain, "greedy --spec 3 must emit the plain ids"
+    assert gids == oids
+    assert [r[:2] for r in grounds] == [r[:2] for r in orounds], "drafts and acceptance differ from the oracle"
+
+
+def test_tiny_forced_drafts_state_equals_plain(ctx, tiny):
+    print("case tiny forced drafts", flush=True)
+    gp = aq.State(tiny["gm"], 0, 160)
+    plain, _ = plain_run(gp, tiny["prompt"], 40)
+    gs = aq.State(tiny["gm"], 3, 160)
+    os_ = O.State(tiny["om"], 3, 160)
+    x = gs.spec_prefill(tiny["prompt"])
+    assert x == os_.spec_prefill(tiny["prompt"]) == plain[0]
+    rng = np.random.default_rng(7)
+    out = [x]
+    for r in range(8):
+        j = len(out)  # plain[j:j+3] are the correct drafts for this round
+        n_ok = int(rng.integers(0, 4))
+        d = [plain[j + i] if i < n_ok else (plain[j + i] + 1) % tiny["cfg"].vocab for i in range(3)]
+        gs.set_drafts(d)
+        os_.set_drafts(d)
+        m, em = gs.spec_round(out[-1])
+        mo, emo = os_.spec_round(out[-1])
+        assert (m, em) == (mo, emo)
+        assert m >= n_ok and em == plain[j:j + len(em)]
+        out += em
+        # the device state equals a plain run to the same position, bit for bit, and the oracle's within 1e-3
+        ref = aq.State(tiny["gm"], 0, 160)
+        ref.prefill(tiny["prompt"])
+        for tok in out[:-1]:
+            ref.forward_token(tok)
+        a, b = gs.export(), ref.export()
+        assert gs.pos == ref.pos == len(tiny["prompt"]) + len(out) - 1
+        assert np.array_equal(a[: b.size], b), f"round {r}: spec state differs from the plain state"
+        assert rel(a, os_.export()) <= 1e-3
+
+
+# ----------------------------------------------------------------------------------- isolated recurrence
+def test_deltanet_recurrence_rollback(ctx):
+    nv, nk, dk, dv, t = 32, 16, 128, 128, 4
+    rng = np.random.default_rng(5)
+    L = O.lib()
+    for trial, keep in enumerate([1, 2, 3, 4, 2]):
+        print(f"case deltanet trial {trial} keep {keep}", flush=True)
+        s0 = (rng.standard_normal((nv, dk, dv)) * 0.1).astype(np.float32)
+        q = rng.standard_normal((t, nk * dk)).astype(np.float32)
+        k = rng.standard_normal((t, nk * dk)).astype(np.float32)
+        for arr in (q, k):
+            for i in range(t):
+                for h in range(nk):
+                    seg = np.ascontiguousarray(arr[i, h * dk:(h + 1) * dk])
+                    L.or_l2norm(O.ptr(seg), dk, C.c_float(1e-6))
+                    arr[i, h * dk:(h + 1) * dk] = seg
+        v = rng.standard_normal((t, nv * dv)).astype(np.float32)
+        beta = np.array([[L.or_sigmoid(float(z)) for z in row] for row in rng.standard_normal((t, nv))], np.float32)
+        g = np.array([[-L.or_softplus(float(z)) for z in row] for row in rng.standard_normal((t, nv))], np.float32)
+        # oracle: sequential steps; the state after `keep` rows
+        so = s0.copy()
+        out_o = np.zeros((t, nv * dv), np.float32)
+        s_keep = None
+        for i in range(t):
+            for p in range(nv):
+                kh = p % nk
+                sp = np.ascontiguousarray(so[p])
+                o = np.zeros(dv, np.float32)
+                L.or_deltanet_step(O.ptr(np.ascontiguousarray(q[i, kh * dk:(kh + 1) * dk])),
+                                   O.ptr(np.ascontiguousarray(k[i, kh * dk:(kh + 1) * dk])),
+                                   O.ptr(np.ascontiguousarray(v[i, p * dv:(p + 1) * dv])), float(g[i, p]),
+                                   float(beta[i, p]), O.ptr(sp), O.ptr(o), dk, dv)
+                so[p] = sp
+                out_o[i, p * dv:(p + 1) * dv] = o
+            if i + 1 == keep:
+                s_keep = so.copy()
+        st = aq.DeviceBuffer(ctx, s0.nbytes)
+        st.upload(s0)
+        out_g = aq.deltanet_verify_commit(ctx, nk, nv, dk, dv, keep, q, k, v, g, beta, st)
+        s_dev = st.download(np.float32, s0.size).reshape(s0.shape)
+        # plain sequential reference on the device: the kept rows only, committed
+        st2 = aq.DeviceBuffer(ctx, s0.nbytes)
+        st2.upload(s0)
+        aq.deltanet_verify_commit(ctx, nk, nv, dk, dv, keep, q[:keep], k[:keep], v[:keep], g[:keep], beta[:keep], st2)
+        s_seq = st2.download(np.float32, s0.size).reshape(s0.shape)
+        r_out, r_state = rel(out_g, out_o), rel(s_dev, s_keep)
+        print(f"deltanet keep {keep}: out rel {r_out:.2e}, state rel {r_state:.2e}, "
+              f"exact {np.array_equal(out_g, out_o)}/{np.array_equal(s_dev, s_keep)}", flush=True)
+        assert np.array_equal(s_dev, s_seq), "rolled-back state differs from the sequential state"
+        assert r_out <= 1e-4 and r_state <= 1e-4
