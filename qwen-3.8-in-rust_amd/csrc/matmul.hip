@@ -358,8 +358,80 @@ int launch_kq(const Weight &w, const Act &x, size_t ncols, float *y, const float
     }
 }
 
+// dot.rs:180-200 for F32 weights (ssm_alpha / ssm_beta: few rows, long columns): one work-group per row;
+// thread b computes block b's 32-element partial left to right for every column, then one thread per column
+// adds the partials in block order (acc += part), and `acc + 0.0f` when the row has no short tail.
+template <int NC>
+__global__ void __launch_bounds__(256) f32_matmul_kernel(Q8Args a) {
+    extern __shared__ float prods[]; // nb32 x NC
+    const int row = blockIdx.x, nb = a.nb32;
+    const size_t n = a.n;
+    const float *w = reinterpret_cast<const float *>(a.qa) + (size_t)row * n;
+    for (int b = threadIdx.x; b < nb; b += 256) {
+        const size_t e0 = (size_t)b * 32;
+        const int ne = n - e0 < 32 ? (int)(n - e0) : 32;
+        float wv[32];
+        if (ne == 32 && n % 4 == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 t = *reinterpret_cast<const float4 *>(w + e0 + 4 * i);
+                wv[4 * i] = t.x;
+                wv[4 * i + 1] = t.y;
+                wv[4 * i + 2] = t.z;
+                wv[4 * i + 3] = t.w;
+            }
+        } else {
+            for (int i = 0; i < 32; i++) wv[i] = i < ne ? w[e0 + i] : 0.0f;
+        }
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const float *x = a.xf + (size_t)c * n + e0;
+            float part = 0.0f;
+            if (ne == 32 && n % 4 == 0) {
+                float xv[32];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float4 t = *reinterpret_cast<const float4 *>(x + 4 * i);
+                    xv[4 * i] = t.x;
+                    xv[4 * i + 1] = t.y;
+                    xv[4 * i + 2] = t.z;
+                    xv[4 * i + 3] = t.w;
+                }
+#pragma unroll
+                for (int i = 0; i < 32; i++) part += wv[i] * xv[i];
+            } else {
+                for (int i = 0; i < ne; i++) part += wv[i] * x[i];
+            }
+            prods[b * NC + c] = part;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < NC) {
+        const int c = threadIdx.x;
+        float acc = 0.0f;
+        int b = 0;
+        for (; b + 8 <= nb; b += 8) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = prods[(b + i) * NC + c];
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc += v[i];
+        }
+        for (; b < nb; b++) acc += prods[b * NC + c];
+        if (n % 32 == 0) acc = acc + 0.0f;
+        const size_t o = (size_t)c * a.rows + row;
+        a.y[o] = a.resid ? a.resid[o] + acc : acc;
+    }
+}
+
 template <int NC>
 int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
+    if (args.type == AQ_TYPE_F32) {
+        const size_t lds = (size_t)args.nb32 * NC * sizeof(float);
+        if (lds > 64 * 1024) return fail(AQ_EUNSUP, "f32 matmul: row too long for the LDS chain");
+        hipLaunchKernelGGL((f32_matmul_kernel<NC>), dim3((unsigned)args.rows), dim3(256), lds, stream, args);
+        return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "f32_matmul launch");
+    }
     // rows per block chosen so the LDS products fit in 64 KiB
     const size_t per_row = (size_t)args.nb32 * NC * sizeof(float);
     int rpb = 16;

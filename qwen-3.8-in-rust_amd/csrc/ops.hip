@@ -47,18 +47,15 @@ __global__ void __launch_bounds__(256) embed_q4k_kernel(Weight w, const uint32_t
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const float *x, size_t x_stride, const float *w, float eps, int n,
                                                       float *y, size_t y_stride, Act qa, int kind, size_t col0,
                                                       size_t eoff, int act_f32) {
-    extern __shared__ float xs[]; // n + 16
+    extern __shared__ float xs[]; // 2n + 16: the row, 16 partials, the weights
     float *red = xs + n;
     const int row = blockIdx.x, tid = threadIdx.x;
-    const float *xr = x + (size_t)row * x_stride;
-    for (int i = tid; i < n; i += 256) xs[i] = xr[i];
+    float *wsh = red + 16; // the norm weights, staged like the row
+    copy_rows_in(xs, x + (size_t)row * x_stride, n, tid, 256);
+    copy_rows_in(wsh, w, n, tid, 256);
     __syncthreads();
     const int n8 = n / 8 * 8;
-    if (tid < 8) {
-        float acc = 0.0f;
-        for (int i = tid; i < n8; i += 8) acc += xs[i] * xs[i];
-        red[tid] = acc;
-    }
+    if (tid < 8) red[tid] = seq_sum<true>(xs, tid, n8, 8, 0.0f);
     __syncthreads();
     if (tid == 0) {
         float ss = reduce8_f(red);
@@ -69,7 +66,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float *x, size_t x_s
     __syncthreads();
     const float inv = red[8];
     for (int i = tid; i < n; i += 256) {
-        const float v = (xs[i] * inv) * w[i];
+        const float v = (xs[i] * inv) * wsh[i];
         xs[i] = v;
         if (y) y[(size_t)row * y_stride + i] = v;
         if (act_f32) qa.f32[(col0 + row) * qa.n + eoff + i] = v;
@@ -108,8 +105,13 @@ __global__ void __launch_bounds__(256) swiglu_q80_kernel(const float *g, const f
     if (blk >= total) return;
     const size_t nb = n / 32, row = blk / nb, b = blk % nb;
     const size_t e = row * n + b * 32;
-    float v[32];
-    for (int i = 0; i < 32; i++) v[i] = silu_f(g[e + i]) * u[e + i];
+    float v[32], gv[32], uv[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        gv[i] = g[e + i];
+        uv[i] = u[e + i];
+    }
+    for (int i = 0; i < 32; i++) v[i] = silu_f(gv[i]) * uv[i];
     if (h)
         for (int i = 0; i < 32; i++) h[e + i] = v[i];
     if (quant) q8_0_block_store(qa, col0 + row, b, v);
@@ -194,9 +196,7 @@ __global__ void __launch_bounds__(256) dn_core_kernel(DnArgs a) {
             beta = a.rbeta[(size_t)i * a.nv + p];
         } else {
             if (j == 0 || j == tk) { // deltanet.rs:19-29 l2norm, eps 1e-6
-                const float *x = j == 0 ? qn : kn;
-                float ss = 0.0f;
-                for (int k = 0; k < DK; k++) ss += x[k] * x[k];
+                const float ss = seq_sum<true>(j == 0 ? qn : kn, 0, DK, 1, 0.0f);
                 red[j == 0 ? 0 : 1] = 1.0f / sqrtf(ss + 1e-6f);
             }
             __syncthreads();
@@ -230,11 +230,7 @@ __global__ void __launch_bounds__(256) dn_core_kernel(DnArgs a) {
                 if (has_v) ob[j] = ov;
                 __syncthreads();
                 const int n8 = dv / 8 * 8;
-                if (j < 8) {
-                    float acc = 0.0f;
-                    for (int e = j; e < n8; e += 8) acc += ob[e] * ob[e];
-                    red[4 + j] = acc;
-                }
+                if (j < 8) red[4 + j] = seq_sum<true>(ob, j, n8, 8, 0.0f);
                 __syncthreads();
                 if (j == 0) {
                     float ss = reduce8_f(red + 4);
@@ -278,11 +274,7 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnArgs a) {
     xs[d] = src[d];
     __syncthreads();
     const int n8 = hd / 8 * 8;
-    if (d < 8) {
-        float acc = 0.0f;
-        for (int e = d; e < n8; e += 8) acc += xs[e] * xs[e];
-        red[d] = acc;
-    }
+    if (d < 8) red[d] = seq_sum<true>(xs, d, n8, 8, 0.0f);
     __syncthreads();
     if (d == 0) {
         float ss = reduce8_f(red);
@@ -328,7 +320,31 @@ __global__ void __launch_bounds__(256) attn_core_kernel(AttnArgs a) {
     for (size_t tt = tid; tt < len; tt += 256) {
         const float *kr = a.kcache + tt * a.stride + (size_t)kvh * hd;
         float acc = 0.0f;
-        for (int d = 0; d < hd; d++) acc += qs[d] * kr[d];
+        int d = 0;
+        for (; d + 32 <= hd; d += 32) { // 8 loads in flight; the sum stays sequential in d
+            float4 kv4[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) kv4[u] = *reinterpret_cast<const float4 *>(kr + d + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                acc += qs[d + 4 * u] * kv4[u].x;
+                acc += qs[d + 4 * u + 1] * kv4[u].y;
+                acc += qs[d + 4 * u + 2] * kv4[u].z;
+                acc += qs[d + 4 * u + 3] * kv4[u].w;
+            }
+        }
+        for (; d < hd; d += 8) { // hd % 8 == 0
+            const float4 k0 = *reinterpret_cast<const float4 *>(kr + d);
+            const float4 k1 = *reinterpret_cast<const float4 *>(kr + d + 4);
+            acc += qs[d] * k0.x;
+            acc += qs[d + 1] * k0.y;
+            acc += qs[d + 2] * k0.z;
+            acc += qs[d + 3] * k0.w;
+            acc += qs[d + 4] * k1.x;
+            acc += qs[d + 5] * k1.y;
+            acc += qs[d + 6] * k1.z;
+            acc += qs[d + 7] * k1.w;
+        }
         const float v = acc * a.scaling;
         sc[tt] = v;
         mx = v > mx ? v : mx;
@@ -344,11 +360,7 @@ __global__ void __launch_bounds__(256) attn_core_kernel(AttnArgs a) {
     for (size_t tt = tid; tt < len; tt += 256) sc[tt] = exp_f(sc[tt] - mx);
     __syncthreads();
     const size_t n8 = len / 8 * 8;
-    if (tid < 8) {
-        float acc = 0.0f;
-        for (size_t e = tid; e < n8; e += 8) acc += sc[e];
-        red[tid] = acc;
-    }
+    if (tid < 8) red[tid] = seq_sum<false>(sc, tid, (int)n8, 8, 0.0f);
     __syncthreads();
     if (tid == 0) {
         float s = reduce8_f(red);
@@ -360,8 +372,17 @@ __global__ void __launch_bounds__(256) attn_core_kernel(AttnArgs a) {
     for (size_t tt = tid; tt < len; tt += 256) sc[tt] = sc[tt] / ssum;
     __syncthreads();
     for (int d = tid; d < hd; d += 256) {
+        const float *vc = a.vcache + (size_t)kvh * hd + d;
         float acc = 0.0f;
-        for (size_t tt = 0; tt < len; tt++) acc += sc[tt] * a.vcache[tt * a.stride + (size_t)kvh * hd + d];
+        size_t tt = 0;
+        for (; tt + 8 <= len; tt += 8) { // 8 loads in flight; the sum stays sequential in tt
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = vc[(tt + u) * a.stride];
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc += sc[tt + u] * v[u];
+        }
+        for (; tt < len; tt++) acc += sc[tt] * vc[tt * a.stride];
         const float gate = a.qg[(size_t)i * 2 * a.nh * hd + (size_t)h * 2 * hd + hd + d];
         a.out[(size_t)i * a.nh * hd + (size_t)h * hd + d] = acc * sigmoid_f(gate);
     }
@@ -399,7 +420,14 @@ __global__ void __launch_bounds__(256) argmax_partial_kernel(const float *x, siz
     const size_t lo = (size_t)c * ARGMAX_CHUNK, hi = lo + ARGMAX_CHUNK < n ? lo + ARGMAX_CHUNK : n;
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
-    for (size_t e = lo + threadIdx.x; e < hi; e += 256) amax_merge(bv, bi, xr[e], (uint32_t)e);
+    for (size_t e = lo + threadIdx.x; e < hi; e += 8 * 256) { // 8 loads in flight per thread
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = e + u * 256 < hi ? xr[e + u * 256] : -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (e + u * 256 < hi) amax_merge(bv, bi, v[u], (uint32_t)(e + u * 256));
+    }
     amax_block(bv, bi, sv, si);
     if (threadIdx.x == 0) {
         pv[(size_t)r * nchunk + c] = bv;
@@ -470,7 +498,7 @@ int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, s
     } else {
         AQ_REQUIRE(q.kind == QK_NONE && !q.f32, "rmsnorm: quantised output without a buffer");
     }
-    const size_t shmem = (n + 16) * sizeof(float);
+    const size_t shmem = (2 * n + 16) * sizeof(float);
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)t), dim3(256), shmem, stream, x, x_stride, w, eps, (int)n, y_f32,
                        y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0);
     return launched("rmsnorm");

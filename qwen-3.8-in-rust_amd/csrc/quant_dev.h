@@ -27,6 +27,52 @@ __device__ __forceinline__ float softplus_f(float x) {
     return (float)log1p((double)e);
 }
 
+// Sequential sum acc + x[start] + x[start+stride] + ... over [start, end), in that order, reading 16 values
+// ahead so the chain waits on adds, not on each load. SQUARE: the terms are x*x (each product rounded).
+template <bool SQUARE>
+__device__ __forceinline__ float seq_sum(const float *x, int start, int end, int stride, float acc) {
+    int i = start;
+    for (; i + 15 * stride < end; i += 16 * stride) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = x[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < 16; u++) acc += SQUARE ? v[u] * v[u] : v[u];
+    }
+    for (; i < end; i += stride) acc += SQUARE ? x[i] * x[i] : x[i];
+    return acc;
+}
+
+// Work-group copy of n floats from global memory into LDS, every load of a thread issued before the first wait
+// (a plain strided loop waits for each load before issuing the next): batches of 8 predicated loads, float4
+// when n and both pointers allow.
+__device__ __forceinline__ void copy_rows_in(float *dst, const float *src, int n, int tid, int nthreads) {
+    if ((n & 3) == 0 && ((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 15) == 0) {
+        const int n4 = n >> 2;
+        const float4 *s4 = reinterpret_cast<const float4 *>(src);
+        float4 *d4 = reinterpret_cast<float4 *>(dst);
+        for (int i = tid; i < n4; i += 8 * nthreads) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (i + u * nthreads < n4) v[u] = s4[i + u * nthreads];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (i + u * nthreads < n4) d4[i + u * nthreads] = v[u];
+        }
+        return;
+    }
+    for (int i = tid; i < n; i += 8 * nthreads) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i + u * nthreads < n) v[u] = src[i + u * nthreads];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i + u * nthreads < n) dst[i + u * nthreads] = v[u];
+    }
+}
+
 // rmsnorm.rs reduce8 / reduce4 pairings.
 __device__ __forceinline__ float reduce8_f(const float *l) {
     return ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
