@@ -240,6 +240,11 @@ int aq_deltanet_verify_commit(aq_ctx *ctx, uint32_t nk, uint32_t nv, uint32_t dk
                               const float *q, const float *k, const float *v, const float *g, const float *beta,
                               float *state_dev, float *out);
 
+/* The device's scalar activations, elementwise on host arrays (fn: 0 exp, 1 log1p, 2 silu, 3 sigmoid, 4 softplus;
+ * act.rs:7-40). No counterpart in the reference: the parity tests use it to show the device evaluates exp and
+ * log1p exactly as the CPU oracle does. */
+int aq_eval_math(aq_ctx *ctx, int fn, const float *x, float *y, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,14 +12,20 @@ SOURCES = ["oracle_kernels.c", "oracle_model.c"]
 LIB = os.path.join(HERE, "liboracle.so")
 
 
+LIB_LIBM = os.path.join(HERE, "liboracle_libm.so")
+MATH_DIR = os.path.join(os.path.dirname(HERE), "qwen-3.8-in-rust_amd", "csrc")  # aq_math.h, shared with the device
+
+
 def build(verbose: bool = False) -> str:
-    cmd = ["gcc", "-O3", "-std=gnu11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off", "-fno-fast-math",
-           "-mavx2", "-Wall", "-Wno-unknown-pragmas", "-o", LIB + ".tmp"]
-    cmd += [os.path.join(HERE, s) for s in SOURCES] + ["-lm"]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
-    os.replace(LIB + ".tmp", LIB)
+    """liboracle.so (exp / log1p from aq_math.h) and liboracle_libm.so (the platform libm's expf / log1pf)."""
+    for out, libm in ((LIB, 0), (LIB_LIBM, 1)):
+        cmd = ["gcc", "-O3", "-std=gnu11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off", "-fno-fast-math",
+               "-mavx2", "-Wall", "-Wno-unknown-pragmas", f"-DOR_LIBM={libm}", "-I", MATH_DIR, "-o", out + ".tmp"]
+        cmd += [os.path.join(HERE, s) for s in SOURCES] + ["-lm"]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        os.replace(out + ".tmp", out)
     return LIB
 
 

@@ -49,6 +49,9 @@ void or_matmul(int type, const uint8_t *w, size_t rows, size_t cols, const float
 void or_rmsnorm(const float *x, const float *w, float eps, float *y, size_t n);
 void or_rmsnorm_gated(const float *x, const float *gate, const float *w, float eps, float *y, size_t n);
 void or_softmax(const float *x, float *y, size_t n);
+float or_expf(float x);
+float or_log1pf(float x);
+void or_eval_math(int fn, const float *x, float *y, size_t n);
 float or_silu(float x);
 float or_sigmoid(float x);
 float or_softplus(float x);

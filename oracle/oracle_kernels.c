@@ -10,6 +10,8 @@
 #include "oracle.h"
 #include "oracle_internal.h"
 
+#include "aq_math.h"
+
 /* ===================================================================================== f16 (half 2.7.1) */
 
 /* quant.rs:33-36 `f16_to_f32`: exact widening, subnormals and inf/NaN included. */
@@ -602,10 +604,36 @@ void or_rmsnorm(const float *x, const float *w, float eps, float *y, size_t n) {
     for (size_t i = 0; i < n; i++) y[i] = (x[i] * inv) * w[i];
 }
 
+/* The reference's f32 exp / log1p are the platform libm's expf / log1pf. The oracle evaluates them with aq_math.h,
+ * the routine the device uses too (pinned against libm by tests/test_math.py), so device and oracle agree bit for
+ * bit at any depth; building with -DOR_LIBM=1 restores the platform libm calls (liboracle_libm.so) to measure how
+ * far a libm's last-ulp choices move the outputs. */
+#if OR_LIBM
+#define OR_EXPF expf
+#define OR_LOG1PF log1pf
+#else
+#define OR_EXPF aq_expf
+#define OR_LOG1PF aq_log1pf
+#endif
+
 /* act.rs:7-9 `silu`, 12-14 `sigmoid`, 33-40 `softplus` */
-float or_silu(float x) { return x / (1.0f + expf(-x)); }
-float or_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
-float or_softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+float or_silu(float x) { return x / (1.0f + OR_EXPF(-x)); }
+float or_sigmoid(float x) { return 1.0f / (1.0f + OR_EXPF(-x)); }
+float or_softplus(float x) { return x > 20.0f ? x : OR_LOG1PF(OR_EXPF(x)); }
+float or_expf(float x) { return OR_EXPF(x); }
+float or_log1pf(float x) { return OR_LOG1PF(x); }
+/* fn: 0 exp, 1 log1p, 2 silu, 3 sigmoid, 4 softplus, elementwise */
+void or_eval_math(int fn, const float *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        switch (fn) {
+        case 0: y[i] = OR_EXPF(x[i]); break;
+        case 1: y[i] = OR_LOG1PF(x[i]); break;
+        case 2: y[i] = or_silu(x[i]); break;
+        case 3: y[i] = or_sigmoid(x[i]); break;
+        default: y[i] = or_softplus(x[i]); break;
+        }
+    }
+}
 
 /* rmsnorm.rs:37-46 `rmsnorm_gated` */
 void or_rmsnorm_gated(const float *x, const float *gate, const float *w, float eps, float *y, size_t n) {
@@ -623,7 +651,7 @@ void or_softmax(const float *x, float *y, size_t n) {
     float m = -INFINITY;
     for (size_t i = 0; i < n; i++)
         if (x[i] > m) m = x[i];
-    for (size_t i = 0; i < n; i++) y[i] = expf(x[i] - m);
+    for (size_t i = 0; i < n; i++) y[i] = OR_EXPF(x[i] - m);
     size_t n8 = n / 8 * 8;
     float l[8] = {0};
     for (size_t i = 0; i < n8; i += 8)
@@ -693,7 +721,7 @@ float or_gate_g(float a, float dt_bias, float big_a) { return big_a * or_softplu
 /* deltanet.rs:43-86 `deltanet_step` */
 void or_deltanet_step(const float *q, const float *k, const float *v, float g, float beta, float *s, float *out,
                       size_t dk, size_t dv) {
-    float decay = expf(g);
+    float decay = OR_EXPF(g);
     for (size_t i = 0; i < dk * dv; i++) s[i] *= decay;
     for (size_t vv = 0; vv < dv; vv++) out[vv] = 0.0f;
     for (size_t kk = 0; kk < dk; kk++) {

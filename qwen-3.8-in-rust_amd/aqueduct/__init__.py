@@ -96,6 +96,7 @@ def lib():
         "aq_state_pos": (i, [P, P]),
         "aq_state_export": (i, [P, P, sz, C.POINTER(sz)]),
         "aq_layer_run": (i, [P, P, P, sz, i, P, sz, C.c_uint32, P, P, P, P, P, C.c_uint32, P]),
+        "aq_eval_math": (i, [P, i, P, P, sz]),
         "aq_deltanet_verify_commit": (i, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, sz, sz, P, P, P, P, P,
                                           P, P]),
     }
@@ -473,3 +474,11 @@ def deltanet_verify_commit(ctx: Context, nk, nv, dk, dv, keep, q, k, v, g, beta,
     check(lib().aq_deltanet_verify_commit(ctx.h, nk, nv, dk, dv, t, keep, ptr(q), ptr(k), ptr(v), ptr(g), ptr(beta),
                                           state.p, ptr(out)))
     return out
+
+
+def eval_math(ctx: Context, fn, x):
+    """The device's activations elementwise (aq_eval_math): fn 0 exp, 1 log1p, 2 silu, 3 sigmoid, 4 softplus."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.zeros_like(x)
+    check(lib().aq_eval_math(ctx.h, fn, ptr(x), ptr(y), x.size))
+    return y

@@ -1317,6 +1317,20 @@ int aq_layer_run(aq_ctx *ctx, const aq_model_config *cfg, const aq_tensor *tenso
     return rc;
 }
 
+int aq_eval_math(aq_ctx *ctx, int fn, const float *x, float *y, size_t n) {
+    AQ_REQUIRE(ctx && x && y, "aq_eval_math: null argument");
+    AQ_HIP(hipSetDevice(ctx->device));
+    float *d = nullptr;
+    if (hipMalloc(&d, 2 * n * 4 + 256) != hipSuccess) return fail(AQ_ENOMEM, "aq_eval_math: buffer");
+    int rc = hipMemcpyAsync(d, x, n * 4, hipMemcpyHostToDevice, ctx->stream) == hipSuccess ? 0 : fail(AQ_EHIP, "upload");
+    if (!rc) rc = launch_eval_math(fn, d, d + n, n, ctx->stream);
+    if (!rc && hipMemcpyAsync(y, d + n, n * 4, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess)
+        rc = fail(AQ_EHIP, "aq_eval_math: download");
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess && !rc) rc = fail(AQ_EHIP, "aq_eval_math: sync");
+    (void)hipFree(d);
+    return rc;
+}
+
 int aq_deltanet_verify_commit(aq_ctx *ctx, uint32_t nk, uint32_t nv, uint32_t dk, uint32_t dv, size_t t, size_t keep,
                               const float *q, const float *k, const float *v, const float *g, const float *beta,
                               float *state_dev, float *out) {

@@ -83,6 +83,9 @@ int launch_argmax(const float *x, size_t n, size_t stride, size_t t, uint32_t *i
 int launch_accept(const uint32_t *argmax_ids, const uint32_t *drafts, int k, uint32_t *emitted, uint32_t *info,
                   hipStream_t stream);
 
+// y = f(x) elementwise with the device's activation functions (fn: 0 exp, 1 log1p, 2 silu, 3 sigmoid, 4 softplus).
+int launch_eval_math(int fn, const float *x, float *y, size_t n, hipStream_t stream);
+
 // batch = [x_p, drafts[0..k)]
 int launch_make_batch(uint32_t x_p, const uint32_t *drafts, int k, uint32_t *batch, hipStream_t stream);
 

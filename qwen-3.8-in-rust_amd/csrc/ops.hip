@@ -471,6 +471,22 @@ __global__ void make_batch_kernel(uint32_t x_p, const uint32_t *drafts, int k, u
     else if (i <= k) batch[i] = drafts[i - 1];
 }
 
+// fn: 0 exp, 1 log1p, 2 silu, 3 sigmoid, 4 softplus (the device forms every kernel above uses)
+__global__ void eval_math_kernel(int fn, const float *x, float *y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    float r;
+    switch (fn) {
+    case 0: r = exp_f(v); break;
+    case 1: r = aq_log1pf(v); break;
+    case 2: r = silu_f(v); break;
+    case 3: r = sigmoid_f(v); break;
+    default: r = softplus_f(v); break;
+    }
+    y[i] = r;
+}
+
 int launched(const char *what) {
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail(AQ_EHIP, std::string(what) + " launch: " + hipGetErrorString(e));
@@ -584,6 +600,13 @@ int launch_accept(const uint32_t *argmax_ids, const uint32_t *drafts, int k, uin
                   hipStream_t stream) {
     hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(64), 0, stream, argmax_ids, drafts, k, emitted, info);
     return launched("accept");
+}
+
+int launch_eval_math(int fn, const float *x, float *y, size_t n, hipStream_t stream) {
+    AQ_REQUIRE(fn >= 0 && fn <= 4, "eval_math: fn must be 0..4");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(eval_math_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, fn, x, y, n);
+    return launched("eval_math");
 }
 
 int launch_make_batch(uint32_t x_p, const uint32_t *drafts, int k, uint32_t *batch, hipStream_t stream) {

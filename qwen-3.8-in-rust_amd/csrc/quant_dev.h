@@ -3,6 +3,7 @@
 #pragma once
 
 #include "aq_common.h"
+#include "aq_math.h"
 
 namespace aq {
 
@@ -12,20 +13,12 @@ __device__ __forceinline__ float f16_to_f32(uint16_t bits) {
     return (float)f;
 }
 
-// f32 exp rounded once from a double evaluation: the correctly rounded value except in vanishingly rare
-// hard cases. The reference calls the platform libm `expf` (act.rs:7-40, softmax.rs:22-49, deltanet.rs:43-86),
-// which is not always correctly rounded; the two agree on all but about 1 in 13,000 inputs (an exhaustive
-// sweep of |x| <= 88), and a disagreement is one ulp.
-__device__ __forceinline__ float exp_f(float x) { return (float)exp((double)x); }
-
-// act.rs:7-9 `silu`, 12-14 `sigmoid`, 33-40 `softplus` (threshold 20), same operation order.
+// act.rs:7-9 `silu`, 12-14 `sigmoid`, 33-40 `softplus` (threshold 20), same operation order; exp and log1p from
+// aq_math.h (the same bits as the CPU oracle's).
+__device__ __forceinline__ float exp_f(float x) { return aq_expf(x); }
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + exp_f(-x)); }
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + exp_f(-x)); }
-__device__ __forceinline__ float softplus_f(float x) {
-    if (x > 20.0f) return x;
-    const float e = exp_f(x);
-    return (float)log1p((double)e);
-}
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : aq_log1pf(exp_f(x)); }
 
 // Sequential sum acc + x[start] + x[start+stride] + ... over [start, end), in that order, reading 16 values
 // ahead so the chain waits on adds, not on each load. SQUARE: the terms are x*x (each product rounded).

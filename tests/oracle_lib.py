@@ -43,13 +43,33 @@ def tensor_table(tensors):
 
 
 _lib = None
+_lib_libm = None
+
+
+def lib_libm():
+    """The oracle built with the platform libm's expf / log1pf (or_eval_math and the model entry points)."""
+    global _lib_libm
+    if _lib_libm is None:
+        lib()
+        L = C.CDLL(os.path.join(ROOT, "oracle", "liboracle_libm.so"))
+        L.or_eval_math.restype = None
+        L.or_eval_math.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_size_t]
+        _lib_libm = L
+    return _lib_libm
+
+
+def eval_math(fn, x, libm=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.zeros_like(x)
+    (lib_libm() if libm else lib()).or_eval_math(fn, x.ctypes.data, y.ctypes.data, x.size)
+    return y
 
 
 def lib():
     global _lib
     if _lib is not None:
         return _lib
-    if not os.path.exists(LIB_PATH):
+    if not (os.path.exists(LIB_PATH) and os.path.exists(os.path.join(ROOT, "oracle", "liboracle_libm.so"))):
         import importlib.util
         spec = importlib.util.spec_from_file_location("build_oracle", os.path.join(ROOT, "oracle", "build_oracle.py"))
         mod = importlib.util.module_from_spec(spec)
@@ -75,6 +95,7 @@ def lib():
         "or_rmsnorm_gated": (None, [P, P, P, C.c_float, P, sz]),
         "or_softmax": (None, [P, P, sz]),
         "or_silu": (C.c_float, [C.c_float]),
+        "or_eval_math": (None, [C.c_int, P, P, sz]),
         "or_sigmoid": (C.c_float, [C.c_float]),
         "or_softplus": (C.c_float, [C.c_float]),
         "or_swiglu": (None, [P, P, P, sz]),
