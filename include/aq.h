@@ -103,6 +103,7 @@ int aq_dev_alloc(aq_ctx *ctx, size_t nbytes, void **dev_out);
 int aq_dev_free(aq_ctx *ctx, void *dev);
 int aq_memcpy_htod(aq_ctx *ctx, void *dev, const void *host, size_t nbytes);
 int aq_memcpy_dtoh(aq_ctx *ctx, void *host, const void *dev, size_t nbytes);
+int aq_memcpy_dtod(aq_ctx *ctx, void *dst, const void *src, size_t nbytes);
 
 /* --------------------------------------------------------------------------------------- operator level */
 

@@ -64,6 +64,7 @@ def lib():
         "aq_dev_free": (i, [P, P]),
         "aq_memcpy_htod": (i, [P, P, P, sz]),
         "aq_memcpy_dtoh": (i, [P, P, P, sz]),
+        "aq_memcpy_dtod": (i, [P, P, P, sz]),
         "aq_weight_upload": (i, [P, i, sz, sz, P, C.POINTER(P)]),
         "aq_weight_free": (i, [P]),
         "aq_weight_download": (i, [P, P]),
@@ -157,6 +158,9 @@ class DeviceBuffer:
         arr = np.ascontiguousarray(arr)
         assert arr.nbytes <= self.nbytes
         check(lib().aq_memcpy_htod(self.ctx.h, self.p, ptr(arr), arr.nbytes))
+
+    def copy_from(self, other, nbytes):
+        check(lib().aq_memcpy_dtod(self.ctx.h, self.p, other.p, nbytes))
 
     def download(self, dtype, count):
         out = np.zeros(count, dtype)

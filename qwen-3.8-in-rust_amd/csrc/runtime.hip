@@ -194,6 +194,14 @@ int aq_memcpy_htod(aq_ctx *ctx, void *dev, const void *host, size_t nbytes) {
     return 0;
 }
 
+int aq_memcpy_dtod(aq_ctx *ctx, void *dst, const void *src, size_t nbytes) {
+    AQ_REQUIRE(ctx && dst && src, "aq_memcpy_dtod: null argument");
+    AQ_HIP(hipSetDevice(ctx->device));
+    AQ_HIP(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, ctx->stream));
+    AQ_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
 int aq_memcpy_dtoh(aq_ctx *ctx, void *host, const void *dev, size_t nbytes) {
     AQ_REQUIRE(ctx && dev && host, "aq_memcpy_dtoh: null argument");
     AQ_HIP(hipMemcpyAsync(host, dev, nbytes, hipMemcpyDeviceToHost, ctx->stream));
