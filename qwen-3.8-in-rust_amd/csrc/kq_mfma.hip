@@ -14,7 +14,10 @@
 //  * Thread t = 16g + 4j + r of a wave owns weight row 4g + r (16 rows per wave) and the two reference lanes j and
 //    j+4: one instruction set with blocks (g, j) computes lane j, a second one lane j+4. Per-row work (scale
 //    decode, the min lanes) is shared by the row's 4 threads instead of 8, and every min lane j (0..3) is a thread.
-//  * The integer scale of each sub-block multiplies the MFMA partial with a full-rate 24-bit integer mad.
+//  * Q4_K / Q5_K: the 6-bit sub-block scale is split into 3-bit (2-bit) digits folded into the int8 weight operand
+//    (sb_products_split), so the MFMA accumulator sums the scaled sub-block dots; Q6_K (int8 scales) multiplies
+//    each MFMA partial by its scale with a full-rate 24-bit integer mad.
+//  * Results go to VGPRs (built with -amdgpu-mfma-vgpr-form): no accumulator-register copies.
 //  * Activations are staged in LDS per chunk of super-blocks, double-buffered (chunk k+1 is fetched into registers
 //    while chunk k is computed); weights stream from HBM as 16-byte loads, prefetched PF super-blocks ahead.
 //  * Matrices with few rows split K across KS waves of the work-group: wave w takes super-blocks w, w+KS, ...;
@@ -49,6 +52,13 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 __device__ __forceinline__ v4i mfma(uint32_t a, uint32_t b) {
     return __builtin_amdgcn_mfma_i32_4x4x4i8((int)a, (int)b, (v4i){0, 0, 0, 0}, 0, 0, 0);
 }
+__device__ __forceinline__ v4i mfma_acc(uint32_t a, uint32_t b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_4x4x4i8((int)a, (int)b, c, 0, 0, 0);
+}
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x2 as_u16x2(uint32_t w) { return __builtin_bit_cast(u16x2, w); }
+__device__ __forceinline__ uint32_t as_u32(u16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
 __device__ __forceinline__ int ubyte(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xFF); }
@@ -74,6 +84,218 @@ __device__ __forceinline__ void load_w(WRegs<TYPE> &w, const MfArgs &a, size_t w
     } else if constexpr (TYPE == AQ_TYPE_Q6_K) {
         w.qb = *reinterpret_cast<const uint4 *>(a.qb + wsb * 64 + j * 16);
         w.d6 = *reinterpret_cast<const uint16_t *>(a.dm + wsb * 2);
+    }
+}
+
+// The products of one super-block for one thread: pr0/pr1 = (dx*dw)*float(lane sum) of lanes j and j+4, pm the
+// Q4_K/Q5_K min product of min lane j, for every column. xq: the super-block's codes, 256 bytes per column (lane-slot
+// order); xd: its f32 scales per column; xm: its activation-sum pairs [pair][ncp]. kdot.rs:37-140 per lane.
+template <int TYPE, int NC>
+__device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t *xq, const float *xd,
+                                            const uint32_t *xm, int ncp, int j, int r, float *pr0, float *pr1,
+                                            float *pm) {
+    constexpr int NCG = (NC + 3) / 4;
+    constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
+    uint32_t code0[8], code1[8]; // 4 unsigned codes per sub-block, lanes j and j+4
+    int scl0[8], scl1[8];        // integer scale per sub-block, lanes j and j+4
+    int mn0 = 0, mn1 = 0;        // Q4_K/Q5_K mins of sub-blocks 2j, 2j+1 (min lane j)
+    int os00 = 0, os01 = 0, os10 = 0, os11 = 0; // Q6_K -32 fold scales: groups 2l, 2l+1 of l = j, j+4
+    float dw, dminw = 0.0f;
+    if constexpr (Q6) {
+        const uint32_t ql0[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w};
+        const uint32_t ql1[4] = {wv.qa1.x, wv.qa1.y, wv.qa1.z, wv.qa1.w};
+        const uint32_t qh0[2] = {wv.qb.x, wv.qb.y}, qh1[2] = {wv.qb.z, wv.qb.w};
+        const uint32_t sw[4] = {wv.sc.x, wv.sc.y, wv.sc.z, wv.sc.w};
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const int s = hh * 4 + kk;
+                const int li = kk < 2 ? hh * 2 + kk : hh * 2 + kk - 2, sh = kk < 2 ? 0 : 4;
+                code0[s] = ((ql0[li] >> sh) & 0x0F0F0F0Fu) | (((qh0[hh] >> (2 * kk)) & 0x03030303u) << 4);
+                code1[s] = ((ql1[li] >> sh) & 0x0F0F0F0Fu) | (((qh1[hh] >> (2 * kk)) & 0x03030303u) << 4);
+                const int gi = hh * 8 + 2 * kk; // lane j (< 4) uses group gi, lane j+4 group gi+1
+                scl0[s] = sbyte(sw[gi >> 2], gi & 3);
+                scl1[s] = sbyte(sw[(gi + 1) >> 2], (gi + 1) & 3);
+            }
+        // groups 2l, 2l+1: l = j -> bytes 2j, 2j+1 of word j/2; l = j+4 -> word 2 + j/2
+        os00 = sbyte(sw[j >> 1], 2 * (j & 1));
+        os01 = sbyte(sw[j >> 1], 2 * (j & 1) + 1);
+        os10 = sbyte(sw[2 + (j >> 1)], 2 * (j & 1));
+        os11 = sbyte(sw[2 + (j >> 1)], 2 * (j & 1) + 1);
+        dw = h2f(wv.d6);
+    } else {
+        const uint32_t q0 = wv.sc.y, q1 = wv.sc.z, q2 = wv.sc.w;
+        const uint32_t sc_lo = q0 & 0x3F3F3F3Fu, mn_lo = q1 & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (q2 & 0x0F0F0F0Fu) | ((q0 >> 2) & 0x30303030u);
+        const uint32_t mn_hi = ((q2 >> 4) & 0x0F0F0F0Fu) | ((q1 >> 2) & 0x30303030u);
+        const uint32_t mnw = j < 2 ? mn_lo : mn_hi;
+        mn0 = ubyte(mnw, 2 * (j & 1));
+        mn1 = ubyte(mnw, 2 * (j & 1) + 1);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            scl0[s] = scl1[s] = ubyte(sc_lo, s);
+            scl0[s + 4] = scl1[s + 4] = ubyte(sc_hi, s);
+        }
+        const uint32_t w0[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w};
+        const uint32_t w1[4] = {wv.qa1.x, wv.qa1.y, wv.qa1.z, wv.qa1.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            code0[2 * q] = w0[q] & 0x0F0F0F0Fu;
+            code0[2 * q + 1] = (w0[q] >> 4) & 0x0F0F0F0Fu;
+            code1[2 * q] = w1[q] & 0x0F0F0F0Fu;
+            code1[2 * q + 1] = (w1[q] >> 4) & 0x0F0F0F0Fu;
+        }
+        if constexpr (TYPE == AQ_TYPE_Q5_K) {
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                code0[s] |= ((wv.qb.x >> s) & 0x01010101u) << 4;
+                code1[s] |= ((wv.qb.y >> s) & 0x01010101u) << 4;
+            }
+        }
+        dw = h2f(wv.sc.x & 0xFFFF);
+        dminw = h2f(wv.sc.x >> 16);
+    }
+#pragma unroll
+    for (int cg = 0; cg < NCG; cg++) {
+        const int cA = cg * 4 + r < NC ? cg * 4 + r : 0; // this thread's A-operand column
+        const uint4 *xp = reinterpret_cast<const uint4 *>(xq + cA * 256 + j * 64);
+        const uint4 va = xp[0], vb = xp[1], vc = xp[2], vd = xp[3];
+        const uint32_t x0[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w}; // lane j
+        const uint32_t x1[8] = {vc.x, vc.y, vc.z, vc.w, vd.x, vd.y, vd.z, vd.w}; // lane j+4
+        int s0[4] = {0, 0, 0, 0}, s1[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const v4i d0 = mfma(x0[s], code0[s]);
+            const v4i d1 = mfma(x1[s], code1[s]);
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                if (cg * 4 + c < NC) { // the block's columns past NC are padding
+                    s0[c] += __mul24(scl0[s], d0[c]); // |d| <= 4*63*127 fits 24 bits
+                    s1[c] += __mul24(scl1[s], d1[c]);
+                }
+            }
+        }
+        const float4 dx4 = *reinterpret_cast<const float4 *>(xd + cg * 4);
+        const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+        const uint4 m0 = *reinterpret_cast<const uint4 *>(xm + j * ncp + cg * 4);
+        const uint32_t mw0[4] = {m0.x, m0.y, m0.z, m0.w};
+        uint32_t mw1[4] = {0, 0, 0, 0};
+        if constexpr (Q6) {
+            const uint4 m1 = *reinterpret_cast<const uint4 *>(xm + (j + 4) * ncp + cg * 4);
+            mw1[0] = m1.x;
+            mw1[1] = m1.y;
+            mw1[2] = m1.z;
+            mw1[3] = m1.w;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int col = cg * 4 + c;
+            if (col < NC) {
+                const float dd = dxs[c] * dw;
+                const int lo0 = (int)(int16_t)(mw0[c] & 0xFFFF), hi0 = (int)(int16_t)(mw0[c] >> 16);
+                if constexpr (Q6) {
+                    const int lo1 = (int)(int16_t)(mw1[c] & 0xFFFF), hi1 = (int)(int16_t)(mw1[c] >> 16);
+                    pr0[col] = dd * (float)(s0[c] - 32 * (lo0 * os00 + hi0 * os01));
+                    pr1[col] = dd * (float)(s1[c] - 32 * (lo1 * os10 + hi1 * os11));
+                } else {
+                    pr0[col] = dd * (float)s0[c];
+                    pr1[col] = dd * (float)s1[c];
+                    pm[col] = (-dxs[c] * dminw) * (float)(mn0 * lo0 + mn1 * hi0);
+                }
+            }
+        }
+    }
+}
+
+// Q4_K / Q5_K products with the sub-block scale inside the matrix-core operand. A 6-bit scale sc is split into
+// digits of DB bits (sc = sum_i digit_i << (DB*i); DB = 3 for Q4_K codes <= 15, DB = 2 for Q5_K codes <= 31), so
+// code * digit <= 105 (resp. 93) is an int8: one 32-bit multiply scales the 4 packed code bytes of a sub-block
+// without carries, and the MFMA accumulator sums sc_i-weighted dots over the 8 sub-blocks. The lane sum is then
+// sum_i D_i << (DB*i) = sum_s sc[s] * dot_s exactly — the same integer as kdot.rs:37-95 — with no per-output
+// scale multiply.
+template <int TYPE, int NC>
+__device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const int8_t *xq, const float *xd,
+                                                  const uint32_t *xm, int ncp, int j, int r, float *pr0,
+                                                  float *pr1, float *pm) {
+    constexpr int NCG = (NC + 3) / 4;
+    constexpr int DB = TYPE == AQ_TYPE_Q4_K ? 3 : 2;   // digit bits
+    constexpr int ND = TYPE == AQ_TYPE_Q4_K ? 2 : 3;   // digits of a 6-bit scale
+    constexpr uint32_t DM = (1u << DB) - 1u;
+    const uint32_t q0 = wv.sc.y, q1 = wv.sc.z, q2 = wv.sc.w;
+    const uint32_t sc_lo = q0 & 0x3F3F3F3Fu, mn_lo = q1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (q2 & 0x0F0F0F0Fu) | ((q0 >> 2) & 0x30303030u);
+    const uint32_t mn_hi = ((q2 >> 4) & 0x0F0F0F0Fu) | ((q1 >> 2) & 0x30303030u);
+    const uint32_t mnw = j < 2 ? mn_lo : mn_hi;
+    const int mn0 = ubyte(mnw, 2 * (j & 1)), mn1 = ubyte(mnw, 2 * (j & 1) + 1);
+    // digit words: byte s of dig[i][0] (s < 4) / dig[i][1] (s >= 4) = digit i of sc[s]
+    uint32_t dig[ND][2];
+#pragma unroll
+    for (int i = 0; i < ND; i++) {
+        dig[i][0] = (sc_lo >> (DB * i)) & (DM * 0x01010101u);
+        dig[i][1] = (sc_hi >> (DB * i)) & (DM * 0x01010101u);
+    }
+    uint32_t code0[8], code1[8];
+    const uint32_t w0[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w};
+    const uint32_t w1[4] = {wv.qa1.x, wv.qa1.y, wv.qa1.z, wv.qa1.w};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        code0[2 * q] = w0[q] & 0x0F0F0F0Fu;
+        code0[2 * q + 1] = (w0[q] >> 4) & 0x0F0F0F0Fu;
+        code1[2 * q] = w1[q] & 0x0F0F0F0Fu;
+        code1[2 * q + 1] = (w1[q] >> 4) & 0x0F0F0F0Fu;
+    }
+    if constexpr (TYPE == AQ_TYPE_Q5_K) {
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            code0[s] |= ((wv.qb.x >> s) & 0x01010101u) << 4;
+            code1[s] |= ((wv.qb.y >> s) & 0x01010101u) << 4;
+        }
+    }
+    const float dw = h2f(wv.sc.x & 0xFFFF), dminw = h2f(wv.sc.x >> 16);
+#pragma unroll
+    for (int cg = 0; cg < NCG; cg++) {
+        const int cA = cg * 4 + r < NC ? cg * 4 + r : 0;
+        const uint4 *xp = reinterpret_cast<const uint4 *>(xq + cA * 256 + j * 64);
+        const uint4 va = xp[0], vb = xp[1], vc = xp[2], vd = xp[3];
+        const uint32_t x0[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w}; // lane j
+        const uint32_t x1[8] = {vc.x, vc.y, vc.z, vc.w, vd.x, vd.y, vd.z, vd.w}; // lane j+4
+        v4i a0[ND], a1[ND];
+#pragma unroll
+        for (int i = 0; i < ND; i++) a0[i] = a1[i] = (v4i){0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+#pragma unroll
+            for (int i = 0; i < ND; i++) {
+                // digit i of sc[s] in both 16-bit halves, then one packed 16-bit multiply per code word (the four
+                // byte products stay below 256, so no carry crosses a byte)
+                const uint32_t sel = (uint32_t)(s & 3) | 0x0C00u | ((uint32_t)(s & 3) << 16) | 0x0C000000u;
+                const u16x2 d2 = as_u16x2(__builtin_amdgcn_perm(0u, dig[i][s >> 2], sel));
+                a0[i] = mfma_acc(x0[s], as_u32(as_u16x2(code0[s]) * d2), a0[i]);
+                a1[i] = mfma_acc(x1[s], as_u32(as_u16x2(code1[s]) * d2), a1[i]);
+            }
+        }
+        const float4 dx4 = *reinterpret_cast<const float4 *>(xd + cg * 4);
+        const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+        const uint4 m0 = *reinterpret_cast<const uint4 *>(xm + j * ncp + cg * 4);
+        const uint32_t mw0[4] = {m0.x, m0.y, m0.z, m0.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int col = cg * 4 + c;
+            if (col < NC) {
+                int s0 = a0[ND - 1][c], s1 = a1[ND - 1][c];
+#pragma unroll
+                for (int i = ND - 2; i >= 0; i--) {
+                    s0 = (s0 << DB) + a0[i][c];
+                    s1 = (s1 << DB) + a1[i][c];
+                }
+                const float dd = dxs[c] * dw;
+                const int lo0 = (int)(int16_t)(mw0[c] & 0xFFFF), hi0 = (int)(int16_t)(mw0[c] >> 16);
+                pr0[col] = dd * (float)s0;
+                pr1[col] = dd * (float)s1;
+                pm[col] = (-dxs[c] * dminw) * (float)(mn0 * lo0 + mn1 * hi0);
+            }
+        }
     }
 }
 
@@ -190,118 +412,12 @@ __global__ void __launch_bounds__(256) kq_mfma_kernel(MfArgs a) {
         const int ch = nb - c0 < CH ? nb - c0 : CH;
         const Lds<NC, CH> &L = lds_buf[k & 1];
 
-        // Products of one super-block: pr0/pr1 (lanes j, j+4) and pm (min lane j), per column.
         auto process = [&](const WRegs<TYPE> &wv, const int sbi, float *pr0, float *pr1, float *pm) {
-            uint32_t code0[8], code1[8]; // 4 unsigned codes per sub-block, lanes j and j+4
-            int scl0[8], scl1[8];        // integer scale per sub-block, lanes j and j+4
-            int mn0 = 0, mn1 = 0;        // Q4_K/Q5_K mins of sub-blocks 2j, 2j+1 (min lane j)
-            int os00 = 0, os01 = 0, os10 = 0, os11 = 0; // Q6_K -32 fold scales: groups 2l, 2l+1 of l = j, j+4
-            float dw, dminw = 0.0f;
-            if constexpr (Q6) {
-                const uint32_t ql0[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w};
-                const uint32_t ql1[4] = {wv.qa1.x, wv.qa1.y, wv.qa1.z, wv.qa1.w};
-                const uint32_t qh0[2] = {wv.qb.x, wv.qb.y}, qh1[2] = {wv.qb.z, wv.qb.w};
-                const uint32_t sw[4] = {wv.sc.x, wv.sc.y, wv.sc.z, wv.sc.w};
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++)
-#pragma unroll
-                    for (int kk = 0; kk < 4; kk++) {
-                        const int s = hh * 4 + kk;
-                        const int li = kk < 2 ? hh * 2 + kk : hh * 2 + kk - 2, sh = kk < 2 ? 0 : 4;
-                        code0[s] = ((ql0[li] >> sh) & 0x0F0F0F0Fu) | (((qh0[hh] >> (2 * kk)) & 0x03030303u) << 4);
-                        code1[s] = ((ql1[li] >> sh) & 0x0F0F0F0Fu) | (((qh1[hh] >> (2 * kk)) & 0x03030303u) << 4);
-                        const int gi = hh * 8 + 2 * kk; // lane j (< 4) uses group gi, lane j+4 group gi+1
-                        scl0[s] = sbyte(sw[gi >> 2], gi & 3);
-                        scl1[s] = sbyte(sw[(gi + 1) >> 2], (gi + 1) & 3);
-                    }
-                // groups 2l, 2l+1: l = j -> bytes 2j, 2j+1 of word j/2; l = j+4 -> word 2 + j/2
-                os00 = sbyte(sw[j >> 1], 2 * (j & 1));
-                os01 = sbyte(sw[j >> 1], 2 * (j & 1) + 1);
-                os10 = sbyte(sw[2 + (j >> 1)], 2 * (j & 1));
-                os11 = sbyte(sw[2 + (j >> 1)], 2 * (j & 1) + 1);
-                dw = h2f(wv.d6);
-            } else {
-                const uint32_t q0 = wv.sc.y, q1 = wv.sc.z, q2 = wv.sc.w;
-                const uint32_t sc_lo = q0 & 0x3F3F3F3Fu, mn_lo = q1 & 0x3F3F3F3Fu;
-                const uint32_t sc_hi = (q2 & 0x0F0F0F0Fu) | ((q0 >> 2) & 0x30303030u);
-                const uint32_t mn_hi = ((q2 >> 4) & 0x0F0F0F0Fu) | ((q1 >> 2) & 0x30303030u);
-                const uint32_t mnw = j < 2 ? mn_lo : mn_hi;
-                mn0 = ubyte(mnw, 2 * (j & 1));
-                mn1 = ubyte(mnw, 2 * (j & 1) + 1);
-#pragma unroll
-                for (int s = 0; s < 4; s++) {
-                    scl0[s] = scl1[s] = ubyte(sc_lo, s);
-                    scl0[s + 4] = scl1[s + 4] = ubyte(sc_hi, s);
-                }
-                const uint32_t w0[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w};
-                const uint32_t w1[4] = {wv.qa1.x, wv.qa1.y, wv.qa1.z, wv.qa1.w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    code0[2 * q] = w0[q] & 0x0F0F0F0Fu;
-                    code0[2 * q + 1] = (w0[q] >> 4) & 0x0F0F0F0Fu;
-                    code1[2 * q] = w1[q] & 0x0F0F0F0Fu;
-                    code1[2 * q + 1] = (w1[q] >> 4) & 0x0F0F0F0Fu;
-                }
-                if constexpr (TYPE == AQ_TYPE_Q5_K) {
-#pragma unroll
-                    for (int s = 0; s < 8; s++) {
-                        code0[s] |= ((wv.qb.x >> s) & 0x01010101u) << 4;
-                        code1[s] |= ((wv.qb.y >> s) & 0x01010101u) << 4;
-                    }
-                }
-                dw = h2f(wv.sc.x & 0xFFFF);
-                dminw = h2f(wv.sc.x >> 16);
-            }
-#pragma unroll
-            for (int cg = 0; cg < NCG; cg++) {
-                const int cA = cg * 4 + r < NC ? cg * 4 + r : 0; // this thread's A-operand column
-                const uint4 *xp = reinterpret_cast<const uint4 *>(&L.xq[sbi][cA][j * 64]);
-                const uint4 xa = xp[0], xb = xp[1], xc = xp[2], xd = xp[3];
-                const uint32_t x0[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w}; // lane j
-                const uint32_t x1[8] = {xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w}; // lane j+4
-                int s0[4] = {0, 0, 0, 0}, s1[4] = {0, 0, 0, 0};
-#pragma unroll
-                for (int s = 0; s < 8; s++) {
-                    const v4i d0 = mfma(x0[s], code0[s]);
-                    const v4i d1 = mfma(x1[s], code1[s]);
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        if (cg * 4 + c < NC) { // the block's columns past NC are padding
-                            s0[c] += scl0[s] * d0[c];
-                            s1[c] += scl1[s] * d1[c];
-                        }
-                    }
-                }
-                const float4 dx4 = *reinterpret_cast<const float4 *>(&L.xd[sbi][cg * 4]);
-                const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-                const uint4 m0 = *reinterpret_cast<const uint4 *>(&L.xm[sbi][j][cg * 4]);
-                const uint32_t mw0[4] = {m0.x, m0.y, m0.z, m0.w};
-                uint32_t mw1[4] = {0, 0, 0, 0};
-                if constexpr (Q6) {
-                    const uint4 m1 = *reinterpret_cast<const uint4 *>(&L.xm[sbi][j + 4][cg * 4]);
-                    mw1[0] = m1.x;
-                    mw1[1] = m1.y;
-                    mw1[2] = m1.z;
-                    mw1[3] = m1.w;
-                }
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const int col = cg * 4 + c;
-                    if (col < NC) {
-                        const float dd = dxs[c] * dw;
-                        const int lo0 = (int)(int16_t)(mw0[c] & 0xFFFF), hi0 = (int)(int16_t)(mw0[c] >> 16);
-                        if constexpr (Q6) {
-                            const int lo1 = (int)(int16_t)(mw1[c] & 0xFFFF), hi1 = (int)(int16_t)(mw1[c] >> 16);
-                            pr0[col] = dd * (float)(s0[c] - 32 * (lo0 * os00 + hi0 * os01));
-                            pr1[col] = dd * (float)(s1[c] - 32 * (lo1 * os10 + hi1 * os11));
-                        } else {
-                            pr0[col] = dd * (float)s0[c];
-                            pr1[col] = dd * (float)s1[c];
-                            pm[col] = (-dxs[c] * dminw) * (float)(mn0 * lo0 + mn1 * hi0);
-                        }
-                    }
-                }
-            }
+            if constexpr (TYPE == AQ_TYPE_Q6_K)
+                sb_products<TYPE, NC>(wv, &L.xq[sbi][0][0], &L.xd[sbi][0], &L.xm[sbi][0][0], NCP, j, r, pr0, pr1, pm);
+            else
+                sb_products_split<TYPE, NC>(wv, &L.xq[sbi][0][0], &L.xd[sbi][0], &L.xm[sbi][0][0], NCP, j, r, pr0, pr1,
+                                            pm);
         };
 
         for (int rb = 0; rb < ch; rb += KS * PF) {
@@ -379,9 +495,10 @@ __global__ void __launch_bounds__(256) kq_mfma_kernel(MfArgs a) {
 
 template <int TYPE, int NC, int KS>
 int launch_ks(const MfArgs &args, hipStream_t stream) {
-    // prefetch depth and chunk (CH a multiple of KS * PF); two chunk buffers in LDS
-    constexpr int PF = NC <= 4 ? 4 : 2;
-    constexpr int CH = KS * PF * (NC <= 2 ? 2 : 1);
+    // prefetch depth and chunk (CH a multiple of KS * PF; two chunk buffers in LDS), from a sweep on MI355X of the
+    // 27B shapes at N = 1, 4: fewer registers and smaller chunks beat deeper prefetch at this occupancy
+    constexpr int PF = KS == 1 ? 4 : 2;
+    constexpr int CH = KS * PF;
     constexpr int ROWS = 64 / KS;
     const dim3 grid((unsigned)((args.rows + ROWS - 1) / ROWS)), block(256);
     hipLaunchKernelGGL((kq_mfma_kernel<TYPE, NC, KS, PF, CH>), grid, block, 0, stream, args);
