@@ -581,13 +581,18 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
     float *bv = mode == VERIFY ? s->sv_b[dn_slot] : s->b;
     if ((rc = mm(s, L.qkv, s->act_h, t, mixed))) return rc;
     if ((rc = mm(s, L.gate_z, s->act_h, t, s->z))) return rc;
-    if ((rc = mm(s, L.alpha, s->act_h, t, av))) return rc;
-    if ((rc = mm(s, L.beta, s->act_h, t, bv))) return rc;
+    AQ_REQUIRE(L.alpha.type == AQ_TYPE_F32 && L.beta.type == AQ_TYPE_F32,
+               "DeltaNet: ssm_alpha / ssm_beta must be F32 in this build");
     DnArgs d;
     d.mixed = mixed;
     d.z = s->z;
-    d.a = av;
+    d.a = av; // ssm_alpha / ssm_beta projections computed inside the DeltaNet kernel, kept here
     d.b = bv;
+    d.x = s->act_h.f32;
+    d.x_stride = s->act_h.n;
+    d.w_alpha = reinterpret_cast<const float *>(L.alpha.qa);
+    d.w_beta = reinterpret_cast<const float *>(L.beta.qa);
+    d.hidden = (int)c.hidden;
     d.conv_src = s->par ? s->conv1[dn_slot] : s->conv0[dn_slot];
     d.conv_dst = mode == VERIFY ? nullptr : (s->par ? s->conv0[dn_slot] : s->conv1[dn_slot]);
     d.conv_w = L.conv_w;
@@ -802,7 +807,7 @@ int aq_model_load(aq_ctx *ctx, const aq_model_config *cfg, const aq_tensor *tens
     src.stream = ctx->stream;
     src.device = ctx->device;
     rc = build_model(ctx, cfg, src, out);
-    if (!rc) AQ_HIP(hipStreamSynchronize(ctx->stream));
+    if (!rc) AQ_HIP(hipDeviceSynchronize()); // vectors went up on the null stream, weights on the context stream
     return rc;
 }
 
@@ -818,7 +823,7 @@ int aq_model_synth(aq_ctx *ctx, const aq_model_config *cfg, int mix, uint64_t se
     src.stream = ctx->stream;
     src.device = ctx->device;
     rc = build_model(ctx, cfg, src, out);
-    if (!rc) AQ_HIP(hipStreamSynchronize(ctx->stream));
+    if (!rc) AQ_HIP(hipDeviceSynchronize()); // vectors went up on the null stream, weights on the context stream
     return rc;
 }
 
@@ -946,6 +951,9 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
     }
     if (!rc && hipHostMalloc((void **)&s->pinned, 64 * 4, hipHostMallocDefault) != hipSuccess)
         rc = fail(AQ_ENOMEM, "state: pinned");
+    // The clears and table uploads above ran on the null stream, which the state's non-blocking stream does not
+    // wait for: finish them before the first kernel on that stream can read the buffers.
+    if (!rc && hipDeviceSynchronize() != hipSuccess) rc = fail(AQ_EHIP, "state: setup sync");
 #undef AQ_S
     if (rc) {
         free_state(s);
@@ -1268,11 +1276,13 @@ int aq_layer_run(aq_ctx *ctx, const aq_model_config *cfg, const aq_tensor *tenso
     const size_t rec_len = (size_t)c.dn_n_v_heads * c.dn_head_dim_k * c.dn_head_dim_v, conv_len = m->cd * 3;
     const size_t stride = (size_t)c.n_head_kv * c.head_dim;
     auto h2d = [&](void *d, const void *hs, size_t bytes) -> int {
-        AQ_HIP(hipMemcpy(d, hs, bytes, hipMemcpyHostToDevice));
+        AQ_HIP(hipMemcpyAsync(d, hs, bytes, hipMemcpyHostToDevice, s->stream));
+        AQ_HIP(hipStreamSynchronize(s->stream));
         return 0;
     };
     auto d2h = [&](void *hs, const void *d, size_t bytes) -> int {
-        AQ_HIP(hipMemcpy(hs, d, bytes, hipMemcpyDeviceToHost));
+        AQ_HIP(hipMemcpyAsync(hs, d, bytes, hipMemcpyDeviceToHost, s->stream));
+        AQ_HIP(hipStreamSynchronize(s->stream));
         return 0;
     };
     if (!rc) rc = h2d(s->xa, x, t * h * 4);

@@ -40,7 +40,11 @@ int launch_swiglu(const float *g, const float *u, size_t n, size_t t, float *h_f
 struct DnArgs {
     const float *mixed = nullptr; // t x cd conv inputs (the qkv projection)
     const float *z = nullptr;     // t x vd output gate (null: no output)
-    const float *a = nullptr, *b = nullptr; // t x nv gate pre-activations
+    float *a = nullptr, *b = nullptr;       // t x nv gate pre-activations (written when x is set, else read)
+    const float *x = nullptr;               // when set: a, b = ssm_alpha / ssm_beta (F32) rows . x rows
+    size_t x_stride = 0;
+    const float *w_alpha = nullptr, *w_beta = nullptr; // nv x hidden F32
+    int hidden = 0;
     const float *conv_src = nullptr;        // cd x (K-1) window
     float *conv_dst = nullptr;              // null: window not written
     const float *conv_w = nullptr;          // cd x K

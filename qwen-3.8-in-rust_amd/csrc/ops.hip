@@ -140,60 +140,150 @@ __device__ __forceinline__ float conv_step(float win[3], const float c[4], float
     return silu_f(acc);
 }
 
-template <int DK>
-__global__ void __launch_bounds__(256) dn_core_kernel(DnArgs a) {
-    __shared__ float qn[DK], kn[DK], ob[256], red[16];
-    const int p = blockIdx.x, j = threadIdx.x;
-    const int kh = p % a.nk, dv = a.dv;
-    const int kd = a.nk * DK, vd = a.nv * dv, cd = 2 * kd + vd;
-    const bool has_qk = j < DK, has_v = j < dv;
-    float wq[3] = {0, 0, 0}, wk[3] = {0, 0, 0}, wv[3] = {0, 0, 0};
-    float cq[4] = {0, 0, 0, 0}, ck[4] = {0, 0, 0, 0}, cv[4] = {0, 0, 0, 0};
-    const int chq = kh * DK + j, chk = kd + kh * DK + j, chv = 2 * kd + p * dv + j;
-    if (!a.raw) {
-        if (has_qk) {
-            for (int e = 0; e < 3; e++) {
-                wq[e] = a.conv_src[(size_t)chq * 3 + e];
-                wk[e] = a.conv_src[(size_t)chk * 3 + e];
-            }
-            for (int e = 0; e < 4; e++) {
-                cq[e] = a.conv_w[(size_t)chq * 4 + e];
-                ck[e] = a.conv_w[(size_t)chk * 4 + e];
-            }
-        }
-        if (has_v) {
-            for (int e = 0; e < 3; e++) wv[e] = a.conv_src[(size_t)chv * 3 + e];
-            for (int e = 0; e < 4; e++) cv[e] = a.conv_w[(size_t)chv * 4 + e];
-        }
-    }
-    float s[DK];
-    float *srec = a.rec + (size_t)p * DK * dv;
-#pragma unroll
-    for (int k = 0; k < DK; k++) s[k] = has_v ? srec[(size_t)k * dv + j] : 0.0f;
-    const float big_a = a.raw ? 0.0f : a.ssm_a[p], dtb = a.raw ? 0.0f : a.dt_bias[p];
-    const int tk = blockDim.x > 64 ? 64 : 1; // the k-norm chain runs in another wave when there is one
+constexpr int DN_TMAX = 8;      // rows per DeltaNet launch
+constexpr int DN_BLK_MAX = 256; // 32-blocks of the alpha/beta rows (hidden <= 8192)
 
-    for (int i = 0; i < a.t; i++) {
-        float vval = 0.0f;
+template <int DK, int DV>
+__global__ void __launch_bounds__(256) dn_core_kernel(DnArgs a) {
+    constexpr int NT = ((DK > DV ? DK : DV) + 63) / 64 * 64;
+    __shared__ float qn[DK], kn[DK], ob[DV], red[16];
+    __shared__ float in_q[DN_TMAX][DK], in_k[DN_TMAX][DK], in_v[DN_TMAX][DV], in_z[DN_TMAX][DV];
+    __shared__ float gab[2][DN_TMAX]; // per row: a (or g), b (or beta)
+    const int p = blockIdx.x, j = threadIdx.x;
+    const int kh = p % a.nk, t = a.t;
+    const int kd = a.nk * DK, vd = a.nv * DV, cd = 2 * kd + vd;
+    const bool has_qk = j < DK, has_v = j < DV;
+    const int jq = has_qk ? j : 0, jv = has_v ? j : 0; // in-range indices for the lanes past a head's width
+    const int chq = kh * DK + jq, chk = kd + kh * DK + jq, chv = 2 * kd + p * DV + jv;
+
+    // ---- every row's inputs to LDS up front (one round trip instead of one per row)
+    for (int i = 0; i < t; i++) {
         if (a.raw) {
             if (has_qk) {
-                qn[j] = a.rq[(size_t)i * kd + kh * DK + j];
-                kn[j] = a.rk[(size_t)i * kd + kh * DK + j];
+                in_q[i][j] = a.rq[(size_t)i * kd + kh * DK + j];
+                in_k[i][j] = a.rk[(size_t)i * kd + kh * DK + j];
             }
-            if (has_v) vval = a.rv[(size_t)i * vd + p * dv + j];
+            if (has_v) in_v[i][j] = a.rv[(size_t)i * vd + p * DV + j];
         } else {
             const float *mrow = a.mixed + (size_t)i * cd;
             if (has_qk) {
-                qn[j] = conv_step(wq, cq, mrow[chq]);
-                kn[j] = conv_step(wk, ck, mrow[chk]);
+                in_q[i][j] = mrow[chq];
+                in_k[i][j] = mrow[chk];
             }
-            if (has_v) vval = conv_step(wv, cv, mrow[chv]);
+            if (has_v) {
+                in_v[i][j] = mrow[chv];
+                if (a.z) in_z[i][j] = a.z[(size_t)i * vd + p * DV + j];
+            }
+        }
+    }
+    if (a.raw) {
+        if (j < t) {
+            gab[0][j] = a.rg[(size_t)j * a.nv + p];
+            gab[1][j] = a.rbeta[(size_t)j * a.nv + p];
+        }
+    } else if (!a.x) {
+        if (j < t) {
+            gab[0][j] = a.a[(size_t)j * a.nv + p];
+            gab[1][j] = a.b[(size_t)j * a.nv + p];
+        }
+    } else {
+        // gated_deltanet.rs:271-274 ssm_alpha / ssm_beta rows of this head on the t input rows, dot.rs:180-200:
+        // 32-element partials left to right (one thread per block and row), then the block chain (one thread per
+        // (row, input)), `acc + part` with the short tail (0.0f when there is none).
+        __shared__ float part[2][DN_TMAX][DN_BLK_MAX];
+        const int n = a.hidden, nblk = (n + 31) / 32;
+        for (int task = j; task < 2 * nblk; task += NT) {
+            const int r = task / nblk, b = task % nblk;
+            const float *w = (r == 0 ? a.w_alpha : a.w_beta) + (size_t)p * n;
+            const int e0 = b * 32, ne = n - e0 < 32 ? n - e0 : 32;
+            float wv[32];
+            if (ne == 32 && (n & 3) == 0) {
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const float4 f = *reinterpret_cast<const float4 *>(w + e0 + 4 * u);
+                    wv[4 * u] = f.x;
+                    wv[4 * u + 1] = f.y;
+                    wv[4 * u + 2] = f.z;
+                    wv[4 * u + 3] = f.w;
+                }
+                for (int i = 0; i < t; i++) {
+                    const float *xr = a.x + (size_t)i * a.x_stride + e0;
+                    float xv[32];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        const float4 f = *reinterpret_cast<const float4 *>(xr + 4 * u);
+                        xv[4 * u] = f.x;
+                        xv[4 * u + 1] = f.y;
+                        xv[4 * u + 2] = f.z;
+                        xv[4 * u + 3] = f.w;
+                    }
+                    float pt = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 32; e++) pt += wv[e] * xv[e];
+                    part[r][i][b] = pt;
+                }
+            } else {
+                for (int i = 0; i < t; i++) {
+                    const float *xr = a.x + (size_t)i * a.x_stride + e0;
+                    float pt = 0.0f;
+                    for (int e = 0; e < ne; e++) pt += w[e0 + e] * xr[e];
+                    part[r][i][b] = pt;
+                }
+            }
+        }
+        __syncthreads();
+        if (j < 2 * t) {
+            const int r = j / t, i = j % t;
+            float v = seq_sum<false>(&part[r][i][0], 0, nblk, 1, 0.0f);
+            if (n % 32 == 0) v = v + 0.0f;
+            gab[r][i] = v;
+            (r == 0 ? a.a : a.b)[(size_t)i * a.nv + p] = v; // kept for the commit
+        }
+    }
+
+    // ---- state and conv windows
+    float wq[3] = {0, 0, 0}, wk[3] = {0, 0, 0}, wv[3] = {0, 0, 0};
+    float cq[4] = {0, 0, 0, 0}, ck[4] = {0, 0, 0, 0}, cv[4] = {0, 0, 0, 0};
+    if (!a.raw) {
+        for (int e = 0; e < 3; e++) {
+            wq[e] = a.conv_src[(size_t)chq * 3 + e];
+            wk[e] = a.conv_src[(size_t)chk * 3 + e];
+            wv[e] = a.conv_src[(size_t)chv * 3 + e];
+        }
+        for (int e = 0; e < 4; e++) {
+            cq[e] = a.conv_w[(size_t)chq * 4 + e];
+            ck[e] = a.conv_w[(size_t)chk * 4 + e];
+            cv[e] = a.conv_w[(size_t)chv * 4 + e];
+        }
+    }
+    float s[DK];
+    float *srec = a.rec + (size_t)p * DK * DV;
+#pragma unroll
+    for (int k = 0; k < DK; k++) s[k] = srec[(size_t)k * DV + jv];
+    const float big_a = a.raw ? 0.0f : a.ssm_a[p], dtb = a.raw ? 0.0f : a.dt_bias[p];
+    const int tk = NT > 64 ? 64 : 1; // the k-norm chain runs in another wave when there is one
+    __syncthreads();
+
+    for (int i = 0; i < t; i++) {
+        float vval = 0.0f;
+        if (a.raw) {
+            if (has_qk) {
+                qn[j] = in_q[i][j];
+                kn[j] = in_k[i][j];
+            }
+            if (has_v) vval = in_v[i][j];
+        } else {
+            if (has_qk) {
+                qn[j] = conv_step(wq, cq, in_q[i][j]);
+                kn[j] = conv_step(wk, ck, in_k[i][j]);
+            }
+            if (has_v) vval = conv_step(wv, cv, in_v[i][j]);
         }
         __syncthreads();
         float g, beta;
         if (a.raw) {
-            g = a.rg[(size_t)i * a.nv + p];
-            beta = a.rbeta[(size_t)i * a.nv + p];
+            g = gab[0][i];
+            beta = gab[1][i];
         } else {
             if (j == 0 || j == tk) { // deltanet.rs:19-29 l2norm, eps 1e-6
                 const float ss = seq_sum<true>(j == 0 ? qn : kn, 0, DK, 1, 0.0f);
@@ -206,11 +296,11 @@ __global__ void __launch_bounds__(256) dn_core_kernel(DnArgs a) {
                 kn[j] = kn[j] * red[1];
             }
             __syncthreads();
-            g = big_a * softplus_f(a.a[(size_t)i * a.nv + p] + dtb); // deltanet.rs:32-35 gate_g
-            beta = sigmoid_f(a.b[(size_t)i * a.nv + p]);
+            g = big_a * softplus_f(gab[0][i] + dtb); // deltanet.rs:32-35 gate_g
+            beta = sigmoid_f(gab[1][i]);
         }
         float ov = 0.0f;
-        if (has_v) { // deltanet.rs:43-86
+        { // deltanet.rs:43-86, column j of the head's state
             const float decay = exp_f(g);
 #pragma unroll
             for (int k = 0; k < DK; k++) s[k] *= decay;
@@ -225,22 +315,22 @@ __global__ void __launch_bounds__(256) dn_core_kernel(DnArgs a) {
         }
         if (a.out) {
             if (a.raw) {
-                if (has_v) a.out[(size_t)i * vd + p * dv + j] = ov;
+                if (has_v) a.out[(size_t)i * vd + p * DV + j] = ov;
             } else {
                 if (has_v) ob[j] = ov;
                 __syncthreads();
-                const int n8 = dv / 8 * 8;
+                constexpr int n8 = DV / 8 * 8;
                 if (j < 8) red[4 + j] = seq_sum<true>(ob, j, n8, 8, 0.0f);
                 __syncthreads();
                 if (j == 0) {
                     float ss = reduce8_f(red + 4);
-                    for (int e = n8; e < dv; e++) ss += ob[e] * ob[e];
-                    red[2] = 1.0f / sqrtf(ss / (float)dv + a.eps);
+                    for (int e = n8; e < DV; e++) ss += ob[e] * ob[e];
+                    red[2] = 1.0f / sqrtf(ss / (float)DV + a.eps);
                 }
                 __syncthreads();
                 if (has_v) {
-                    const size_t o = (size_t)i * vd + p * dv + j;
-                    a.out[o] = (a.ssm_norm[j] * (ov * red[2])) * silu_f(a.z[o]);
+                    const size_t o = (size_t)i * vd + p * DV + j;
+                    a.out[o] = (a.ssm_norm[j] * (ov * red[2])) * silu_f(in_z[i][j]);
                 }
             }
         }
@@ -248,7 +338,7 @@ __global__ void __launch_bounds__(256) dn_core_kernel(DnArgs a) {
     }
     if (a.write_state && has_v) {
 #pragma unroll
-        for (int k = 0; k < DK; k++) srec[(size_t)k * dv + j] = s[k];
+        for (int k = 0; k < DK; k++) srec[(size_t)k * DV + j] = s[k];
     }
     if (a.conv_dst && !a.raw) {
         if (has_v)
@@ -554,13 +644,19 @@ int launch_dn_core(const DnArgs &a, hipStream_t stream) {
     } else {
         AQ_REQUIRE(a.rq && a.rk && a.rv && a.rg && a.rbeta, "deltanet: raw inputs");
     }
+    AQ_REQUIRE(a.t <= DN_TMAX, "deltanet: at most 8 rows per launch");
+    AQ_REQUIRE(a.raw || a.x || (a.a && a.b), "deltanet: gate inputs");
+    AQ_REQUIRE(!a.x || (a.w_alpha && a.w_beta && a.a && a.b && a.hidden > 0 && a.hidden <= 32 * DN_BLK_MAX),
+               "deltanet: alpha/beta projection");
     const int threads = ((a.dk > a.dv ? a.dk : a.dv) + 63) / 64 * 64;
-    switch (a.dk) {
-#define AQ_DK(D)                                                                                              \
-    case D: hipLaunchKernelGGL(dn_core_kernel<D>, dim3((unsigned)a.nv), dim3(threads), 0, stream, a); break;
-        AQ_DK(8) AQ_DK(16) AQ_DK(32) AQ_DK(64) AQ_DK(128)
-#undef AQ_DK
-    default: return fail(AQ_EUNSUP, "deltanet: head_dim_k must be 8, 16, 32, 64 or 128 in this build");
+    const int key = a.dk * 1000 + a.dv;
+    switch (key) {
+#define AQ_DN(K, V)                                                                                           \
+    case K * 1000 + V: hipLaunchKernelGGL((dn_core_kernel<K, V>), dim3((unsigned)a.nv), dim3(threads), 0, stream, a); break;
+        AQ_DN(8, 8) AQ_DN(16, 16) AQ_DN(32, 32) AQ_DN(64, 64) AQ_DN(128, 128) AQ_DN(128, 256) AQ_DN(64, 128)
+#undef AQ_DN
+    default: return fail(AQ_EUNSUP, "deltanet: head dims (k, v) not built: " + std::to_string(a.dk) + ", " +
+                                        std::to_string(a.dv));
     }
     return launched("deltanet");
 }

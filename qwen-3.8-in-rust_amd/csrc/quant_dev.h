@@ -25,10 +25,20 @@ __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : aq
 template <bool SQUARE>
 __device__ __forceinline__ float seq_sum(const float *x, int start, int end, int stride, float acc) {
     int i = start;
-    for (; i + 15 * stride < end; i += 16 * stride) {
+    if (i + 15 * stride < end) {
         float v[16];
 #pragma unroll
         for (int u = 0; u < 16; u++) v[u] = x[i + u * stride];
+        i += 16 * stride;
+        for (; i + 15 * stride < end; i += 16 * stride) { // next batch in flight while this one is summed
+            float w[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) w[u] = x[i + u * stride];
+#pragma unroll
+            for (int u = 0; u < 16; u++) acc += SQUARE ? v[u] * v[u] : v[u];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = w[u];
+        }
 #pragma unroll
         for (int u = 0; u < 16; u++) acc += SQUARE ? v[u] * v[u] : v[u];
     }
@@ -47,8 +57,7 @@ __device__ __forceinline__ void copy_rows_in(float *dst, const float *src, int n
         for (int i = tid; i < n4; i += 8 * nthreads) {
             float4 v[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (i + u * nthreads < n4) v[u] = s4[i + u * nthreads];
+            for (int u = 0; u < 8; u++) v[u] = s4[min(i + u * nthreads, n4 - 1)]; // clamped: always in range
 #pragma unroll
             for (int u = 0; u < 8; u++)
                 if (i + u * nthreads < n4) d4[i + u * nthreads] = v[u];
@@ -58,8 +67,7 @@ __device__ __forceinline__ void copy_rows_in(float *dst, const float *src, int n
     for (int i = tid; i < n; i += 8 * nthreads) {
         float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (i + u * nthreads < n) v[u] = src[i + u * nthreads];
+        for (int u = 0; u < 8; u++) v[u] = src[min(i + u * nthreads, n - 1)];
 #pragma unroll
         for (int u = 0; u < 8; u++)
             if (i + u * nthreads < n) dst[i + u * nthreads] = v[u];
@@ -71,34 +79,50 @@ __device__ __forceinline__ float reduce8_f(const float *l) {
     return ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
 }
 
+// Cross-lane steps on the DPP network (full rate, no LDS round trip).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_mov(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xF, false);
+}
+// Wave-wide max / min of ints (order-free, so exact); the result is uniform.
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = max(v, dpp_mov<0xB1>(v));       // quad_perm [1,0,3,2]
+    v = max(v, dpp_mov<0x4E>(v));       // quad_perm [2,3,0,1]
+    v = max(v, dpp_mov<0x124>(v));      // row_ror:4
+    v = max(v, dpp_mov<0x128>(v));      // row_ror:8 (every lane of a row holds the row's max)
+    v = max(v, dpp_mov<0x142, 0xA>(v)); // row_bcast:15 into rows 1 and 3
+    v = max(v, dpp_mov<0x143, 0xC>(v)); // row_bcast:31 into rows 2 and 3
+    return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+    v = min(v, dpp_mov<0xB1>(v));
+    v = min(v, dpp_mov<0x4E>(v));
+    v = min(v, dpp_mov<0x124>(v));
+    v = min(v, dpp_mov<0x128>(v));
+    v = min(v, dpp_mov<0x142, 0xA>(v));
+    v = min(v, dpp_mov<0x143, 0xC>(v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 // One Q8_K block (256 values) quantised by one wave: lane i holds x[4i..4i+3]. Q8KRow::quantize_scalar_into
 // (q8k.rs:76-114): max = the first element with the largest |x|, iscale = -127/max, q = min(127,
-// round_ties_even(iscale*x)), d = 1/iscale (0 for an all-zero block), bsums per 16, q8s per 32. Writes the
-// block at (qs_blk, *d_out, bs_blk[16], q8s_blk[8]) in the kernels' lane-slot code order.
+// round_ties_even(iscale*x)), d = 1/iscale (0 for an all-zero block), bsums per 16, q8s per 32. The largest |x|
+// (a max, order-free) and then its first index (a min over lanes) come from DPP reductions. Writes the block at
+// (qs_blk, *d_out, bs_blk[16], q8s_blk[8]) in the kernels' lane-slot code order.
 __device__ __forceinline__ void q8k_block_wave(const float x[4], int lane, int8_t *qs_blk, float *d_out,
                                                int16_t *bs_blk, int16_t *q8s_blk) {
-    float amax = 0.0f, maxv = 0.0f;
-    int idx = 0x7fffffff;
+    float la = fabsf(x[0]);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float a = fabsf(x[j]);
-        if (a > amax) {
-            amax = a;
-            idx = lane * 4 + j;
-            maxv = x[j];
-        }
-    }
+    for (int j = 1; j < 4; j++) la = fmaxf(la, fabsf(x[j]));
+    const int amax_bits = wave_max_i32(__float_as_int(la)); // |x| >= 0: int order is float order
+    const float amax = __int_as_float(amax_bits);
+    int first = 0x7fffffff;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float oa = __shfl_xor(amax, off);
-        const int oi = __shfl_xor(idx, off);
-        const float om = __shfl_xor(maxv, off);
-        if (oa > amax || (oa == amax && oi < idx)) {
-            amax = oa;
-            idx = oi;
-            maxv = om;
-        }
-    }
+    for (int j = 3; j >= 0; j--)
+        if (__float_as_int(fabsf(x[j])) == amax_bits) first = lane * 4 + j;
+    const int idx = wave_min_i32(first);
+    const float pick = (idx & 3) == 0 ? x[0] : (idx & 3) == 1 ? x[1] : (idx & 3) == 2 ? x[2] : x[3];
+    const float maxv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pick), idx >> 2));
     int q[4] = {0, 0, 0, 0};
     if (amax != 0.0f) {
         const float iscale = -127.0f / maxv;
@@ -116,10 +140,10 @@ __device__ __forceinline__ void q8k_block_wave(const float x[4], int lane, int8_
                             ((uint32_t)(uint8_t)q[3] << 24);
     *reinterpret_cast<uint32_t *>(qs_blk + lane_slot(l) * 32 + s * 4) = packed;
     int sum = q[0] + q[1] + q[2] + q[3];
-    sum += __shfl_xor(sum, 1);
-    sum += __shfl_xor(sum, 2);
+    sum += dpp_mov<0xB1>(sum); // quad: the 16 values of a group
+    sum += dpp_mov<0x4E>(sum);
     if ((lane & 3) == 0) bs_blk[lane >> 2] = (int16_t)sum;
-    const int s32 = sum + __shfl_xor(sum, 4);
+    const int s32 = sum + dpp_mov<0x12C>(sum); // row_ror:12 = lane i + 4: the next quad, a 32-value sub-block
     if ((lane & 7) == 0) q8s_blk[lane >> 3] = (int16_t)s32;
 }
 

@@ -91,6 +91,8 @@ int alloc_act(Act &a, size_t n, size_t ncols, int device) {
     void *p = nullptr;
     if (hipMalloc(&p, total) != hipSuccess) return fail(AQ_ENOMEM, "act: hipMalloc");
     if (hipMemset(p, 0, total) != hipSuccess) return fail(AQ_EHIP, "act: hipMemset");
+    // The clear runs on the null stream, which the context's non-blocking stream does not wait for.
+    if (hipDeviceSynchronize() != hipSuccess) return fail(AQ_EHIP, "act: clear sync");
     uint8_t *b = (uint8_t *)p;
     a.base = p;
     a.f32 = (float *)b;
