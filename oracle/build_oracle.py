@@ -1,7 +1,8 @@
 """Build recipe for the CPU oracle (test infrastructure only): compiles oracle/*.c into oracle/liboracle.so.
 
 -ffp-contract=off keeps every multiply-add a rounded multiply then a rounded add, as the reference's kernels
-require; -mavx2 lets gcc vectorise the independent-lane loops without changing their order (no -ffast-math).
+require; -mavx2 lets gcc vectorise the independent-lane loops without changing their order (no -ffast-math), and
+-mfma makes the explicit fused multiply-adds of aq_math.h single instructions (with contraction still off).
 """
 import os
 import subprocess
@@ -20,7 +21,7 @@ def build(verbose: bool = False) -> str:
     """liboracle.so (exp / log1p from aq_math.h) and liboracle_libm.so (the platform libm's expf / log1pf)."""
     for out, libm in ((LIB, 0), (LIB_LIBM, 1)):
         cmd = ["gcc", "-O3", "-std=gnu11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off", "-fno-fast-math",
-               "-mavx2", "-Wall", "-Wno-unknown-pragmas", f"-DOR_LIBM={libm}", "-I", MATH_DIR, "-o", out + ".tmp"]
+               "-mavx2", "-mfma", "-Wall", "-Wno-unknown-pragmas", f"-DOR_LIBM={libm}", "-I", MATH_DIR, "-o", out + ".tmp"]
         cmd += [os.path.join(HERE, s) for s in SOURCES] + ["-lm"]
         if verbose:
             print(" ".join(cmd), flush=True)

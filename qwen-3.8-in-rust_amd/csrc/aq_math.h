@@ -1,7 +1,8 @@
 /*
  * aq_math.h — exp and log1p for the f32 activations (silu, sigmoid, softplus, softmax, the DeltaNet decay), built
- * only from IEEE double additions, multiplications, divisions and rint, so the same source gives the same bits on
- * the host (gcc, SSE2) and on the device (hipcc): compile both with floating-point contraction off.
+ * only from IEEE double additions, multiplications, fused multiply-adds, divisions and rint — each correctly rounded
+ * by definition — so the same source gives the same bits on the host (gcc; fma() from libm) and on the device
+ * (hipcc; v_fma_f64): compile both with floating-point contraction off.
  *
  * The reference calls the platform libm's expf / log1pf (act.rs:7-40, softmax.rs:22-49, deltanet.rs:43-86), whose
  * last-ulp behaviour differs between libms; through 64 layers of Q8_K requantisation a single ulp grows into a
@@ -10,7 +11,7 @@
  * value lies within ~1e-15 relative of a rounding boundary.
  *
  * exp:   x = k ln2 + r (Cody-Waite, ln2 split so k*LN2_HI is exact), |r| <= ln2/2, exp(r) by its Taylor series to
- *        degree 13 (truncation < 4e-18), times 2^k built from the exponent bits.
+ *        degree 13 (truncation < 4e-18) in fused Horner steps, times 2^k built from the exponent bits.
  * log1p: small arguments by the series u - u^2/2 + u^3/3; otherwise 1 + u is exact in double for an f32 u in
  *        (2^-29, 2^29), and log(1 + u) = k ln2 + 2 atanh((m - 1)/(m + 1)) with m in [sqrt(1/2), sqrt(2)).
  */
@@ -43,22 +44,22 @@ AQ_MATH_FN double aq_exp_d(double x) {
     if (x < -740.0) return 0.0;
     const double kd = __builtin_rint(x * AQ_INV_LN2);
     const int k = (int)kd;
-    const double r = (x - kd * AQ_LN2_HI) - kd * AQ_LN2_LO;
-    /* Horner, highest degree first: 1 + r(1 + r/2(1 + r/3(...))) as plain coefficients */
+    const double r = __builtin_fma(-kd, AQ_LN2_LO, __builtin_fma(-kd, AQ_LN2_HI, x));
+    /* Horner, highest degree first, one fused step per coefficient 1/n! */
     double p = 1.0 / 6227020800.0; /* 1/13! */
-    p = p * r + 1.0 / 479001600.0;
-    p = p * r + 1.0 / 39916800.0;
-    p = p * r + 1.0 / 3628800.0;
-    p = p * r + 1.0 / 362880.0;
-    p = p * r + 1.0 / 40320.0;
-    p = p * r + 1.0 / 5040.0;
-    p = p * r + 1.0 / 720.0;
-    p = p * r + 1.0 / 120.0;
-    p = p * r + 1.0 / 24.0;
-    p = p * r + 1.0 / 6.0;
-    p = p * r + 0.5;
-    p = p * r + 1.0;
-    p = p * r + 1.0;
+    p = __builtin_fma(p, r, 1.0 / 479001600.0);
+    p = __builtin_fma(p, r, 1.0 / 39916800.0);
+    p = __builtin_fma(p, r, 1.0 / 3628800.0);
+    p = __builtin_fma(p, r, 1.0 / 362880.0);
+    p = __builtin_fma(p, r, 1.0 / 40320.0);
+    p = __builtin_fma(p, r, 1.0 / 5040.0);
+    p = __builtin_fma(p, r, 1.0 / 720.0);
+    p = __builtin_fma(p, r, 1.0 / 120.0);
+    p = __builtin_fma(p, r, 1.0 / 24.0);
+    p = __builtin_fma(p, r, 1.0 / 6.0);
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
     if (k < -1000) return (p * aq_pow2i(k + 600)) * aq_pow2i(-600);
     if (k > 1000) return (p * aq_pow2i(k - 600)) * aq_pow2i(600);
     return p * aq_pow2i(k);
@@ -84,20 +85,20 @@ AQ_MATH_FN double aq_log_d(double v) {
     const double s = (m - 1.0) / (m + 1.0);
     const double s2 = s * s;
     double t = 1.0 / 23.0;
-    t = t * s2 + 1.0 / 21.0;
-    t = t * s2 + 1.0 / 19.0;
-    t = t * s2 + 1.0 / 17.0;
-    t = t * s2 + 1.0 / 15.0;
-    t = t * s2 + 1.0 / 13.0;
-    t = t * s2 + 1.0 / 11.0;
-    t = t * s2 + 1.0 / 9.0;
-    t = t * s2 + 1.0 / 7.0;
-    t = t * s2 + 1.0 / 5.0;
-    t = t * s2 + 1.0 / 3.0;
-    t = t * s2 + 1.0;
+    t = __builtin_fma(t, s2, 1.0 / 21.0);
+    t = __builtin_fma(t, s2, 1.0 / 19.0);
+    t = __builtin_fma(t, s2, 1.0 / 17.0);
+    t = __builtin_fma(t, s2, 1.0 / 15.0);
+    t = __builtin_fma(t, s2, 1.0 / 13.0);
+    t = __builtin_fma(t, s2, 1.0 / 11.0);
+    t = __builtin_fma(t, s2, 1.0 / 9.0);
+    t = __builtin_fma(t, s2, 1.0 / 7.0);
+    t = __builtin_fma(t, s2, 1.0 / 5.0);
+    t = __builtin_fma(t, s2, 1.0 / 3.0);
+    t = __builtin_fma(t, s2, 1.0);
     const double lm = 2.0 * s * t;
     const double kd = (double)k;
-    return (kd * AQ_LN2_HI + lm) + kd * AQ_LN2_LO;
+    return __builtin_fma(kd, AQ_LN2_LO, __builtin_fma(kd, AQ_LN2_HI, lm));
 }
 
 AQ_MATH_FN float aq_expf(float x) { return (float)aq_exp_d((double)x); }

@@ -84,6 +84,106 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float *x, size_t x_s
     }
 }
 
+// The same, for rows of float4s (the model's shapes), 512 threads: each thread keeps its float4s of x and w in
+// registers from the first load to the output; the squares go to LDS transposed (chain l's terms contiguous, so the
+// 8 chain lanes read them as float4s); with Q8_K output, wave w holds whole 256-blocks (its float4s are block
+// w + 8r, lane order), so the quantiser runs on registers.
+constexpr int RN_THREADS = 512, RN_ROUNDS = 8; // n <= 4 * 512 * 8
+
+__host__ __device__ inline int rn_chain_stride(int n) { // floats per chain row in LDS: 4 (mod 32), 16-byte rows
+    const int clen = n / 8;
+    return (clen + 31) / 32 * 32 + 4;
+}
+
+__global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x, size_t x_stride, const float *w,
+                                                                 float eps, int n, float *y, size_t y_stride, Act qa,
+                                                                 int kind, size_t col0, size_t eoff, int act_f32) {
+    extern __shared__ float sm[]; // 8 chains of squares, 16 floats, then (Q8_0 output only) the normalised row
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int n4 = n >> 2, n8 = n / 8 * 8, clen = n8 / 8, cs = rn_chain_stride(n);
+    float *sq = sm, *red = sm + 8 * cs, *xs = red + 16;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)row * x_stride);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float4 xv[RN_ROUNDS], wv[RN_ROUNDS];
+#pragma unroll
+    for (int r = 0; r < RN_ROUNDS; r++) {
+        const int i4 = tid + r * RN_THREADS;
+        if (i4 < n4) {
+            xv[r] = x4[i4];
+            wv[r] = w4[i4];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RN_ROUNDS; r++) {
+        const int i4 = tid + r * RN_THREADS;
+        if (i4 < n4) {
+            const float c[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int e = 4 * i4 + k;
+                if (e < n8) sq[(e & 7) * cs + (e >> 3)] = c[k] * c[k];
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < 8) { // chain tid: x[tid]^2 + x[tid + 8]^2 + ... in order, read a float4 at a time, 8 float4s ahead
+        const float *c = sq + tid * cs;
+        const float4 *c4 = reinterpret_cast<const float4 *>(c);
+        const int nq = clen / 4;
+        float acc = 0.0f;
+        if (nq > 0) {
+            float4 b[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) b[k] = c4[k < nq ? k : nq - 1];
+            for (int v0 = 0; v0 < nq; v0 += 8) {
+                float4 nb[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) nb[k] = c4[v0 + 8 + k < nq ? v0 + 8 + k : nq - 1];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    if (v0 + k < nq) {
+                        acc += b[k].x;
+                        acc += b[k].y;
+                        acc += b[k].z;
+                        acc += b[k].w;
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++) b[k] = nb[k];
+            }
+        }
+        for (int u = nq * 4; u < clen; u++) acc += c[u];
+        red[tid] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float ss = reduce8_f(red);
+        const float *xr = x + (size_t)row * x_stride;
+        for (int i = n8; i < n; i++) ss += xr[i] * xr[i];
+        const float mean = ss / (float)n;
+        red[8] = 1.0f / sqrtf(mean + eps);
+    }
+    __syncthreads();
+    const float inv = red[8];
+#pragma unroll
+    for (int r = 0; r < RN_ROUNDS; r++) {
+        const int i4 = tid + r * RN_THREADS;
+        if (i4 < n4) { // n4 is a multiple of 64 when the output is Q8_K: the condition is wave-uniform there
+            const float v[4] = {(xv[r].x * inv) * wv[r].x, (xv[r].y * inv) * wv[r].y, (xv[r].z * inv) * wv[r].z,
+                                (xv[r].w * inv) * wv[r].w};
+            const float4 v4 = make_float4(v[0], v[1], v[2], v[3]);
+            if (y) *reinterpret_cast<float4 *>(y + (size_t)row * y_stride + 4 * i4) = v4;
+            if (act_f32) *reinterpret_cast<float4 *>(qa.f32 + (col0 + row) * qa.n + eoff + 4 * i4) = v4;
+            if (kind == QK_Q8K) q8k_block_store(qa, col0 + row, eoff / 256 + (i4 >> 6), v, lane);
+            if (kind == QK_Q80) reinterpret_cast<float4 *>(xs)[i4] = v4;
+        }
+    }
+    if (kind == QK_Q80) {
+        __syncthreads();
+        for (int blk = tid; blk < n / 32; blk += RN_THREADS) q8_0_block_store(qa, col0 + row, eoff / 32 + blk, xs + blk * 32);
+    }
+}
+
 // --------------------------------------------------------------------------------------------------- swiglu
 // act.rs:24-30: h = silu(g) * u. Q8_K: one wave per 256-block; Q8_0 / none: one lane per 32-block.
 __global__ void __launch_bounds__(256) swiglu_q8k_kernel(const float *g, const float *u, size_t n, size_t total,
@@ -118,236 +218,278 @@ __global__ void __launch_bounds__(256) swiglu_q80_kernel(const float *g, const f
 }
 
 // ------------------------------------------------------------------------------------------ Gated DeltaNet
-// One work-group per V head p (K head p % nk, gated_deltanet.rs:172); thread j owns column j of the head's
-// state S[k][v] (row-major, dk x dv) in registers, and the conv windows of channels q_j, k_j, v_j.
-// Per row (gated_deltanet.rs:261-375, deltanet.rs:19-86, conv.rs:11-36):
+// One work-group of 256 threads per V head p (K head p % nk, gated_deltanet.rs:172). Per row
+// (gated_deltanet.rs:261-375, deltanet.rs:19-86, conv.rs:11-36):
 //   conv step + SiLU of the head's q/k/v channels; l2norm(q), l2norm(k) (eps 1e-6, sequential sums);
 //   q *= 1/sqrt(dk); g = ssm_a * softplus(a + dt_bias); beta = sigmoid(b);
 //   S *= exp(g); kv = sum_k S[k][v] k[k]; delta = (v - kv) beta; S[k][v] += k[k] delta; o = sum_k S[k][v] q[k];
 //   y = (w * (o * inv_rms(o))) * silu(z)  (rmsnorm.rs:37-46).
-// Each column's sums run in its own thread in the reference's order. The state is written back only when asked
-// (write_state); the conv windows go to conv_dst (a second buffer, so work-groups sharing a K head never read a
-// window another one has already advanced): v channels by every head, q/k channels by head p == kh.
-__device__ __forceinline__ float conv_step(float win[3], const float c[4], float x) {
-    float acc = 0.0f;
-    acc += c[0] * win[0];
-    acc += c[1] * win[1];
-    acc += c[2] * win[2];
-    acc += c[3] * x;
-    win[0] = win[1];
-    win[1] = win[2];
-    win[2] = x;
-    return silu_f(acc);
-}
-
+// Only the recurrence is sequential over rows, so everything else runs for all rows at once, each sum still in
+// one lane in the reference's order:
+//   A  every thread: conv + SiLU of whole channels over all rows, silu(z), and the 32-element alpha/beta partials
+//      (dot.rs:180-200); the state column of thread j (S[.][j], registers) is loaded meanwhile;
+//   B  wave 0: the 2t l2norm sums; wave 1: the 2t alpha/beta block chains, then the gates per row;
+//   C  thread j < dv: the recurrence of column j, row after row, with no barrier between rows;
+//   D  wave 0: the output RMS of each row (8 lanes of the reduce8 pattern per row); every thread: gated output.
+// The state is written back only when asked (write_state); the conv windows go to conv_dst (a second buffer, so
+// work-groups sharing a K head never read a window another one has already advanced): v channels by every head,
+// q/k channels by head p == kh.
 constexpr int DN_TMAX = 8;      // rows per DeltaNet launch
 constexpr int DN_BLK_MAX = 256; // 32-blocks of the alpha/beta rows (hidden <= 8192)
+constexpr int DN_THREADS = 512; // waves 0-3 hold state columns (dv <= 256); 4 and 5 run the per-row sums
 
 template <int DK, int DV>
-__global__ void __launch_bounds__(256) dn_core_kernel(DnArgs a) {
-    constexpr int NT = ((DK > DV ? DK : DV) + 63) / 64 * 64;
-    __shared__ float qn[DK], kn[DK], ob[DV], red[16];
-    __shared__ float in_q[DN_TMAX][DK], in_k[DN_TMAX][DK], in_v[DN_TMAX][DV], in_z[DN_TMAX][DV];
-    __shared__ float gab[2][DN_TMAX]; // per row: a (or g), b (or beta)
-    const int p = blockIdx.x, j = threadIdx.x;
+__global__ void __launch_bounds__(DN_THREADS) dn_core_kernel(DnArgs a) {
+    static_assert(DK <= 256 && DV <= 256 && DN_THREADS >= 384 && DN_TMAX * 8 <= 64, "DeltaNet work-group shape");
+    __shared__ float sq[DN_TMAX][DK], sk[DN_TMAX][DK], sv[DN_TMAX][DV], sz[DN_TMAX][DV], so[DN_TMAX][DV];
+    __shared__ float part[2][DN_TMAX][DN_BLK_MAX];
+    __shared__ float rdec[DN_TMAX], rbeta[DN_TMAX], rq[DN_TMAX], rk[DN_TMAX], ro[DN_TMAX];
+    const int p = blockIdx.x, j = threadIdx.x, lane = j & 63, wave = j >> 6;
     const int kh = p % a.nk, t = a.t;
     const int kd = a.nk * DK, vd = a.nv * DV, cd = 2 * kd + vd;
-    const bool has_qk = j < DK, has_v = j < DV;
-    const int jq = has_qk ? j : 0, jv = has_v ? j : 0; // in-range indices for the lanes past a head's width
-    const int chq = kh * DK + jq, chk = kd + kh * DK + jq, chv = 2 * kd + p * DV + jv;
+    const bool has_v = j < DV;
+    const bool gated = a.out && !a.raw;
 
-    // ---- every row's inputs to LDS up front (one round trip instead of one per row)
-    for (int i = 0; i < t; i++) {
-        if (a.raw) {
-            if (has_qk) {
-                in_q[i][j] = a.rq[(size_t)i * kd + kh * DK + j];
-                in_k[i][j] = a.rk[(size_t)i * kd + kh * DK + j];
-            }
-            if (has_v) in_v[i][j] = a.rv[(size_t)i * vd + p * DV + j];
-        } else {
-            const float *mrow = a.mixed + (size_t)i * cd;
-            if (has_qk) {
-                in_q[i][j] = mrow[chq];
-                in_k[i][j] = mrow[chk];
-            }
-            if (has_v) {
-                in_v[i][j] = mrow[chv];
-                if (a.z) in_z[i][j] = a.z[(size_t)i * vd + p * DV + j];
-            }
-        }
-    }
+    // ---- A: channels over all rows
     if (a.raw) {
-        if (j < t) {
-            gab[0][j] = a.rg[(size_t)j * a.nv + p];
-            gab[1][j] = a.rbeta[(size_t)j * a.nv + p];
+        for (int e = j; e < t * DK; e += DN_THREADS) {
+            const int i = e / DK, c = e % DK;
+            sq[i][c] = a.rq[(size_t)i * kd + kh * DK + c];
+            sk[i][c] = a.rk[(size_t)i * kd + kh * DK + c];
         }
-    } else if (!a.x) {
-        if (j < t) {
-            gab[0][j] = a.a[(size_t)j * a.nv + p];
-            gab[1][j] = a.b[(size_t)j * a.nv + p];
+        for (int e = j; e < t * DV; e += DN_THREADS) {
+            const int i = e / DV, c = e % DV;
+            sv[i][c] = a.rv[(size_t)i * vd + p * DV + c];
         }
     } else {
-        // gated_deltanet.rs:271-274 ssm_alpha / ssm_beta rows of this head on the t input rows, dot.rs:180-200:
-        // 32-element partials left to right (one thread per block and row), then the block chain (one thread per
-        // (row, input)), `acc + part` with the short tail (0.0f when there is none).
-        __shared__ float part[2][DN_TMAX][DN_BLK_MAX];
-        const int n = a.hidden, nblk = (n + 31) / 32;
-        for (int task = j; task < 2 * nblk; task += NT) {
-            const int r = task / nblk, b = task % nblk;
-            const float *w = (r == 0 ? a.w_alpha : a.w_beta) + (size_t)p * n;
-            const int e0 = b * 32, ne = n - e0 < 32 ? n - e0 : 32;
-            float wv[32];
-            if (ne == 32 && (n & 3) == 0) {
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const float4 f = *reinterpret_cast<const float4 *>(w + e0 + 4 * u);
-                    wv[4 * u] = f.x;
-                    wv[4 * u + 1] = f.y;
-                    wv[4 * u + 2] = f.z;
-                    wv[4 * u + 3] = f.w;
-                }
-                for (int i = 0; i < t; i++) {
-                    const float *xr = a.x + (size_t)i * a.x_stride + e0;
-                    float xv[32];
+        if (a.x) {
+            // gated_deltanet.rs:271-274 ssm_alpha / ssm_beta rows of this head on the t input rows: per 32-block a
+            // left-to-right partial for every row (four rows' chains interleaved)
+            const int n = a.hidden, nblk = (n + 31) / 32;
+            const bool vec = (n & 3) == 0 && (a.x_stride & 3) == 0;
+            for (int task = j; task < 2 * nblk; task += DN_THREADS) {
+                const int r = task / nblk, b = task % nblk;
+                const float *w = (r == 0 ? a.w_alpha : a.w_beta) + (size_t)p * n;
+                const int e0 = b * 32, ne = n - e0 < 32 ? n - e0 : 32;
+                if (ne == 32 && vec) {
+                    float wv[32];
 #pragma unroll
                     for (int u = 0; u < 8; u++) {
-                        const float4 f = *reinterpret_cast<const float4 *>(xr + 4 * u);
-                        xv[4 * u] = f.x;
-                        xv[4 * u + 1] = f.y;
-                        xv[4 * u + 2] = f.z;
-                        xv[4 * u + 3] = f.w;
+                        const float4 f = *reinterpret_cast<const float4 *>(w + e0 + 4 * u);
+                        wv[4 * u] = f.x, wv[4 * u + 1] = f.y, wv[4 * u + 2] = f.z, wv[4 * u + 3] = f.w;
                     }
-                    float pt = 0.0f;
+                    for (int i0 = 0; i0 < t; i0 += 4) {
+                        float xv[4][32];
 #pragma unroll
-                    for (int e = 0; e < 32; e++) pt += wv[e] * xv[e];
-                    part[r][i][b] = pt;
-                }
-            } else {
-                for (int i = 0; i < t; i++) {
-                    const float *xr = a.x + (size_t)i * a.x_stride + e0;
-                    float pt = 0.0f;
-                    for (int e = 0; e < ne; e++) pt += w[e0 + e] * xr[e];
-                    part[r][i][b] = pt;
+                        for (int q = 0; q < 4; q++) {
+                            const int i = i0 + q < t ? i0 + q : t - 1;
+                            const float *xr = a.x + (size_t)i * a.x_stride + e0;
+#pragma unroll
+                            for (int u = 0; u < 8; u++) {
+                                const float4 f = *reinterpret_cast<const float4 *>(xr + 4 * u);
+                                xv[q][4 * u] = f.x, xv[q][4 * u + 1] = f.y, xv[q][4 * u + 2] = f.z,
+                                          xv[q][4 * u + 3] = f.w;
+                            }
+                        }
+                        float pt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int e = 0; e < 32; e++)
+#pragma unroll
+                            for (int q = 0; q < 4; q++) pt[q] += wv[e] * xv[q][e];
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+                            if (i0 + q < t) part[r][i0 + q][b] = pt[q];
+                    }
+                } else {
+                    for (int i = 0; i < t; i++) {
+                        const float *xr = a.x + (size_t)i * a.x_stride + e0;
+                        float pt = 0.0f;
+                        for (int e = 0; e < ne; e++) pt += w[e0 + e] * xr[e];
+                        part[r][i][b] = pt;
+                    }
                 }
             }
         }
-        __syncthreads();
-        if (j < 2 * t) {
-            const int r = j / t, i = j % t;
-            float v = seq_sum<false>(&part[r][i][0], 0, nblk, 1, 0.0f);
-            if (n % 32 == 0) v = v + 0.0f;
-            gab[r][i] = v;
-            (r == 0 ? a.a : a.b)[(size_t)i * a.nv + p] = v; // kept for the commit
-        }
-    }
-
-    // ---- state and conv windows
-    float wq[3] = {0, 0, 0}, wk[3] = {0, 0, 0}, wv[3] = {0, 0, 0};
-    float cq[4] = {0, 0, 0, 0}, ck[4] = {0, 0, 0, 0}, cv[4] = {0, 0, 0, 0};
-    if (!a.raw) {
-        for (int e = 0; e < 3; e++) {
-            wq[e] = a.conv_src[(size_t)chq * 3 + e];
-            wk[e] = a.conv_src[(size_t)chk * 3 + e];
-            wv[e] = a.conv_src[(size_t)chv * 3 + e];
-        }
-        for (int e = 0; e < 4; e++) {
-            cq[e] = a.conv_w[(size_t)chq * 4 + e];
-            ck[e] = a.conv_w[(size_t)chk * 4 + e];
-            cv[e] = a.conv_w[(size_t)chv * 4 + e];
-        }
-    }
-    float s[DK];
-    float *srec = a.rec + (size_t)p * DK * DV;
+        // task c: q channel c (c < DK), k channel c - DK, v channel c - 2 DK (conv, conv.rs:11-36), then the
+        // z channels (silu only)
+        const int n_conv = 2 * DK + DV, n_task = n_conv + (gated ? DV : 0);
+        for (int c = j; c < n_task; c += DN_THREADS) {
+            if (c < n_conv) {
+                const int kind = c < DK ? 0 : c < 2 * DK ? 1 : 2;
+                const int cc = kind == 2 ? c - 2 * DK : c - kind * DK;
+                const int ch = kind == 0 ? kh * DK + cc : kind == 1 ? kd + kh * DK + cc : 2 * kd + p * DV + cc;
+                float seq[DN_TMAX + 3];
 #pragma unroll
-    for (int k = 0; k < DK; k++) s[k] = srec[(size_t)k * DV + jv];
-    const float big_a = a.raw ? 0.0f : a.ssm_a[p], dtb = a.raw ? 0.0f : a.dt_bias[p];
-    const int tk = NT > 64 ? 64 : 1; // the k-norm chain runs in another wave when there is one
+                for (int e = 0; e < 3; e++) seq[e] = a.conv_src[(size_t)ch * 3 + e];
+                float cw[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) cw[e] = a.conv_w[(size_t)ch * 4 + e];
+#pragma unroll
+                for (int i = 0; i < DN_TMAX; i++) seq[3 + i] = a.mixed[(size_t)(i < t ? i : t - 1) * cd + ch];
+                float *dst = kind == 0 ? &sq[0][cc] : kind == 1 ? &sk[0][cc] : &sv[0][cc];
+                const int dstride = kind == 2 ? DV : DK;
+#pragma unroll
+                for (int i = 0; i < DN_TMAX; i++) {
+                    if (i < t) {
+                        float acc = 0.0f;
+                        acc += cw[0] * seq[i];
+                        acc += cw[1] * seq[i + 1];
+                        acc += cw[2] * seq[i + 2];
+                        acc += cw[3] * seq[i + 3];
+                        dst[i * dstride] = silu_f(acc);
+                    }
+                }
+                if (a.conv_dst && (kind == 2 || p == kh)) {
+#pragma unroll
+                    for (int i = 0; i <= DN_TMAX; i++) // the window after row t - 1: seq[t .. t + 2]
+                        if (i == t)
+                            for (int e = 0; e < 3; e++) a.conv_dst[(size_t)ch * 3 + e] = seq[i + e];
+                }
+            } else {
+                const int cc = c - n_conv;
+                float zr[DN_TMAX];
+#pragma unroll
+                for (int i = 0; i < DN_TMAX; i++) zr[i] = a.z[(size_t)(i < t ? i : t - 1) * vd + p * DV + cc];
+#pragma unroll
+                for (int i = 0; i < DN_TMAX; i++)
+                    if (i < t) sz[i][cc] = silu_f(zr[i]);
+            }
+        }
+    }
     __syncthreads();
 
-    for (int i = 0; i < t; i++) {
-        float vval = 0.0f;
+    // ---- B: norms (wave 4) and gates (wave 5), one sum per lane
+    if (wave == 4 && !a.raw && lane < 2 * t) {
+        const int i = lane >> 1;
+        const float ss = seq_sum<true>((lane & 1) ? sk[i] : sq[i], 0, DK, 1, 0.0f);
+        const float inv = 1.0f / sqrtf(ss + 1e-6f); // deltanet.rs:19-29 l2norm
+        if (lane & 1)
+            rk[i] = inv;
+        else
+            rq[i] = inv;
+    }
+    if (wave == 5 && lane < 2 * t) {
+        const int r = lane / t, i = lane % t;
+        float v;
         if (a.raw) {
-            if (has_qk) {
-                qn[j] = in_q[i][j];
-                kn[j] = in_k[i][j];
-            }
-            if (has_v) vval = in_v[i][j];
+            v = (r == 0 ? a.rg : a.rbeta)[(size_t)i * a.nv + p];
+        } else if (a.x) {
+            // dot.rs:180-200: the block chain, `acc + part` with the short tail (0.0f when there is none)
+            const int n = a.hidden, nblk = (n + 31) / 32;
+            v = seq_sum<false>(&part[r][i][0], 0, nblk, 1, 0.0f);
+            if (n % 32 == 0) v = v + 0.0f;
+            (r == 0 ? a.a : a.b)[(size_t)i * a.nv + p] = v; // kept for the commit
         } else {
-            if (has_qk) {
-                qn[j] = conv_step(wq, cq, in_q[i][j]);
-                kn[j] = conv_step(wk, ck, in_k[i][j]);
-            }
-            if (has_v) vval = conv_step(wv, cv, in_v[i][j]);
+            v = (r == 0 ? a.a : a.b)[(size_t)i * a.nv + p];
+        }
+        if (r == 0) {
+            const float g = a.raw ? v : a.ssm_a[p] * softplus_f(v + a.dt_bias[p]); // deltanet.rs:32-35 gate_g
+            rdec[i] = exp_f(g);
+        } else {
+            rbeta[i] = a.raw ? v : sigmoid_f(v);
+        }
+    }
+    // ---- the state column (waves 0-3, which skip the sums above: the loads fly while waves 4 and 5 work; placed
+    // after the sums so the column's registers are not live inside them)
+    float s[DK];
+    float *srec = a.rec + (size_t)p * DK * DV;
+    if (has_v) {
+#pragma unroll
+        for (int k = 0; k < DK; k++) s[k] = srec[(size_t)k * DV + j];
+    }
+    __syncthreads();
+    if (!a.raw) {
+        for (int e = j; e < t * DK; e += DN_THREADS) {
+            const int i = e / DK, c = e % DK;
+            sq[i][c] = (sq[i][c] * rq[i]) * a.qscale;
+            sk[i][c] = sk[i][c] * rk[i];
         }
         __syncthreads();
-        float g, beta;
-        if (a.raw) {
-            g = gab[0][i];
-            beta = gab[1][i];
-        } else {
-            if (j == 0 || j == tk) { // deltanet.rs:19-29 l2norm, eps 1e-6
-                const float ss = seq_sum<true>(j == 0 ? qn : kn, 0, DK, 1, 0.0f);
-                red[j == 0 ? 0 : 1] = 1.0f / sqrtf(ss + 1e-6f);
-            }
-            __syncthreads();
-            if (has_qk) {
-                const float qv = qn[j] * red[0];
-                qn[j] = qv * a.qscale;
-                kn[j] = kn[j] * red[1];
-            }
-            __syncthreads();
-            g = big_a * softplus_f(gab[0][i] + dtb); // deltanet.rs:32-35 gate_g
-            beta = sigmoid_f(gab[1][i]);
-        }
-        float ov = 0.0f;
-        { // deltanet.rs:43-86, column j of the head's state
-            const float decay = exp_f(g);
-#pragma unroll
-            for (int k = 0; k < DK; k++) s[k] *= decay;
+    }
+
+    // ---- C: the recurrence of column j (deltanet.rs:43-86). S *= decay and the kv sum share one pass over k,
+    // the update and the o sum another; each pass reads k (and q) from LDS a chunk of 32 at a time, all reads of a
+    // chunk issued before its first use.
+    if (has_v) {
+        constexpr int CH = DK < 32 ? DK : 32, NCH = DK / CH;    // pass 1 chunk (k)
+        constexpr int CH2 = DK < 16 ? DK : 16, NCH2 = DK / CH2; // pass 2 chunk (k and q)
+        static_assert(DK % CH == 0 && CH % 4 == 0 && DK % CH2 == 0 && CH2 % 4 == 0, "DeltaNet key width");
+        for (int i = 0; i < t; i++) {
+            const float decay = rdec[i], beta = rbeta[i], vval = sv[i][j];
+            const float4 *k4 = reinterpret_cast<const float4 *>(sk[i]), *q4 = reinterpret_cast<const float4 *>(sq[i]);
             float kv = 0.0f;
 #pragma unroll
-            for (int k = 0; k < DK; k++) kv += s[k] * kn[k];
+            for (int c = 0; c < NCH; c++) {
+                float4 kb[CH / 4];
+#pragma unroll
+                for (int u = 0; u < CH / 4; u++) kb[u] = k4[c * (CH / 4) + u];
+#pragma unroll
+                for (int u = 0; u < CH / 4; u++) {
+                    const float kk[4] = {kb[u].x, kb[u].y, kb[u].z, kb[u].w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int k = c * CH + 4 * u + e;
+                        s[k] *= decay;
+                        kv += s[k] * kk[e];
+                    }
+                }
+            }
             const float delta = (vval - kv) * beta;
+            float ov = 0.0f;
+            // k is read again rather than kept: holding it next to S leaves no registers for reading ahead
+            __asm__ volatile("" ::: "memory");
 #pragma unroll
-            for (int k = 0; k < DK; k++) s[k] += kn[k] * delta;
+            for (int c = 0; c < NCH2; c++) {
+                float4 kb[CH2 / 4], qb[CH2 / 4];
 #pragma unroll
-            for (int k = 0; k < DK; k++) ov += s[k] * qn[k];
-        }
-        if (a.out) {
+                for (int u = 0; u < CH2 / 4; u++) {
+                    kb[u] = k4[c * (CH2 / 4) + u];
+                    qb[u] = q4[c * (CH2 / 4) + u];
+                }
+#pragma unroll
+                for (int u = 0; u < CH2 / 4; u++) {
+                    const float kk[4] = {kb[u].x, kb[u].y, kb[u].z, kb[u].w};
+                    const float qq[4] = {qb[u].x, qb[u].y, qb[u].z, qb[u].w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int k = c * CH2 + 4 * u + e;
+                        s[k] += kk[e] * delta;
+                        ov += s[k] * qq[e];
+                    }
+                }
+            }
             if (a.raw) {
-                if (has_v) a.out[(size_t)i * vd + p * DV + j] = ov;
+                if (a.out) a.out[(size_t)i * vd + p * DV + j] = ov;
             } else {
-                if (has_v) ob[j] = ov;
-                __syncthreads();
-                constexpr int n8 = DV / 8 * 8;
-                if (j < 8) red[4 + j] = seq_sum<true>(ob, j, n8, 8, 0.0f);
-                __syncthreads();
-                if (j == 0) {
-                    float ss = reduce8_f(red + 4);
-                    for (int e = n8; e < DV; e++) ss += ob[e] * ob[e];
-                    red[2] = 1.0f / sqrtf(ss / (float)DV + a.eps);
-                }
-                __syncthreads();
-                if (has_v) {
-                    const size_t o = (size_t)i * vd + p * DV + j;
-                    a.out[o] = (a.ssm_norm[j] * (ov * red[2])) * silu_f(in_z[i][j]);
-                }
+                so[i][j] = ov;
             }
         }
-        __syncthreads(); // qn, kn, ob, red are rewritten by the next row
-    }
-    if (a.write_state && has_v) {
+        if (a.write_state) {
 #pragma unroll
-        for (int k = 0; k < DK; k++) srec[(size_t)k * DV + j] = s[k];
+            for (int k = 0; k < DK; k++) srec[(size_t)k * DV + j] = s[k];
+        }
     }
-    if (a.conv_dst && !a.raw) {
-        if (has_v)
-            for (int e = 0; e < 3; e++) a.conv_dst[(size_t)chv * 3 + e] = wv[e];
-        if (has_qk && p == kh)
-            for (int e = 0; e < 3; e++) {
-                a.conv_dst[(size_t)chq * 3 + e] = wq[e];
-                a.conv_dst[(size_t)chk * 3 + e] = wk[e];
+
+    // ---- D: gated RMSNorm of each output row
+    if (gated) {
+        __syncthreads();
+        if (wave == 0) {
+            constexpr int n8 = DV / 8 * 8;
+            const int i = lane >> 3, m = lane & 7;
+            const float part8 = i < t ? seq_sum<true>(so[i < t ? i : 0], m, n8, 8, 0.0f) : 0.0f;
+            float l8[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) l8[u] = __shfl(part8, (lane & ~7) + u);
+            if (m == 0 && i < t) {
+                float ss = reduce8_f(l8);
+                for (int e = n8; e < DV; e++) ss += so[i][e] * so[i][e];
+                ro[i] = 1.0f / sqrtf(ss / (float)DV + a.eps);
             }
+        }
+        __syncthreads();
+        if (has_v)
+            for (int i = 0; i < t; i++)
+                a.out[(size_t)i * vd + p * DV + j] = (a.ssm_norm[j] * (so[i][j] * ro[i])) * sz[i][j];
     }
 }
 
@@ -604,6 +746,17 @@ int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, s
     } else {
         AQ_REQUIRE(q.kind == QK_NONE && !q.f32, "rmsnorm: quantised output without a buffer");
     }
+    const auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    const bool vec = n % 4 == 0 && n <= 4 * RN_THREADS * RN_ROUNDS && x_stride % 4 == 0 && al16(x) && al16(w) &&
+                     (!y_f32 || (y_stride % 4 == 0 && al16(y_f32))) &&
+                     (!q.f32 || (act.n % 4 == 0 && q.elem_off % 4 == 0 && al16(act.f32)));
+    const size_t vshmem = ((size_t)8 * rn_chain_stride((int)n) + 16 + (q.kind == QK_Q80 ? n : 0)) * sizeof(float);
+    if (vec && vshmem <= 65536) {
+        const size_t shmem = vshmem;
+        hipLaunchKernelGGL(rmsnorm_vec_kernel, dim3((unsigned)t), dim3(RN_THREADS), shmem, stream, x, x_stride, w, eps,
+                           (int)n, y_f32, y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0);
+        return launched("rmsnorm");
+    }
     const size_t shmem = (2 * n + 16) * sizeof(float);
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)t), dim3(256), shmem, stream, x, x_stride, w, eps, (int)n, y_f32,
                        y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0);
@@ -648,7 +801,7 @@ int launch_dn_core(const DnArgs &a, hipStream_t stream) {
     AQ_REQUIRE(a.raw || a.x || (a.a && a.b), "deltanet: gate inputs");
     AQ_REQUIRE(!a.x || (a.w_alpha && a.w_beta && a.a && a.b && a.hidden > 0 && a.hidden <= 32 * DN_BLK_MAX),
                "deltanet: alpha/beta projection");
-    const int threads = ((a.dk > a.dv ? a.dk : a.dv) + 63) / 64 * 64;
+    const int threads = DN_THREADS;
     const int key = a.dk * 1000 + a.dv;
     switch (key) {
 #define AQ_DN(K, V)                                                                                           \
