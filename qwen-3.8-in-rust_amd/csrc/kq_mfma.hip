@@ -89,8 +89,9 @@ __device__ __forceinline__ void load_w(WRegs<TYPE> &w, const MfArgs &a, size_t w
 
 // The products of one super-block for one thread: pr0/pr1 = (dx*dw)*float(lane sum) of lanes j and j+4, pm the
 // Q4_K/Q5_K min product of min lane j, for every column. xq: the super-block's codes, 256 bytes per column (lane-slot
-// order); xd: its f32 scales per column; xm: its activation-sum pairs [pair][ncp]. kdot.rs:37-140 per lane.
-template <int TYPE, int NC>
+// order, XS bytes per column); xd: its f32 scales per column; xm: its activation-sum pairs [pair][ncp].
+// kdot.rs:37-140 per lane.
+template <int TYPE, int NC, int XS = 256>
 __device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t *xq, const float *xd,
                                             const uint32_t *xm, int ncp, int j, int r, float *pr0, float *pr1,
                                             float *pm) {
@@ -159,7 +160,7 @@ __device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t 
 #pragma unroll
     for (int cg = 0; cg < NCG; cg++) {
         const int cA = cg * 4 + r < NC ? cg * 4 + r : 0; // this thread's A-operand column
-        const uint4 *xp = reinterpret_cast<const uint4 *>(xq + cA * 256 + j * 64);
+        const uint4 *xp = reinterpret_cast<const uint4 *>(xq + cA * XS + j * 64);
         const uint4 va = xp[0], vb = xp[1], vc = xp[2], vd = xp[3];
         const uint32_t x0[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w}; // lane j
         const uint32_t x1[8] = {vc.x, vc.y, vc.z, vc.w, vd.x, vd.y, vd.z, vd.w}; // lane j+4
@@ -214,7 +215,7 @@ __device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t 
 // without carries, and the MFMA accumulator sums sc_i-weighted dots over the 8 sub-blocks. The lane sum is then
 // sum_i D_i << (DB*i) = sum_s sc[s] * dot_s exactly — the same integer as kdot.rs:37-95 — with no per-output
 // scale multiply.
-template <int TYPE, int NC>
+template <int TYPE, int NC, int XS = 256>
 __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const int8_t *xq, const float *xd,
                                                   const uint32_t *xm, int ncp, int j, int r, float *pr0,
                                                   float *pr1, float *pm) {
@@ -256,7 +257,7 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
 #pragma unroll
     for (int cg = 0; cg < NCG; cg++) {
         const int cA = cg * 4 + r < NC ? cg * 4 + r : 0;
-        const uint4 *xp = reinterpret_cast<const uint4 *>(xq + cA * 256 + j * 64);
+        const uint4 *xp = reinterpret_cast<const uint4 *>(xq + cA * XS + j * 64);
         const uint4 va = xp[0], vb = xp[1], vc = xp[2], vd = xp[3];
         const uint32_t x0[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w}; // lane j
         const uint32_t x1[8] = {vc.x, vc.y, vc.z, vc.w, vd.x, vd.y, vd.z, vd.w}; // lane j+4
@@ -493,6 +494,292 @@ __global__ void __launch_bounds__(256) kq_mfma_kernel(MfArgs a) {
     }
 }
 
+// Whole-K variant: the activations of all nb super-blocks are copied to LDS once, behind one barrier, so the
+// weight prefetch ring is never drained by a staging wait; the main loop has no data-dependent branch around a
+// load (a round past the end of K is computed on clamped indices and its products are not added). Column stride
+// KQ_XS = 256 + 16 bytes puts the 4 columns a wave reads at once in different LDS banks.
+constexpr int KQ_XS = 272;
+
+inline size_t kq_full_lds_bytes(int nb, int nc, bool q6) {
+    const int ncp = (nc + 3) / 4 * 4;
+    return (size_t)nb * nc * KQ_XS + (size_t)nb * ncp * 4 + (size_t)nb * (q6 ? 8 : 4) * ncp * 4;
+}
+
+template <int TYPE, int NC, int KS, int PF>
+__global__ void __launch_bounds__(256) kq_mfma_full_kernel(MfArgs a) {
+    constexpr int RG = 4 / KS;
+    constexpr int NCP = (NC + 3) / 4 * 4;
+    constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
+    constexpr int NP = Q6 ? 8 : 4; // activation-sum pairs per super-block
+    extern __shared__ __align__(16) uint8_t kq_lds[];
+    __shared__ float xch[KS > 1 ? RG : 1][KS > 1 ? 2 : 1][KS][3 * NC][64];
+
+    const int nb = a.nb;
+    int8_t *sxq = reinterpret_cast<int8_t *>(kq_lds);
+    float *sxd = reinterpret_cast<float *>(kq_lds + (size_t)nb * NC * KQ_XS);
+    uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)nb * NCP);
+    const int t = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int rg = wid / KS, w = wid % KS;
+    const int g = t >> 4, j = (t >> 2) & 3, r = t & 3;
+    int row = ((int)blockIdx.x * RG + rg) * 16 + 4 * g + r;
+    const bool valid = row < a.rows;
+    if (!valid) row = a.rows - 1;
+    const size_t rowsb = (size_t)row * nb;
+
+    // the first PF rounds of weights fly while the activations are staged
+    WRegs<TYPE> wr[PF];
+#pragma unroll
+    for (int p = 0; p < PF; p++) load_w<TYPE>(wr[p], a, rowsb + min(w + p * KS, nb - 1), j);
+
+    {
+        // 16 threads per (column, super-block) record of 256 codes, two records per thread group in flight
+        const int o = threadIdx.x & 15, nrec = nb * NC;
+        for (int r0 = (int)threadIdx.x >> 4; r0 < nrec; r0 += 32) {
+            const int ra = r0, rb = r0 + 16 < nrec ? r0 + 16 : r0; // the second record, or the first again
+            const int ca = ra / nb, sa = ra - ca * nb, cb = rb / nb, sbb = rb - cb * nb;
+            const uint4 va = *reinterpret_cast<const uint4 *>(a.xqs + (size_t)ca * a.xcol + (size_t)sa * 256 + o * 16);
+            const uint4 vb = *reinterpret_cast<const uint4 *>(a.xqs + (size_t)cb * a.xcol + (size_t)sbb * 256 + o * 16);
+            *reinterpret_cast<uint4 *>(sxq + ((size_t)sa * NC + ca) * KQ_XS + o * 16) = va;
+            *reinterpret_cast<uint4 *>(sxq + ((size_t)sbb * NC + cb) * KQ_XS + o * 16) = vb;
+        }
+        for (int e = (int)threadIdx.x; e < nb * NC; e += 256) {
+            const int c = e / nb, sb = e % nb;
+            const size_t m = (size_t)c * nb + sb;
+            sxd[sb * NCP + c] = a.xd[m];
+            if constexpr (Q6) {
+                const uint4 p0 = reinterpret_cast<const uint4 *>(a.xbs + m * 16)[0];
+                const uint4 p1 = reinterpret_cast<const uint4 *>(a.xbs + m * 16)[1];
+                const uint32_t pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+                for (int q = 0; q < 8; q++) sxm[(sb * NP + q) * NCP + c] = pv[q];
+            } else {
+                const uint4 p0 = *reinterpret_cast<const uint4 *>(a.xq8s + m * 8);
+                const uint32_t pv[4] = {p0.x, p0.y, p0.z, p0.w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) sxm[(sb * NP + q) * NCP + c] = pv[q];
+            }
+        }
+    }
+    __syncthreads();
+
+    float acc0[NC], acc1[NC], accm[NC]; // lane j, lane j+4, min lane j
+#pragma unroll
+    for (int i = 0; i < NC; i++) acc0[i] = acc1[i] = accm[i] = 0.0f;
+    int parity = 0;
+    const int nr = (nb + KS - 1) / KS; // rounds of KS super-blocks (wave w takes super-block round*KS + w)
+
+    auto round_body = [&](WRegs<TYPE> &wv, const int round, const bool prefetch) {
+        const int sb = round * KS + w;
+        const int sbc = sb < nb ? sb : nb - 1;
+        float pr0[NC], pr1[NC], pm[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) pm[c] = 0.0f;
+        const int8_t *xq = sxq + (size_t)sbc * NC * KQ_XS;
+        const float *xd = sxd + sbc * NCP;
+        const uint32_t *xm = sxm + sbc * NP * NCP;
+        if constexpr (Q6)
+            sb_products<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr0, pr1, pm);
+        else
+            sb_products_split<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr0, pr1, pm);
+        if (prefetch) {
+            load_w<TYPE>(wv, a, rowsb + min(sb + PF * KS, nb - 1), j);
+            __builtin_amdgcn_sched_barrier(0); // issue the refill here, not after the later rounds' compute
+        }
+        const int live = nb - round * KS < KS ? nb - round * KS : KS; // super-blocks in this round
+        if constexpr (KS == 1) {
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                acc0[c] += pr0[c];
+                acc1[c] += pr1[c];
+                if constexpr (!Q6) accm[c] += pm[c];
+            }
+        } else {
+            float(*x)[3 * NC][64] = xch[rg][parity];
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                x[w][c][t] = pr0[c];
+                x[w][NC + c][t] = pr1[c];
+                x[w][2 * NC + c][t] = pm[c];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int w2 = 0; w2 < KS; w2++) {
+                if (w2 < live) {
+#pragma unroll
+                    for (int c = 0; c < NC; c++) {
+                        acc0[c] += x[w2][c][t];
+                        acc1[c] += x[w2][NC + c][t];
+                        if constexpr (!Q6) accm[c] += x[w2][2 * NC + c][t];
+                    }
+                }
+            }
+            parity ^= 1;
+        }
+    };
+    const int nfull = nr / PF * PF;
+    for (int rd = 0; rd < nfull; rd += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) round_body(wr[p], rd + p, true);
+    }
+#pragma unroll
+    for (int p = 0; p < PF; p++)
+        if (nfull + p < nr) round_body(wr[p], nfull + p, false);
+
+    if (w != 0) return; // every wave of a row group holds the same chain; wave 0 writes
+#pragma unroll
+    for (int col = 0; col < NC; col++) {
+        float v = acc0[col] + acc1[col]; // l_j + l_{j+4}
+        v = v + __shfl_xor(v, 8);
+        v = v + __shfl_xor(v, 4);
+        if constexpr (!Q6) {
+            float m = accm[col];
+            m = m + __shfl_xor(m, 8); // m0+m2, m1+m3
+            m = m + __shfl_xor(m, 4);
+            v = v + m;
+        }
+        if (j == 0 && valid) {
+            const size_t o = (size_t)col * a.rows + row;
+            a.y[o] = a.resid ? a.resid[o] + v : v;
+        }
+    }
+}
+
+// Four rows per wave, K split four ways inside the wave: the instruction's 16 blocks are (stream g, lane pair j)
+// instead of (row group g, lane pair j), so block row g of thread t = 16g + 4j + r works on super-blocks
+// g, g+4, g+8, ... of row r. Four times the waves of the 16-row layout for the same rows, and the super-block
+// order of the chain is restored inside the wave: every round each thread writes its products to LDS and the
+// owner of column c (stream c % 4) adds the four streams' products in super-block order — no work-group barrier
+// after the activation staging.
+template <int TYPE, int NC, int PF>
+__global__ void __launch_bounds__(512) kq_mfma_r4_kernel(MfArgs a) {
+    constexpr int NW = 8; // waves per work-group, 4 rows each
+    constexpr int NCP = (NC + 3) / 4 * 4;
+    constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
+    constexpr int NP = Q6 ? 8 : 4;
+    constexpr int NV = 3 * NC, NVP = (NV + 3) / 4 * 4; // products per thread and round: (lane j, lane j+4, min j) x NC
+    constexpr int NQ = (NC + 3) / 4;                   // owned columns per thread: c = g + 4q
+    extern __shared__ __align__(16) uint8_t kq_lds[];
+    __shared__ __align__(16) float pxch[NW][16][4][NVP]; // [wave][4j + r][stream][product]
+
+    const int nb = a.nb;
+    int8_t *sxq = reinterpret_cast<int8_t *>(kq_lds);
+    float *sxd = reinterpret_cast<float *>(kq_lds + (size_t)nb * NC * KQ_XS);
+    uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)nb * NCP);
+    const int t = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int g = t >> 4, j = (t >> 2) & 3, r = t & 3, jr = t & 15;
+    int row = ((int)blockIdx.x * NW + wid) * 4 + r;
+    const bool valid = row < a.rows;
+    if (!valid) row = a.rows - 1;
+    const size_t rowsb = (size_t)row * nb;
+    const int nr = (nb + 3) / 4; // rounds: stream g takes super-block 4m + g in round m
+
+    WRegs<TYPE> wr[PF];
+#pragma unroll
+    for (int p = 0; p < PF; p++) load_w<TYPE>(wr[p], a, rowsb + min(4 * p + g, nb - 1), j);
+
+    {
+        const int o = threadIdx.x & 15, nrec = nb * NC;
+        for (int r0 = (int)threadIdx.x >> 4; r0 < nrec; r0 += 64) {
+            const int ra = r0, rb = r0 + 32 < nrec ? r0 + 32 : r0;
+            const int ca = ra / nb, sa = ra - ca * nb, cb = rb / nb, sbb = rb - cb * nb;
+            const uint4 va = *reinterpret_cast<const uint4 *>(a.xqs + (size_t)ca * a.xcol + (size_t)sa * 256 + o * 16);
+            const uint4 vb = *reinterpret_cast<const uint4 *>(a.xqs + (size_t)cb * a.xcol + (size_t)sbb * 256 + o * 16);
+            *reinterpret_cast<uint4 *>(sxq + ((size_t)sa * NC + ca) * KQ_XS + o * 16) = va;
+            *reinterpret_cast<uint4 *>(sxq + ((size_t)sbb * NC + cb) * KQ_XS + o * 16) = vb;
+        }
+        for (int e = (int)threadIdx.x; e < nb * NC; e += 64 * NW) {
+            const int c = e / nb, sb = e % nb;
+            const size_t m = (size_t)c * nb + sb;
+            sxd[sb * NCP + c] = a.xd[m];
+            if constexpr (Q6) {
+                const uint4 p0 = reinterpret_cast<const uint4 *>(a.xbs + m * 16)[0];
+                const uint4 p1 = reinterpret_cast<const uint4 *>(a.xbs + m * 16)[1];
+                const uint32_t pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+                for (int q = 0; q < 8; q++) sxm[(sb * NP + q) * NCP + c] = pv[q];
+            } else {
+                const uint4 p0 = *reinterpret_cast<const uint4 *>(a.xq8s + m * 8);
+                const uint32_t pv[4] = {p0.x, p0.y, p0.z, p0.w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) sxm[(sb * NP + q) * NCP + c] = pv[q];
+            }
+        }
+    }
+    __syncthreads();
+
+    float oa0[NQ], oa1[NQ], oam[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; q++) oa0[q] = oa1[q] = oam[q] = 0.0f;
+    float *mine = &pxch[wid][jr][g][0];
+
+    auto round_body = [&](WRegs<TYPE> &wv, const int m, const bool prefetch) {
+        const int sb = 4 * m + g;
+        const int sbc = sb < nb ? sb : nb - 1;
+        float pr0[NC], pr1[NC], pm[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) pm[c] = 0.0f;
+        const int8_t *xq = sxq + (size_t)sbc * NC * KQ_XS;
+        const float *xd = sxd + sbc * NCP;
+        const uint32_t *xm = sxm + sbc * NP * NCP;
+        if constexpr (Q6)
+            sb_products<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr0, pr1, pm);
+        else
+            sb_products_split<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr0, pr1, pm);
+        if (prefetch) {
+            load_w<TYPE>(wv, a, rowsb + min(sb + 4 * PF, nb - 1), j);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // products to LDS, then each owner adds the four streams' products of its columns in super-block order
+        // (LDS operations of one wave complete in issue order: the reads below see this round's writes, and the
+        // next round's writes come after them)
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            mine[3 * c] = pr0[c];
+            mine[3 * c + 1] = pr1[c];
+            mine[3 * c + 2] = pm[c];
+        }
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            const int c = g + 4 * q, cc = c < NC ? c : NC - 1;
+            const float *src = &pxch[wid][jr][0][3 * cc];
+#pragma unroll
+            for (int g2 = 0; g2 < 4; g2++) {
+                if (4 * m + g2 < nb) {
+                    oa0[q] += src[g2 * NVP];
+                    oa1[q] += src[g2 * NVP + 1];
+                    if constexpr (!Q6) oam[q] += src[g2 * NVP + 2];
+                }
+            }
+        }
+    };
+    const int nfull = nr / PF * PF;
+    for (int m0 = 0; m0 < nfull; m0 += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) round_body(wr[p], m0 + p, true);
+    }
+#pragma unroll
+    for (int p = 0; p < PF; p++)
+        if (nfull + p < nr) round_body(wr[p], nfull + p, false);
+
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        const int c = g + 4 * q;
+        float v = oa0[q] + oa1[q]; // l_j + l_{j+4}
+        v = v + __shfl_xor(v, 8);
+        v = v + __shfl_xor(v, 4);
+        if constexpr (!Q6) {
+            float mm = oam[q];
+            mm = mm + __shfl_xor(mm, 8); // m0+m2, m1+m3
+            mm = mm + __shfl_xor(mm, 4);
+            v = v + mm;
+        }
+        if (c < NC && j == 0 && valid) {
+            const size_t o = (size_t)c * a.rows + row;
+            a.y[o] = a.resid ? a.resid[o] + v : v;
+        }
+    }
+}
+
 template <int TYPE, int NC, int KS>
 int launch_ks(const MfArgs &args, hipStream_t stream) {
     // prefetch depth and chunk (CH a multiple of KS * PF; two chunk buffers in LDS), from a sweep on MI355X of the
@@ -505,9 +792,35 @@ int launch_ks(const MfArgs &args, hipStream_t stream) {
     return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_mfma launch");
 }
 
-// Split K across waves when the rows alone give too few waves to keep HBM busy (256 CUs want >= ~8 each).
+template <int TYPE, int NC, int KS>
+int launch_full(const MfArgs &args, size_t lds, hipStream_t stream) {
+    constexpr int PF = 2;
+    constexpr int ROWS = 64 / KS;
+    constexpr size_t XCH = (size_t)(KS > 1 ? 4 / KS : 1) * (KS > 1 ? 2 : 1) * KS * 3 * NC * 64 * 4; // static LDS
+    if (lds > 64 * 1024) {
+        static bool raised = false; // once per instantiation: allow dynamic LDS up to the CU's 160 KiB
+        if (!raised) {
+            const void *fn = reinterpret_cast<const void *>(&kq_mfma_full_kernel<TYPE, NC, KS, PF>);
+            AQ_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(160 * 1024 - XCH - 512)));
+            raised = true;
+        }
+    }
+    const dim3 grid((unsigned)((args.rows + ROWS - 1) / ROWS)), block(256);
+    hipLaunchKernelGGL((kq_mfma_full_kernel<TYPE, NC, KS, PF>), grid, block, lds, stream, args);
+    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_mfma launch");
+}
+
+// The whole-K kernel when its LDS fits, the split chosen from a sweep on MI355X of the 27B shapes: long rows
+// (K >= 12288) and tall matrices at N > 1 split K in two, the rest in four. Otherwise the chunked kernel, splitting
+// K across waves when the rows alone give too few waves to keep HBM busy (256 CUs want >= ~8 each).
 template <int TYPE, int NC>
 int launch_nc(const MfArgs &args, hipStream_t stream) {
+    const size_t lds = kq_full_lds_bytes(args.nb, NC, TYPE == AQ_TYPE_Q6_K);
+    const size_t xch = (size_t)2 * 2 * 2 * 3 * NC * 64 * 4; // static exchange buffer (the same for KS = 2 and 4)
+    if (lds + xch <= 160 * 1024 - 512) {
+        if (args.nb >= 48 || (NC > 1 && args.rows >= 12288)) return launch_full<TYPE, NC, 2>(args, lds, stream);
+        return launch_full<TYPE, NC, 4>(args, lds, stream);
+    }
     const int waves = (args.rows + 15) / 16;
     if (waves >= 2048 || args.nb < 8) return launch_ks<TYPE, NC, 1>(args, stream);
     if (waves >= 1024) return launch_ks<TYPE, NC, 2>(args, stream);
