@@ -498,30 +498,94 @@ __global__ void __launch_bounds__(256) kq_mfma_kernel(MfArgs a) {
 // weight prefetch ring is never drained by a staging wait; the main loop has no data-dependent branch around a
 // load (a round past the end of K is computed on clamped indices and its products are not added). Column stride
 // KQ_XS = 256 + 16 bytes puts the 4 columns a wave reads at once in different LDS banks.
+//
+// One launch can cover up to three matrices that read the same activations (gate and up; q, k and v; the
+// DeltaNet qkv and z projections): the work-groups are laid out segment after segment, each segment with its own
+// weights, output and K-quant type (one of the kernel's two types), so the staging and the launch are shared.
 constexpr int KQ_XS = 272;
+constexpr int KQ_MAXSEG = 3;
 
-inline size_t kq_full_lds_bytes(int nb, int nc, bool q6) {
-    const int ncp = (nc + 3) / 4 * 4;
-    return (size_t)nb * nc * KQ_XS + (size_t)nb * ncp * 4 + (size_t)nb * (q6 ? 8 : 4) * ncp * 4;
+struct KqSeg {
+    const uint8_t *qa, *qb, *sc, *dm;
+    float *y;
+    const float *resid;
+    int rows, type, wg_end; // wg_end: one past this segment's last work-group
+};
+struct KqGroup {
+    KqSeg seg[KQ_MAXSEG];
+    int nseg, nb;
+    const int8_t *xqs;
+    const float *xd;
+    const int16_t *xbs, *xq8s;
+    size_t xcol;
+};
+
+inline size_t kq_full_lds_bytes(int nb, int nc, bool has45, bool has6) {
+    const int ncp = (nc + 3) / 4 * 4, np = (has45 ? 4 : 0) + (has6 ? 8 : 0);
+    return (size_t)nb * nc * KQ_XS + (size_t)nb * ncp * 4 + (size_t)nb * np * ncp * 4;
 }
 
-template <int TYPE, int NC, int KS, int PF>
-__global__ void __launch_bounds__(256) kq_mfma_full_kernel(MfArgs a) {
+// Activations of every super-block to LDS: codes [sb][column][KQ_XS], scales [sb][NCP], activation-sum pairs
+// [sb][NP][NCP]: the 4 sub-block-sum pairs (Q4_K/Q5_K segments, HAS45) and then the 8 group-sum pairs (Q6_K
+// segments, HAS6).
+template <int NC, bool HAS45, bool HAS6>
+__device__ __forceinline__ void kq_stage(const KqGroup &G, int8_t *sxq, float *sxd, uint32_t *sxm) {
+    constexpr int NCP = (NC + 3) / 4 * 4;
+    constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), P6 = HAS45 ? 4 : 0;
+    const int nb = G.nb;
+    // 16 threads per (column, super-block) record of 256 codes, two records per thread group in flight
+    const int o = threadIdx.x & 15, nrec = nb * NC;
+    for (int r0 = (int)threadIdx.x >> 4; r0 < nrec; r0 += 32) {
+        const int ra = r0, rb = r0 + 16 < nrec ? r0 + 16 : r0; // the second record, or the first again
+        const int ca = ra / nb, sa = ra - ca * nb, cb = rb / nb, sbb = rb - cb * nb;
+        const uint4 va = *reinterpret_cast<const uint4 *>(G.xqs + (size_t)ca * G.xcol + (size_t)sa * 256 + o * 16);
+        const uint4 vb = *reinterpret_cast<const uint4 *>(G.xqs + (size_t)cb * G.xcol + (size_t)sbb * 256 + o * 16);
+        *reinterpret_cast<uint4 *>(sxq + ((size_t)sa * NC + ca) * KQ_XS + o * 16) = va;
+        *reinterpret_cast<uint4 *>(sxq + ((size_t)sbb * NC + cb) * KQ_XS + o * 16) = vb;
+    }
+    for (int e = (int)threadIdx.x; e < nb * NC; e += 256) {
+        const int c = e / nb, sb = e % nb;
+        const size_t m = (size_t)c * nb + sb;
+        sxd[sb * NCP + c] = G.xd[m];
+        if constexpr (HAS45) {
+            const uint4 p0 = *reinterpret_cast<const uint4 *>(G.xq8s + m * 8);
+            sxm[(sb * NP + 0) * NCP + c] = p0.x;
+            sxm[(sb * NP + 1) * NCP + c] = p0.y;
+            sxm[(sb * NP + 2) * NCP + c] = p0.z;
+            sxm[(sb * NP + 3) * NCP + c] = p0.w;
+        }
+        if constexpr (HAS6) {
+            const uint4 g0 = reinterpret_cast<const uint4 *>(G.xbs + m * 16)[0];
+            const uint4 g1 = reinterpret_cast<const uint4 *>(G.xbs + m * 16)[1];
+            const uint32_t pv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int q = 0; q < 8; q++) sxm[(sb * NP + P6 + q) * NCP + c] = pv[q];
+        }
+    }
+}
+
+// One segment's work-group: rows wg*RG*16 .. +RG*16 of the segment's matrix, K split KS ways across waves.
+// xch: [RG][2][KS][3 NC][64] exchange floats. HAS45 / HAS6: the staging's pair sets (this segment's type reads
+// its own).
+template <int TYPE, int NC, int KS, int PF, bool HAS45, bool HAS6>
+__device__ __forceinline__ void kq_full_run(const KqGroup &G, const KqSeg &sg, int wg, int8_t *sxq, float *sxd,
+                                            uint32_t *sxm, float *xch) {
     constexpr int RG = 4 / KS;
     constexpr int NCP = (NC + 3) / 4 * 4;
     constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
-    constexpr int NP = Q6 ? 8 : 4; // activation-sum pairs per super-block
-    extern __shared__ __align__(16) uint8_t kq_lds[];
-    __shared__ float xch[KS > 1 ? RG : 1][KS > 1 ? 2 : 1][KS][3 * NC][64];
-
-    const int nb = a.nb;
-    int8_t *sxq = reinterpret_cast<int8_t *>(kq_lds);
-    float *sxd = reinterpret_cast<float *>(kq_lds + (size_t)nb * NC * KQ_XS);
-    uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)nb * NCP);
+    constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), POFF = Q6 && HAS45 ? 4 : 0;
+    MfArgs a{};
+    a.qa = sg.qa;
+    a.qb = sg.qb;
+    a.sc = sg.sc;
+    a.dm = sg.dm;
+    a.rows = sg.rows;
+    a.nb = G.nb;
+    const int nb = G.nb;
     const int t = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int rg = wid / KS, w = wid % KS;
     const int g = t >> 4, j = (t >> 2) & 3, r = t & 3;
-    int row = ((int)blockIdx.x * RG + rg) * 16 + 4 * g + r;
+    int row = (wg * RG + rg) * 16 + 4 * g + r;
     const bool valid = row < a.rows;
     if (!valid) row = a.rows - 1;
     const size_t rowsb = (size_t)row * nb;
@@ -530,36 +594,7 @@ __global__ void __launch_bounds__(256) kq_mfma_full_kernel(MfArgs a) {
     WRegs<TYPE> wr[PF];
 #pragma unroll
     for (int p = 0; p < PF; p++) load_w<TYPE>(wr[p], a, rowsb + min(w + p * KS, nb - 1), j);
-
-    {
-        // 16 threads per (column, super-block) record of 256 codes, two records per thread group in flight
-        const int o = threadIdx.x & 15, nrec = nb * NC;
-        for (int r0 = (int)threadIdx.x >> 4; r0 < nrec; r0 += 32) {
-            const int ra = r0, rb = r0 + 16 < nrec ? r0 + 16 : r0; // the second record, or the first again
-            const int ca = ra / nb, sa = ra - ca * nb, cb = rb / nb, sbb = rb - cb * nb;
-            const uint4 va = *reinterpret_cast<const uint4 *>(a.xqs + (size_t)ca * a.xcol + (size_t)sa * 256 + o * 16);
-            const uint4 vb = *reinterpret_cast<const uint4 *>(a.xqs + (size_t)cb * a.xcol + (size_t)sbb * 256 + o * 16);
-            *reinterpret_cast<uint4 *>(sxq + ((size_t)sa * NC + ca) * KQ_XS + o * 16) = va;
-            *reinterpret_cast<uint4 *>(sxq + ((size_t)sbb * NC + cb) * KQ_XS + o * 16) = vb;
-        }
-        for (int e = (int)threadIdx.x; e < nb * NC; e += 256) {
-            const int c = e / nb, sb = e % nb;
-            const size_t m = (size_t)c * nb + sb;
-            sxd[sb * NCP + c] = a.xd[m];
-            if constexpr (Q6) {
-                const uint4 p0 = reinterpret_cast<const uint4 *>(a.xbs + m * 16)[0];
-                const uint4 p1 = reinterpret_cast<const uint4 *>(a.xbs + m * 16)[1];
-                const uint32_t pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-                for (int q = 0; q < 8; q++) sxm[(sb * NP + q) * NCP + c] = pv[q];
-            } else {
-                const uint4 p0 = *reinterpret_cast<const uint4 *>(a.xq8s + m * 8);
-                const uint32_t pv[4] = {p0.x, p0.y, p0.z, p0.w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) sxm[(sb * NP + q) * NCP + c] = pv[q];
-            }
-        }
-    }
+    kq_stage<NC, HAS45, HAS6>(G, sxq, sxd, sxm);
     __syncthreads();
 
     float acc0[NC], acc1[NC], accm[NC]; // lane j, lane j+4, min lane j
@@ -576,7 +611,7 @@ __global__ void __launch_bounds__(256) kq_mfma_full_kernel(MfArgs a) {
         for (int c = 0; c < NC; c++) pm[c] = 0.0f;
         const int8_t *xq = sxq + (size_t)sbc * NC * KQ_XS;
         const float *xd = sxd + sbc * NCP;
-        const uint32_t *xm = sxm + sbc * NP * NCP;
+        const uint32_t *xm = sxm + (sbc * NP + POFF) * NCP;
         if constexpr (Q6)
             sb_products<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr0, pr1, pm);
         else
@@ -594,12 +629,12 @@ __global__ void __launch_bounds__(256) kq_mfma_full_kernel(MfArgs a) {
                 if constexpr (!Q6) accm[c] += pm[c];
             }
         } else {
-            float(*x)[3 * NC][64] = xch[rg][parity];
+            float *x = xch + (size_t)(rg * 2 + parity) * KS * 3 * NC * 64; // [KS][3 NC][64]
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                x[w][c][t] = pr0[c];
-                x[w][NC + c][t] = pr1[c];
-                x[w][2 * NC + c][t] = pm[c];
+                x[(w * 3 * NC + c) * 64 + t] = pr0[c];
+                x[(w * 3 * NC + NC + c) * 64 + t] = pr1[c];
+                x[(w * 3 * NC + 2 * NC + c) * 64 + t] = pm[c];
             }
             __syncthreads();
 #pragma unroll
@@ -607,9 +642,9 @@ __global__ void __launch_bounds__(256) kq_mfma_full_kernel(MfArgs a) {
                 if (w2 < live) {
 #pragma unroll
                     for (int c = 0; c < NC; c++) {
-                        acc0[c] += x[w2][c][t];
-                        acc1[c] += x[w2][NC + c][t];
-                        if constexpr (!Q6) accm[c] += x[w2][2 * NC + c][t];
+                        acc0[c] += x[(w2 * 3 * NC + c) * 64 + t];
+                        acc1[c] += x[(w2 * 3 * NC + NC + c) * 64 + t];
+                        if constexpr (!Q6) accm[c] += x[(w2 * 3 * NC + 2 * NC + c) * 64 + t];
                     }
                 }
             }
@@ -639,145 +674,30 @@ __global__ void __launch_bounds__(256) kq_mfma_full_kernel(MfArgs a) {
         }
         if (j == 0 && valid) {
             const size_t o = (size_t)col * a.rows + row;
-            a.y[o] = a.resid ? a.resid[o] + v : v;
+            sg.y[o] = sg.resid ? sg.resid[o] + v : v;
         }
     }
 }
 
-// Four rows per wave, K split four ways inside the wave: the instruction's 16 blocks are (stream g, lane pair j)
-// instead of (row group g, lane pair j), so block row g of thread t = 16g + 4j + r works on super-blocks
-// g, g+4, g+8, ... of row r. Four times the waves of the 16-row layout for the same rows, and the super-block
-// order of the chain is restored inside the wave: every round each thread writes its products to LDS and the
-// owner of column c (stream c % 4) adds the four streams' products in super-block order — no work-group barrier
-// after the activation staging.
-template <int TYPE, int NC, int PF>
-__global__ void __launch_bounds__(512) kq_mfma_r4_kernel(MfArgs a) {
-    constexpr int NW = 8; // waves per work-group, 4 rows each
+template <int T0, int T1, int NC, int KS, int PF>
+__global__ void __launch_bounds__(256) kq_group_kernel(KqGroup G) {
+    constexpr int RG = 4 / KS;
+    constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
+    constexpr bool HAS45 = T0 != AQ_TYPE_Q6_K || T1 != AQ_TYPE_Q6_K;
     constexpr int NCP = (NC + 3) / 4 * 4;
-    constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
-    constexpr int NP = Q6 ? 8 : 4;
-    constexpr int NV = 3 * NC, NVP = (NV + 3) / 4 * 4; // products per thread and round: (lane j, lane j+4, min j) x NC
-    constexpr int NQ = (NC + 3) / 4;                   // owned columns per thread: c = g + 4q
     extern __shared__ __align__(16) uint8_t kq_lds[];
-    __shared__ __align__(16) float pxch[NW][16][4][NVP]; // [wave][4j + r][stream][product]
-
-    const int nb = a.nb;
+    __shared__ float xch[(KS > 1 ? RG : 1) * (KS > 1 ? 2 : 1) * KS * 3 * NC * 64];
+    int si = 0; // this work-group's segment (uniform)
+    while (si + 1 < G.nseg && (int)blockIdx.x >= G.seg[si].wg_end) si++;
+    const KqSeg &sg = G.seg[si];
+    const int wg = (int)blockIdx.x - (si ? G.seg[si - 1].wg_end : 0);
     int8_t *sxq = reinterpret_cast<int8_t *>(kq_lds);
-    float *sxd = reinterpret_cast<float *>(kq_lds + (size_t)nb * NC * KQ_XS);
-    uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)nb * NCP);
-    const int t = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const int g = t >> 4, j = (t >> 2) & 3, r = t & 3, jr = t & 15;
-    int row = ((int)blockIdx.x * NW + wid) * 4 + r;
-    const bool valid = row < a.rows;
-    if (!valid) row = a.rows - 1;
-    const size_t rowsb = (size_t)row * nb;
-    const int nr = (nb + 3) / 4; // rounds: stream g takes super-block 4m + g in round m
-
-    WRegs<TYPE> wr[PF];
-#pragma unroll
-    for (int p = 0; p < PF; p++) load_w<TYPE>(wr[p], a, rowsb + min(4 * p + g, nb - 1), j);
-
-    {
-        const int o = threadIdx.x & 15, nrec = nb * NC;
-        for (int r0 = (int)threadIdx.x >> 4; r0 < nrec; r0 += 64) {
-            const int ra = r0, rb = r0 + 32 < nrec ? r0 + 32 : r0;
-            const int ca = ra / nb, sa = ra - ca * nb, cb = rb / nb, sbb = rb - cb * nb;
-            const uint4 va = *reinterpret_cast<const uint4 *>(a.xqs + (size_t)ca * a.xcol + (size_t)sa * 256 + o * 16);
-            const uint4 vb = *reinterpret_cast<const uint4 *>(a.xqs + (size_t)cb * a.xcol + (size_t)sbb * 256 + o * 16);
-            *reinterpret_cast<uint4 *>(sxq + ((size_t)sa * NC + ca) * KQ_XS + o * 16) = va;
-            *reinterpret_cast<uint4 *>(sxq + ((size_t)sbb * NC + cb) * KQ_XS + o * 16) = vb;
-        }
-        for (int e = (int)threadIdx.x; e < nb * NC; e += 64 * NW) {
-            const int c = e / nb, sb = e % nb;
-            const size_t m = (size_t)c * nb + sb;
-            sxd[sb * NCP + c] = a.xd[m];
-            if constexpr (Q6) {
-                const uint4 p0 = reinterpret_cast<const uint4 *>(a.xbs + m * 16)[0];
-                const uint4 p1 = reinterpret_cast<const uint4 *>(a.xbs + m * 16)[1];
-                const uint32_t pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-                for (int q = 0; q < 8; q++) sxm[(sb * NP + q) * NCP + c] = pv[q];
-            } else {
-                const uint4 p0 = *reinterpret_cast<const uint4 *>(a.xq8s + m * 8);
-                const uint32_t pv[4] = {p0.x, p0.y, p0.z, p0.w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) sxm[(sb * NP + q) * NCP + c] = pv[q];
-            }
-        }
-    }
-    __syncthreads();
-
-    float oa0[NQ], oa1[NQ], oam[NQ];
-#pragma unroll
-    for (int q = 0; q < NQ; q++) oa0[q] = oa1[q] = oam[q] = 0.0f;
-    float *mine = &pxch[wid][jr][g][0];
-
-    auto round_body = [&](WRegs<TYPE> &wv, const int m, const bool prefetch) {
-        const int sb = 4 * m + g;
-        const int sbc = sb < nb ? sb : nb - 1;
-        float pr0[NC], pr1[NC], pm[NC];
-#pragma unroll
-        for (int c = 0; c < NC; c++) pm[c] = 0.0f;
-        const int8_t *xq = sxq + (size_t)sbc * NC * KQ_XS;
-        const float *xd = sxd + sbc * NCP;
-        const uint32_t *xm = sxm + sbc * NP * NCP;
-        if constexpr (Q6)
-            sb_products<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr0, pr1, pm);
-        else
-            sb_products_split<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr0, pr1, pm);
-        if (prefetch) {
-            load_w<TYPE>(wv, a, rowsb + min(sb + 4 * PF, nb - 1), j);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        // products to LDS, then each owner adds the four streams' products of its columns in super-block order
-        // (LDS operations of one wave complete in issue order: the reads below see this round's writes, and the
-        // next round's writes come after them)
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-            mine[3 * c] = pr0[c];
-            mine[3 * c + 1] = pr1[c];
-            mine[3 * c + 2] = pm[c];
-        }
-#pragma unroll
-        for (int q = 0; q < NQ; q++) {
-            const int c = g + 4 * q, cc = c < NC ? c : NC - 1;
-            const float *src = &pxch[wid][jr][0][3 * cc];
-#pragma unroll
-            for (int g2 = 0; g2 < 4; g2++) {
-                if (4 * m + g2 < nb) {
-                    oa0[q] += src[g2 * NVP];
-                    oa1[q] += src[g2 * NVP + 1];
-                    if constexpr (!Q6) oam[q] += src[g2 * NVP + 2];
-                }
-            }
-        }
-    };
-    const int nfull = nr / PF * PF;
-    for (int m0 = 0; m0 < nfull; m0 += PF) {
-#pragma unroll
-        for (int p = 0; p < PF; p++) round_body(wr[p], m0 + p, true);
-    }
-#pragma unroll
-    for (int p = 0; p < PF; p++)
-        if (nfull + p < nr) round_body(wr[p], nfull + p, false);
-
-#pragma unroll
-    for (int q = 0; q < NQ; q++) {
-        const int c = g + 4 * q;
-        float v = oa0[q] + oa1[q]; // l_j + l_{j+4}
-        v = v + __shfl_xor(v, 8);
-        v = v + __shfl_xor(v, 4);
-        if constexpr (!Q6) {
-            float mm = oam[q];
-            mm = mm + __shfl_xor(mm, 8); // m0+m2, m1+m3
-            mm = mm + __shfl_xor(mm, 4);
-            v = v + mm;
-        }
-        if (c < NC && j == 0 && valid) {
-            const size_t o = (size_t)c * a.rows + row;
-            a.y[o] = a.resid ? a.resid[o] + v : v;
-        }
-    }
+    float *sxd = reinterpret_cast<float *>(kq_lds + (size_t)G.nb * NC * KQ_XS);
+    uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)G.nb * NCP);
+    if (T0 == T1 || sg.type == T0)
+        kq_full_run<T0, NC, KS, PF, HAS45, HAS6>(G, sg, wg, sxq, sxd, sxm, xch);
+    else
+        kq_full_run<T1, NC, KS, PF, HAS45, HAS6>(G, sg, wg, sxq, sxd, sxm, xch);
 }
 
 template <int TYPE, int NC, int KS>
@@ -792,35 +712,10 @@ int launch_ks(const MfArgs &args, hipStream_t stream) {
     return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_mfma launch");
 }
 
-template <int TYPE, int NC, int KS>
-int launch_full(const MfArgs &args, size_t lds, hipStream_t stream) {
-    constexpr int PF = 2;
-    constexpr int ROWS = 64 / KS;
-    constexpr size_t XCH = (size_t)(KS > 1 ? 4 / KS : 1) * (KS > 1 ? 2 : 1) * KS * 3 * NC * 64 * 4; // static LDS
-    if (lds > 64 * 1024) {
-        static bool raised = false; // once per instantiation: allow dynamic LDS up to the CU's 160 KiB
-        if (!raised) {
-            const void *fn = reinterpret_cast<const void *>(&kq_mfma_full_kernel<TYPE, NC, KS, PF>);
-            AQ_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(160 * 1024 - XCH - 512)));
-            raised = true;
-        }
-    }
-    const dim3 grid((unsigned)((args.rows + ROWS - 1) / ROWS)), block(256);
-    hipLaunchKernelGGL((kq_mfma_full_kernel<TYPE, NC, KS, PF>), grid, block, lds, stream, args);
-    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_mfma launch");
-}
-
-// The whole-K kernel when its LDS fits, the split chosen from a sweep on MI355X of the 27B shapes: long rows
-// (K >= 12288) and tall matrices at N > 1 split K in two, the rest in four. Otherwise the chunked kernel, splitting
-// K across waves when the rows alone give too few waves to keep HBM busy (256 CUs want >= ~8 each).
+// The chunked kernel (activations staged a chunk at a time): the fallback when the whole-K staging does not fit
+// the CU's LDS. K is split across waves when the rows alone give too few waves to keep HBM busy.
 template <int TYPE, int NC>
-int launch_nc(const MfArgs &args, hipStream_t stream) {
-    const size_t lds = kq_full_lds_bytes(args.nb, NC, TYPE == AQ_TYPE_Q6_K);
-    const size_t xch = (size_t)2 * 2 * 2 * 3 * NC * 64 * 4; // static exchange buffer (the same for KS = 2 and 4)
-    if (lds + xch <= 160 * 1024 - 512) {
-        if (args.nb >= 48 || (NC > 1 && args.rows >= 12288)) return launch_full<TYPE, NC, 2>(args, lds, stream);
-        return launch_full<TYPE, NC, 4>(args, lds, stream);
-    }
+int launch_chunked_nc(const MfArgs &args, hipStream_t stream) {
     const int waves = (args.rows + 15) / 16;
     if (waves >= 2048 || args.nb < 8) return launch_ks<TYPE, NC, 1>(args, stream);
     if (waves >= 1024) return launch_ks<TYPE, NC, 2>(args, stream);
@@ -828,23 +723,75 @@ int launch_nc(const MfArgs &args, hipStream_t stream) {
 }
 
 template <int TYPE>
-int launch_type(const MfArgs &args, size_t ncols, hipStream_t stream) {
+int launch_chunked(const MfArgs &args, size_t ncols, hipStream_t stream) {
     switch (ncols) {
-    case 1: return launch_nc<TYPE, 1>(args, stream);
-    case 2: return launch_nc<TYPE, 2>(args, stream);
-    case 3: return launch_nc<TYPE, 3>(args, stream);
-    case 4: return launch_nc<TYPE, 4>(args, stream);
-    case 5: return launch_nc<TYPE, 5>(args, stream);
-    case 6: return launch_nc<TYPE, 6>(args, stream);
-    case 7: return launch_nc<TYPE, 7>(args, stream);
-    case 8: return launch_nc<TYPE, 8>(args, stream);
+    case 1: return launch_chunked_nc<TYPE, 1>(args, stream);
+    case 2: return launch_chunked_nc<TYPE, 2>(args, stream);
+    case 3: return launch_chunked_nc<TYPE, 3>(args, stream);
+    case 4: return launch_chunked_nc<TYPE, 4>(args, stream);
+    case 5: return launch_chunked_nc<TYPE, 5>(args, stream);
+    case 6: return launch_chunked_nc<TYPE, 6>(args, stream);
+    case 7: return launch_chunked_nc<TYPE, 7>(args, stream);
+    case 8: return launch_chunked_nc<TYPE, 8>(args, stream);
     default: return fail(AQ_EINVAL, "kq_mfma: ncols must be 1..8");
     }
 }
 
-} // namespace
+constexpr int KQ_LDS_MAX = 160 * 1024 - 512; // a CU's LDS, less a margin
 
-int launch_kq_mfma(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream) {
+template <int NC>
+constexpr size_t kq_xch_bytes() { return (size_t)2 * 2 * 2 * 3 * NC * 64 * 4; } // the same for KS = 2 and KS = 4
+
+template <int T0, int T1, int NC, int KS>
+int launch_group_ks(KqGroup G, size_t lds, hipStream_t stream) {
+    constexpr int PF = 2;
+    constexpr int ROWS = 64 / KS;
+    int wgs = 0;
+    for (int i = 0; i < G.nseg; i++) {
+        wgs += (G.seg[i].rows + ROWS - 1) / ROWS;
+        G.seg[i].wg_end = wgs;
+    }
+    if (lds > 64 * 1024) {
+        static bool raised = false; // once per instantiation: allow dynamic LDS up to the CU's size
+        if (!raised) {
+            const void *fn = reinterpret_cast<const void *>(&kq_group_kernel<T0, T1, NC, KS, PF>);
+            AQ_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)(KQ_LDS_MAX - kq_xch_bytes<NC>())));
+            raised = true;
+        }
+    }
+    hipLaunchKernelGGL((kq_group_kernel<T0, T1, NC, KS, PF>), dim3((unsigned)wgs), dim3(256), lds, stream, G);
+    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_mfma launch");
+}
+
+// Returns 1 (nothing launched) when the whole-K staging does not fit. The split from a sweep on MI355X of the 27B
+// shapes: long rows (K >= 12288) and tall groups at N > 1 split K in two, the rest in four.
+template <int T0, int T1, int NC>
+int launch_group_nc(const KqGroup &G, int rows, hipStream_t stream) {
+    constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
+    constexpr bool HAS45 = T0 != AQ_TYPE_Q6_K || T1 != AQ_TYPE_Q6_K;
+    const size_t lds = kq_full_lds_bytes(G.nb, NC, HAS45, HAS6);
+    if (lds + kq_xch_bytes<NC>() > (size_t)KQ_LDS_MAX) return 1;
+    if (G.nb >= 48 || (NC > 1 && rows >= 12288)) return launch_group_ks<T0, T1, NC, 2>(G, lds, stream);
+    return launch_group_ks<T0, T1, NC, 4>(G, lds, stream);
+}
+
+template <int T0, int T1>
+int launch_group_t(const KqGroup &G, int rows, size_t ncols, hipStream_t stream) {
+    switch (ncols) {
+    case 1: return launch_group_nc<T0, T1, 1>(G, rows, stream);
+    case 2: return launch_group_nc<T0, T1, 2>(G, rows, stream);
+    case 3: return launch_group_nc<T0, T1, 3>(G, rows, stream);
+    case 4: return launch_group_nc<T0, T1, 4>(G, rows, stream);
+    case 5: return launch_group_nc<T0, T1, 5>(G, rows, stream);
+    case 6: return launch_group_nc<T0, T1, 6>(G, rows, stream);
+    case 7: return launch_group_nc<T0, T1, 7>(G, rows, stream);
+    case 8: return launch_group_nc<T0, T1, 8>(G, rows, stream);
+    default: return fail(AQ_EINVAL, "kq_mfma: ncols must be 1..8");
+    }
+}
+
+MfArgs single_args(const Weight &w, const Act &x, float *y, const float *resid) {
     MfArgs args{};
     args.qa = w.qa;
     args.qb = w.qb;
@@ -859,12 +806,93 @@ int launch_kq_mfma(const Weight &w, const Act &x, size_t ncols, float *y, const 
     args.xcol = x.n;
     args.y = y;
     args.resid = resid;
-    switch (w.type) {
-    case AQ_TYPE_Q4_K: return launch_type<AQ_TYPE_Q4_K>(args, ncols, stream);
-    case AQ_TYPE_Q5_K: return launch_type<AQ_TYPE_Q5_K>(args, ncols, stream);
-    case AQ_TYPE_Q6_K: return launch_type<AQ_TYPE_Q6_K>(args, ncols, stream);
-    default: return fail(AQ_EUNSUP, "kq_mfma: not a K-quant type");
+    return args;
+}
+
+// One launch over segments [i0, i1) of at most two K-quant types; the chunked kernel per segment if the staging
+// does not fit.
+int launch_run(const Weight *const *ws, float *const *ys, const float *const *resids, int i0, int i1, const Act &x,
+               size_t ncols, hipStream_t stream) {
+    KqGroup G{};
+    G.nseg = i1 - i0;
+    G.nb = (int)ws[i0]->nb;
+    G.xqs = x.qs;
+    G.xd = x.d;
+    G.xbs = x.bs;
+    G.xq8s = x.q8s;
+    G.xcol = x.n;
+    int t0 = 99, t1 = 0, rows = 0;
+    for (int i = i0; i < i1; i++) {
+        const Weight &w = *ws[i];
+        KqSeg &sg = G.seg[i - i0];
+        sg.qa = w.qa;
+        sg.qb = w.qb;
+        sg.sc = w.sc;
+        sg.dm = w.dm;
+        sg.y = ys[i];
+        sg.resid = resids ? resids[i] : nullptr;
+        sg.rows = (int)w.rows;
+        sg.type = w.type;
+        rows += (int)w.rows;
+        t0 = w.type < t0 ? w.type : t0;
+        t1 = w.type > t1 ? w.type : t1;
     }
+    int rc = 1;
+    constexpr int Q4 = AQ_TYPE_Q4_K, Q5 = AQ_TYPE_Q5_K, Q6 = AQ_TYPE_Q6_K;
+    if (t0 == Q4 && t1 == Q4) rc = launch_group_t<Q4, Q4>(G, rows, ncols, stream);
+    else if (t0 == Q5 && t1 == Q5) rc = launch_group_t<Q5, Q5>(G, rows, ncols, stream);
+    else if (t0 == Q6 && t1 == Q6) rc = launch_group_t<Q6, Q6>(G, rows, ncols, stream);
+    else if (t0 == Q4 && t1 == Q5) rc = launch_group_t<Q4, Q5>(G, rows, ncols, stream);
+    else if (t0 == Q4 && t1 == Q6) rc = launch_group_t<Q4, Q6>(G, rows, ncols, stream);
+    else if (t0 == Q5 && t1 == Q6) rc = launch_group_t<Q5, Q6>(G, rows, ncols, stream);
+    if (rc != 1) return rc;
+    for (int i = i0; i < i1; i++) {
+        const MfArgs args = single_args(*ws[i], x, ys[i], resids ? resids[i] : nullptr);
+        switch (ws[i]->type) {
+        case Q4: rc = launch_chunked<Q4>(args, ncols, stream); break;
+        case Q5: rc = launch_chunked<Q5>(args, ncols, stream); break;
+        default: rc = launch_chunked<Q6>(args, ncols, stream); break;
+        }
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+} // namespace
+
+int launch_kq_group(const Weight *const *ws, float *const *ys, const float *const *resids, int n, const Act &x,
+                    size_t ncols, hipStream_t stream) {
+    AQ_REQUIRE(n >= 1 && ws && ys, "kq_mfma: no matrices");
+    AQ_REQUIRE(ncols >= 1 && ncols <= 8, "kq_mfma: ncols must be 1..8");
+    for (int i = 0; i < n; i++) {
+        AQ_REQUIRE(is_kquant(ws[i]->type), "kq_mfma: not a K-quant type");
+        AQ_REQUIRE(ws[i]->nb == ws[0]->nb, "kq_mfma: grouped matrices must share K");
+        AQ_REQUIRE(ws[i]->cols == x.n, "kq_mfma: activation length != weight columns");
+    }
+    // consecutive runs of at most KQ_MAXSEG matrices and two types per launch
+    int i0 = 0;
+    while (i0 < n) {
+        int i1 = i0 + 1, ta = ws[i0]->type, tb = ta;
+        while (i1 < n && i1 - i0 < KQ_MAXSEG) {
+            const int t = ws[i1]->type;
+            if (t != ta && t != tb) {
+                if (ta != tb) break;
+                tb = t;
+            }
+            i1++;
+        }
+        const int rc = launch_run(ws, ys, resids, i0, i1, x, ncols, stream);
+        if (rc) return rc;
+        i0 = i1;
+    }
+    return 0;
+}
+
+int launch_kq_mfma(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream) {
+    const Weight *ws[1] = {&w};
+    float *ys[1] = {y};
+    const float *rs[1] = {resid};
+    return launch_kq_group(ws, ys, rs, 1, x, ncols, stream);
 }
 
 } // namespace aq

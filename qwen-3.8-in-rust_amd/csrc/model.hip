@@ -508,6 +508,18 @@ int mm(aq_state *s, const Weight &w, const Act &x, size_t t, float *y, const flo
     return launch_matmul(w, x, t, y, resid, s->stream);
 }
 
+// Several matrices over the same activations: one grouped launch when all are K-quants of one K.
+int mm_multi(aq_state *s, int n, const Weight *const *ws, float *const *ys, const Act &x, size_t t) {
+    bool grouped = true;
+    for (int i = 0; i < n; i++) grouped = grouped && is_kquant(ws[i]->type) && ws[i]->nb == ws[0]->nb;
+    if (grouped) return launch_kq_group(ws, ys, nullptr, n, x, t, s->stream);
+    for (int i = 0; i < n; i++) {
+        const int rc = mm(s, *ws[i], x, t, ys[i]);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 enum Mode { PLAIN = 0, VERIFY = 1 };
 
 Needs mixer_needs(const DevLayer &L) {
@@ -543,9 +555,9 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
     const aq_model_config &c = m->cfg;
     int rc = 0;
     if (L.attention) {
-        if ((rc = mm(s, L.q, s->act_h, t, s->qg))) return rc;
-        if ((rc = mm(s, L.k, s->act_h, t, s->kk))) return rc;
-        if ((rc = mm(s, L.v, s->act_h, t, s->vv))) return rc;
+        const Weight *ws[3] = {&L.q, &L.k, &L.v};
+        float *ys[3] = {s->qg, s->kk, s->vv};
+        if ((rc = mm_multi(s, 3, ws, ys, s->act_h, t))) return rc;
         AQ_REQUIRE(kv->len + t <= kv->cap, "attention: KV cache full");
         AttnArgs a;
         a.qg = s->qg;
@@ -579,8 +591,11 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
     float *mixed = mode == VERIFY ? s->sv_mixed[dn_slot] : s->mixed;
     float *av = mode == VERIFY ? s->sv_a[dn_slot] : s->a;
     float *bv = mode == VERIFY ? s->sv_b[dn_slot] : s->b;
-    if ((rc = mm(s, L.qkv, s->act_h, t, mixed))) return rc;
-    if ((rc = mm(s, L.gate_z, s->act_h, t, s->z))) return rc;
+    {
+        const Weight *ws[2] = {&L.qkv, &L.gate_z};
+        float *ys[2] = {mixed, s->z};
+        if ((rc = mm_multi(s, 2, ws, ys, s->act_h, t))) return rc;
+    }
     AQ_REQUIRE(L.alpha.type == AQ_TYPE_F32 && L.beta.type == AQ_TYPE_F32,
                "DeltaNet: ssm_alpha / ssm_beta must be F32 in this build");
     DnArgs d;
@@ -620,8 +635,9 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
 // mlp.rs:114-132 on the rows in act_h: y_out = resid + down(silu(gate x) * up x).
 int mlp(aq_state *s, const DevLayer &L, size_t t, float *y_out, const float *resid) {
     const size_t ffn = s->m->cfg.ffn;
-    int rc = mm(s, L.gate, s->act_h, t, s->g);
-    if (!rc) rc = mm(s, L.up, s->act_h, t, s->u);
+    const Weight *ws[2] = {&L.gate, &L.up};
+    float *ys[2] = {s->g, s->u};
+    int rc = mm_multi(s, 2, ws, ys, s->act_h, t);
     if (rc) return rc;
     QuantOut q;
     q.act = &s->act_ffn;
