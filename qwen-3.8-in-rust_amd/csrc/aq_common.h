@@ -49,21 +49,44 @@ inline int block_bytes(int t) {
 }
 inline bool is_kquant(int t) { return t == AQ_TYPE_Q4_K || t == AQ_TYPE_Q5_K || t == AQ_TYPE_Q6_K; }
 
+// Device weight planes. A ggml row of `nb` blocks is split into planes so that every kernel load is an aligned
+// vector load; the integer math is unchanged (the GGUF bytes are the source of truth and aq_weight_download
+// restores them exactly).
+//
+// K-quants are stored by tile: tile (row >> 2, sb) = 4 consecutive rows x 1 super-block, tiles in row-group-major
+// order (tile index (row >> 2) * nb + sb, rows padded to a multiple of 4), so the 16 (lane pair, row) threads of
+// a matrix-core block read one contiguous 256-byte run per load. Within a tile, r = row & 3 and lane l = p + 4h
+// (p = l & 3, h = l >> 2):
+//   Q4_K: qa 512 B  codes: qa[h*256 + (p*4 + r)*16 + q*4 + b] = qs[32q + 4l + b] (q = sub-block pair 0..3)
+//         sc  64 B  per row r at r*16: f16 d, f16 dmin, then the 12 packed 6-bit scale/min bytes (as stored)
+//   Q5_K: as Q4_K plus qb 128 B: qb[(p*4 + r)*8 + h*4 + b] = qh[4l + b]
+//   Q6_K: qa 512 B  ql: qa[h*256 + (p*4 + r)*16 + (g*2 + k)*4 + b] = ql[g*64 + k*32 + 4l + b] (g = half, k = 0/1)
+//         qb 256 B  qh: qb[(p*4 + r)*16 + h*8 + g*4 + b] = qh[g*32 + 4l + b]
+//         sc  64 B  int8 group scales of row r at r*16       dm 8 B  f16 d of row r at r*2
 // Lane l (0..7) of a super-block owns elements 32s + 4l + b (s = sub-block 0..7, b = 0..3): the lane of the
-// reference's 8 exact i32 partial sums (kdot.rs:1-18). Lanes are stored in slot order slot(l) = 2*(l&3) + (l>>2)
-// (0,4,1,5,2,6,3,7), so lanes j and j+4, the pair one kernel thread owns, are adjacent.
+// reference's 8 exact i32 partial sums (kdot.rs:1-18).
+// Per 32-block (Q8_0 / Q4_0): qa 32 B / 16 B codes (as stored), dm 2 B f16 d, row-major. F32: qa = the rows.
+__host__ __device__ inline size_t kq_tile(size_t row, size_t sb, size_t nb) { return (row >> 2) * nb + sb; }
+__host__ __device__ inline size_t kq_qa_off(size_t row, size_t sb, size_t nb, int l) {
+    return kq_tile(row, sb, nb) * 512 + (size_t)(l >> 2) * 256 + (size_t)((l & 3) * 4 + (int)(row & 3)) * 16;
+}
+__host__ __device__ inline size_t kq_sc_off(size_t row, size_t sb, size_t nb) {
+    return kq_tile(row, sb, nb) * 64 + (row & 3) * 16;
+}
+// Q5_K qh bytes of lane l (4 B); Q6_K qh bytes of lane l (8 B: halves g = 0, 1)
+__host__ __device__ inline size_t kq_qb5_off(size_t row, size_t sb, size_t nb, int l) {
+    return kq_tile(row, sb, nb) * 128 + (size_t)((l & 3) * 4 + (int)(row & 3)) * 8 + (size_t)(l >> 2) * 4;
+}
+__host__ __device__ inline size_t kq_qb6_off(size_t row, size_t sb, size_t nb, int l) {
+    return kq_tile(row, sb, nb) * 256 + (size_t)((l & 3) * 4 + (int)(row & 3)) * 16 + (size_t)(l >> 2) * 8;
+}
+__host__ __device__ inline size_t kq_dm_off(size_t row, size_t sb, size_t nb) {
+    return kq_tile(row, sb, nb) * 8 + (row & 3) * 2;
+}
+// Activation Q8_K codes are stored by lane slot slot(l) = 2*(l&3) + (l>>2) (0,4,1,5,2,6,3,7), so lanes j and
+// j+4, the pair one kernel thread owns, are adjacent.
 __host__ __device__ inline int lane_slot(int l) { return 2 * (l & 3) + (l >> 2); }
 
-// Device weight planes. A ggml row of `nb` blocks is split into planes so that every kernel load is an
-// aligned vector load; the integer math is unchanged (the GGUF bytes are the source of truth and
-// aq_weight_download restores them exactly). Per super-block (K-quants):
-//   Q4_K: qa 128 B  nibbles by lane: qa[slot(l)*16 + q*4 + b] = qs[32q + 4l + b] (q = sub-block pair)
-//         sc  16 B  f16 d, f16 dmin, then the 12 packed 6-bit scale/min bytes (as stored)
-//   Q5_K: as Q4_K plus qb 32 B: qb[slot(l)*4 + b] = qh[4l + b]
-//   Q6_K: qa 128 B  ql by lane: qa[slot(l)*16 + (h*2 + jj)*4 + b] = ql[h*64 + jj*32 + 4l + b]
-//         qb  64 B  qh by lane: qb[slot(l)*8 + h*4 + b] = qh[h*32 + 4l + b]
-//         sc  16 B  int8 group scales                        dm 2 B  f16 d
-// Per 32-block (Q8_0 / Q4_0): qa 32 B / 16 B codes (as stored), dm 2 B f16 d. F32: qa = the rows.
 struct Weight {
     int type = 0;
     size_t rows = 0, cols = 0, nb = 0; // nb: blocks per row

@@ -7,22 +7,19 @@
 // the exact integers are produced is new:
 //
 //  * v_mfma_i32_4x4x4_16b_i8 computes 16 independent 4x4x4 int8 products. Block b of one instruction is
-//    (row group g, lane j): its K = 4 elements are lane j's 4 positions of one sub-block, so it yields the lane-j
-//    partial of that sub-block for 4 weight rows x 4 activation columns, exactly (int32). A = activations (A row i
-//    = column c), B = weight codes (B column = weight row). Register layout, measured on the device: A and B of
-//    block b at lanes 4b+i / 4b+j, D[i][j] at lane 4b+j, VGPR i.
-//  * Thread t = 16g + 4j + r of a wave owns weight row 4g + r (16 rows per wave) and the two reference lanes j and
-//    j+4: one instruction set with blocks (g, j) computes lane j, a second one lane j+4. Per-row work (scale
-//    decode, the min lanes) is shared by the row's 4 threads instead of 8, and every min lane j (0..3) is a thread.
+//    (q, j): its K = 4 elements are lane j's 4 positions of one sub-block, so it yields the lane-j partial of that
+//    sub-block for 4 weight rows x 4 activation columns, exactly (int32). A = activations (A row i = column c),
+//    B = weight codes (B column = weight row). Register layout, measured on the device: A and B of block b at lanes
+//    4b+i / 4b+j, D[i][j] at lane 4b+j, VGPR i.
+//  * Thread 4b + r (b = 4q + j) owns weight row r of its block's row group and the two reference lanes j and j+4:
+//    one instruction set computes lane j, a second one lane j+4. q names a (row group, K slice) pair: a wave covers
+//    16 / KSW rows and KSW consecutive super-blocks per round (kq_wave_run).
 //  * Q4_K / Q5_K: the 6-bit sub-block scale is split into 3-bit (2-bit) digits folded into the int8 weight operand
 //    (sb_products_split), so the MFMA accumulator sums the scaled sub-block dots; Q6_K (int8 scales) multiplies
 //    each MFMA partial by its scale with a full-rate 24-bit integer mad.
 //  * Results go to VGPRs (built with -amdgpu-mfma-vgpr-form): no accumulator-register copies.
-//  * Activations are staged in LDS per chunk of super-blocks, double-buffered (chunk k+1 is fetched into registers
-//    while chunk k is computed); weights stream from HBM as 16-byte loads, prefetched PF super-blocks ahead.
-//  * Matrices with few rows split K across KS waves of the work-group: wave w takes super-blocks w, w+KS, ...;
-//    after every round the waves exchange their f32 products through LDS and each adds them to its copy of the
-//    chain in super-block order, which keeps the chain the reference's sequential sum bit for bit.
+//  * Weights are read from tiled planes (4 rows x 1 super-block per tile, aq_common.h) into a register ring PF
+//    rounds deep; activations are staged in LDS (all of K, or chunks of it) once per work-group.
 #include "aq_common.h"
 
 namespace aq {
@@ -72,18 +69,21 @@ struct WRegs {
     uint32_t d6;    // Q6_K: f16 d
 };
 
+// Tile `tile` (= (row >> 2) * nb + sb), row r = row & 3 within it, lane pair j (tiled planes, aq_common.h): the
+// 16 (j, r) threads of a matrix-core block read contiguous 256-byte runs.
 template <int TYPE>
-__device__ __forceinline__ void load_w(WRegs<TYPE> &w, const MfArgs &a, size_t wsb, int j) {
-    const uint4 *q = reinterpret_cast<const uint4 *>(a.qa + wsb * 128 + j * 32);
-    w.qa0 = q[0];
-    w.qa1 = q[1];
-    w.sc = *reinterpret_cast<const uint4 *>(a.sc + wsb * 16);
+__device__ __forceinline__ void load_w(WRegs<TYPE> &w, const MfArgs &a, size_t tile, int r, int j) {
+    const int jr = j * 4 + r;
+    const uint8_t *qa = a.qa + tile * 512 + jr * 16;
+    w.qa0 = *reinterpret_cast<const uint4 *>(qa);       // lane j
+    w.qa1 = *reinterpret_cast<const uint4 *>(qa + 256); // lane j + 4
+    w.sc = *reinterpret_cast<const uint4 *>(a.sc + tile * 64 + r * 16);
     if constexpr (TYPE == AQ_TYPE_Q5_K) {
-        const uint2 h = *reinterpret_cast<const uint2 *>(a.qb + wsb * 32 + j * 8);
+        const uint2 h = *reinterpret_cast<const uint2 *>(a.qb + tile * 128 + jr * 8);
         w.qb = make_uint4(h.x, h.y, 0, 0);
     } else if constexpr (TYPE == AQ_TYPE_Q6_K) {
-        w.qb = *reinterpret_cast<const uint4 *>(a.qb + wsb * 64 + j * 16);
-        w.d6 = *reinterpret_cast<const uint16_t *>(a.dm + wsb * 2);
+        w.qb = *reinterpret_cast<const uint4 *>(a.qb + tile * 256 + jr * 16);
+        w.d6 = *reinterpret_cast<const uint16_t *>(a.dm + tile * 8 + r * 2);
     }
 }
 
@@ -300,204 +300,18 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
     }
 }
 
-// LDS chunk (per super-block of the chunk): codes xq[CH][NC][256] (by lane slot), f32 scales xd[CH][NCP] and
-// activation-sum pairs xm[CH][8][NCP] (pair i = sums 2i, 2i+1: Q4_K/Q5_K sub-block sums (i < 4), Q6_K group sums),
-// NCP = NC rounded up to 4 so a thread reads its 4 columns with one 16-byte load.
-template <int NC, int CH>
-struct Lds {
-    static constexpr int NCP = (NC + 3) / 4 * 4;
-    int8_t xq[CH][NC][256];
-    float xd[CH][NCP];
-    uint32_t xm[CH][8][NCP];
-};
-
-template <int TYPE, int NC, int KS, int PF, int CH>
-__global__ void __launch_bounds__(256) kq_mfma_kernel(MfArgs a) {
-    static_assert(CH % (KS * PF) == 0, "a chunk must hold whole prefetch rounds");
-    constexpr int RG = 4 / KS;                      // row groups (16 rows each) per work-group
-    constexpr int NCG = (NC + 3) / 4;               // column groups of 4
-    constexpr int NCP = Lds<NC, CH>::NCP;
-    constexpr int NV = (CH * NC * 16 + 255) / 256;  // 16-byte code vectors per thread per chunk
-    constexpr int NM = CH * NC;                     // (super-block, column) meta entries per chunk
-    static_assert(NV <= 4 && NM <= 256, "staging shape");
-    constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
-    __shared__ Lds<NC, CH> lds_buf[2];
-    __shared__ float xch[KS > 1 ? RG : 1][KS > 1 ? 2 : 1][KS][3 * NC][64];
-
-    const int t = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const int rg = wid / KS, w = wid % KS;
-    const int g = t >> 4, j = (t >> 2) & 3, r = t & 3;
-    int row = ((int)blockIdx.x * RG + rg) * 16 + 4 * g + r;
-    const bool valid = row < a.rows;
-    if (!valid) row = a.rows - 1;
-    const int nb = a.nb;
-    const int nchunks = (nb + CH - 1) / CH;
-    const size_t rowsb = (size_t)row * nb;
-
-    float acc0[NC], acc1[NC], accm[NC]; // lane j, lane j+4, min lane j
-#pragma unroll
-    for (int i = 0; i < NC; i++) acc0[i] = acc1[i] = accm[i] = 0.0f;
-
-    WRegs<TYPE> wr[PF];
-#pragma unroll
-    for (int p = 0; p < PF; p++) load_w<TYPE>(wr[p], a, rowsb + min(w + p * KS, nb - 1), j);
-    int parity = 0;
-
-    // ---- activation chunk staging (named registers, never an array: arrays here get demoted to scratch)
-    uint4 sv0 = make_uint4(0, 0, 0, 0), sv1 = sv0, sv2 = sv0, sv3 = sv0, sm0 = sv0, sm1 = sv0;
-    float sd = 0.0f;
-#define AQ_STAGE_VEC(I, SV, BODY)                                                                             \
-    if constexpr (I < NV) {                                                                                   \
-        const int v = (int)threadIdx.x + I * 256;                                                             \
-        const int c = v / (CH * 16), rem = v % (CH * 16), sbi = rem / 16, o = (rem % 16) * 16;                \
-        BODY(SV)                                                                                              \
-    }
-    auto stage_load = [&](int k) {
-        const int c0 = k * CH, ch = nb - c0 < CH ? nb - c0 : CH;
-#define AQ_LOAD_BODY(SV)                                                                                      \
-    if (c < NC && sbi < ch)                                                                                   \
-        SV = *reinterpret_cast<const uint4 *>(a.xqs + (size_t)c * a.xcol + (size_t)(c0 + sbi) * 256 + o);
-        AQ_STAGE_VEC(0, sv0, AQ_LOAD_BODY)
-        AQ_STAGE_VEC(1, sv1, AQ_LOAD_BODY)
-        AQ_STAGE_VEC(2, sv2, AQ_LOAD_BODY)
-        AQ_STAGE_VEC(3, sv3, AQ_LOAD_BODY)
-#undef AQ_LOAD_BODY
-        const int e = (int)threadIdx.x;
-        if (e < NM) {
-            const int c = e / CH, sbi = e % CH;
-            if (sbi < ch) {
-                const size_t xm = (size_t)c * nb + c0 + sbi;
-                sd = a.xd[xm];
-                if constexpr (Q6) {
-                    sm0 = reinterpret_cast<const uint4 *>(a.xbs + xm * 16)[0];
-                    sm1 = reinterpret_cast<const uint4 *>(a.xbs + xm * 16)[1];
-                } else {
-                    sm0 = *reinterpret_cast<const uint4 *>(a.xq8s + xm * 8);
-                }
-            }
-        }
-    };
-    auto stage_store = [&](int buf) {
-        Lds<NC, CH> &L = lds_buf[buf];
-#define AQ_STORE_BODY(SV)                                                                                     \
-    if (c < NC) *reinterpret_cast<uint4 *>(&L.xq[sbi][c][o]) = SV;
-        AQ_STAGE_VEC(0, sv0, AQ_STORE_BODY)
-        AQ_STAGE_VEC(1, sv1, AQ_STORE_BODY)
-        AQ_STAGE_VEC(2, sv2, AQ_STORE_BODY)
-        AQ_STAGE_VEC(3, sv3, AQ_STORE_BODY)
-#undef AQ_STORE_BODY
-        const int e = (int)threadIdx.x;
-        if (e < NM) {
-            const int c = e / CH, sbi = e % CH;
-            L.xd[sbi][c] = sd;
-            L.xm[sbi][0][c] = sm0.x;
-            L.xm[sbi][1][c] = sm0.y;
-            L.xm[sbi][2][c] = sm0.z;
-            L.xm[sbi][3][c] = sm0.w;
-            if constexpr (Q6) {
-                L.xm[sbi][4][c] = sm1.x;
-                L.xm[sbi][5][c] = sm1.y;
-                L.xm[sbi][6][c] = sm1.z;
-                L.xm[sbi][7][c] = sm1.w;
-            }
-        }
-    };
-#undef AQ_STAGE_VEC
-    stage_load(0);
-    stage_store(0);
-    if (nchunks > 1) stage_load(1);
-    __syncthreads();
-
-    for (int k = 0; k < nchunks; k++) {
-        const int c0 = k * CH;
-        const int ch = nb - c0 < CH ? nb - c0 : CH;
-        const Lds<NC, CH> &L = lds_buf[k & 1];
-
-        auto process = [&](const WRegs<TYPE> &wv, const int sbi, float *pr0, float *pr1, float *pm) {
-            if constexpr (TYPE == AQ_TYPE_Q6_K)
-                sb_products<TYPE, NC>(wv, &L.xq[sbi][0][0], &L.xd[sbi][0], &L.xm[sbi][0][0], NCP, j, r, pr0, pr1, pm);
-            else
-                sb_products_split<TYPE, NC>(wv, &L.xq[sbi][0][0], &L.xd[sbi][0], &L.xm[sbi][0][0], NCP, j, r, pr0, pr1,
-                                            pm);
-        };
-
-        for (int rb = 0; rb < ch; rb += KS * PF) {
-#pragma unroll
-            for (int p = 0; p < PF; p++) {
-                const int round0 = rb + p * KS; // first super-block (chunk-relative) of this round
-                if (round0 < ch) {              // uniform across the work-group
-                    const int sbi = round0 + w;
-                    float pr0[NC], pr1[NC], pm[NC];
-#pragma unroll
-                    for (int c = 0; c < NC; c++) pr0[c] = pr1[c] = pm[c] = 0.0f;
-                    if (sbi < ch) {
-                        process(wr[p], sbi, pr0, pr1, pm);
-                        load_w<TYPE>(wr[p], a, rowsb + min(c0 + sbi + PF * KS, nb - 1), j);
-                    }
-                    if constexpr (KS == 1) {
-#pragma unroll
-                        for (int c = 0; c < NC; c++) {
-                            acc0[c] += pr0[c];
-                            acc1[c] += pr1[c];
-                            if constexpr (!Q6) accm[c] += pm[c];
-                        }
-                    } else {
-                        float(*x)[3 * NC][64] = xch[rg][parity];
-#pragma unroll
-                        for (int c = 0; c < NC; c++) {
-                            x[w][c][t] = pr0[c];
-                            x[w][NC + c][t] = pr1[c];
-                            x[w][2 * NC + c][t] = pm[c];
-                        }
-                        __syncthreads();
-                        const int live = ch - round0 < KS ? ch - round0 : KS; // super-blocks in this round
-#pragma unroll
-                        for (int w2 = 0; w2 < KS; w2++) {
-                            if (w2 < live) {
-#pragma unroll
-                                for (int c = 0; c < NC; c++) {
-                                    acc0[c] += x[w2][c][t];
-                                    acc1[c] += x[w2][NC + c][t];
-                                    if constexpr (!Q6) accm[c] += x[w2][2 * NC + c][t];
-                                }
-                            }
-                        }
-                        parity ^= 1;
-                    }
-                }
-            }
-        }
-        if (k + 1 < nchunks) {
-            stage_store((k + 1) & 1);
-            if (k + 2 < nchunks) stage_load(k + 2);
-        }
-        __syncthreads();
-    }
-    // ---------------------------------------------------------------- reduce the 8 lanes of each row
-    // lanes j and j+4 are in one thread; j sits at t = 16g + 4j + r: xor 8 pairs j with j^2, xor 4 with j^1.
-    if (w != 0) return; // every wave of a row group holds the same chain; wave 0 writes
-#pragma unroll
-    for (int col = 0; col < NC; col++) {
-        float v = acc0[col] + acc1[col]; // l_j + l_{j+4}
-        v = v + __shfl_xor(v, 8);
-        v = v + __shfl_xor(v, 4);
-        if constexpr (!Q6) {
-            float m = accm[col];
-            m = m + __shfl_xor(m, 8); // m0+m2, m1+m3
-            m = m + __shfl_xor(m, 4);
-            v = v + m;
-        }
-        if (j == 0 && valid) {
-            const size_t o = (size_t)col * a.rows + row;
-            a.y[o] = a.resid ? a.resid[o] + v : v;
-        }
-    }
-}
-
-// Whole-K variant: the activations of all nb super-blocks are copied to LDS once, behind one barrier, so the
-// weight prefetch ring is never drained by a staging wait; the main loop has no data-dependent branch around a
-// load (a round past the end of K is computed on clamped indices and its products are not added). Column stride
-// KQ_XS = 256 + 16 bytes puts the 4 columns a wave reads at once in different LDS banks.
+// ------------------------------------------------------------------------------------ the wave-split kernel
+// The activations of all nb super-blocks are copied to LDS once per work-group, behind its only barrier (column
+// stride KQ_XS = 256 + 16 bytes puts the 4 columns a wave reads at once in different LDS banks); weights stream
+// from HBM into a register ring PF rounds deep.
+//
+// The 16 matrix-core blocks of a wave are (q, j): j = the lane pair (j, j+4), q = (row group rg, K slice ks) with
+// KSW K slices per wave (1, 2 or 4) and 4 / KSW row groups of 4 rows: a wave owns 16 / KSW rows and in round rd
+// its K slice ks computes super-block rd * KSW + ks. Tall matrices (gate, up) take KSW = 1; short ones (down,
+// ssm_out: 5120 rows) split K four ways inside the wave, so a wave covers 4 rows and the grid still holds enough
+// waves to keep HBM busy. The f32 chains stay the reference's sequential sums: each round the K slices hand their
+// products to the chain owners through the wave's own LDS slot (no work-group barrier; one wave's LDS accesses
+// execute in order), and the owner of a chain adds the KSW products in super-block order.
 //
 // One launch can cover up to three matrices that read the same activations (gate and up; q, k and v; the
 // DeltaNet qkv and z projections): the work-groups are laid out segment after segment, each segment with its own
@@ -514,38 +328,39 @@ struct KqSeg {
 struct KqGroup {
     KqSeg seg[KQ_MAXSEG];
     int nseg, nb;
+    int chk; // super-blocks per activation staging chunk: nb, or a multiple of KSW * PF
     const int8_t *xqs;
     const float *xd;
     const int16_t *xbs, *xq8s;
     size_t xcol;
 };
 
-inline size_t kq_full_lds_bytes(int nb, int nc, bool has45, bool has6) {
-    const int ncp = (nc + 3) / 4 * 4, np = (has45 ? 4 : 0) + (has6 ? 8 : 0);
-    return (size_t)nb * nc * KQ_XS + (size_t)nb * ncp * 4 + (size_t)nb * np * ncp * 4;
-}
-
 // Activations of every super-block to LDS: codes [sb][column][KQ_XS], scales [sb][NCP], activation-sum pairs
 // [sb][NP][NCP]: the 4 sub-block-sum pairs (Q4_K/Q5_K segments, HAS45) and then the 8 group-sum pairs (Q6_K
 // segments, HAS6).
+// Activations of super-blocks s0 .. s0 + ns - 1 to LDS slots 0 .. ns - 1: codes [slot][column][KQ_XS], scales
+// [slot][NCP], activation-sum pairs [slot][NP][NCP] (the 4 sub-block-sum pairs for Q4_K/Q5_K segments, HAS45, then
+// the 8 group-sum pairs for Q6_K segments, HAS6). 16 threads per (column, super-block) record of 256 codes, two
+// records per thread group in flight (few registers: the weight ring stays resident).
 template <int NC, bool HAS45, bool HAS6>
-__device__ __forceinline__ void kq_stage(const KqGroup &G, int8_t *sxq, float *sxd, uint32_t *sxm) {
+__device__ __forceinline__ void kq_stage(const KqGroup &G, int8_t *sxq, float *sxd, uint32_t *sxm, int s0, int ns) {
     constexpr int NCP = (NC + 3) / 4 * 4;
     constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), P6 = HAS45 ? 4 : 0;
     const int nb = G.nb;
-    // 16 threads per (column, super-block) record of 256 codes, two records per thread group in flight
-    const int o = threadIdx.x & 15, nrec = nb * NC;
+    const int o = threadIdx.x & 15, nrec = ns * NC;
     for (int r0 = (int)threadIdx.x >> 4; r0 < nrec; r0 += 32) {
         const int ra = r0, rb = r0 + 16 < nrec ? r0 + 16 : r0; // the second record, or the first again
-        const int ca = ra / nb, sa = ra - ca * nb, cb = rb / nb, sbb = rb - cb * nb;
-        const uint4 va = *reinterpret_cast<const uint4 *>(G.xqs + (size_t)ca * G.xcol + (size_t)sa * 256 + o * 16);
-        const uint4 vb = *reinterpret_cast<const uint4 *>(G.xqs + (size_t)cb * G.xcol + (size_t)sbb * 256 + o * 16);
+        const int ca = ra / ns, sa = ra - ca * ns, cb = rb / ns, sbb = rb - cb * ns;
+        const uint4 va =
+            *reinterpret_cast<const uint4 *>(G.xqs + (size_t)ca * G.xcol + (size_t)(s0 + sa) * 256 + o * 16);
+        const uint4 vb =
+            *reinterpret_cast<const uint4 *>(G.xqs + (size_t)cb * G.xcol + (size_t)(s0 + sbb) * 256 + o * 16);
         *reinterpret_cast<uint4 *>(sxq + ((size_t)sa * NC + ca) * KQ_XS + o * 16) = va;
         *reinterpret_cast<uint4 *>(sxq + ((size_t)sbb * NC + cb) * KQ_XS + o * 16) = vb;
     }
-    for (int e = (int)threadIdx.x; e < nb * NC; e += 256) {
-        const int c = e / nb, sb = e % nb;
-        const size_t m = (size_t)c * nb + sb;
+    for (int e = (int)threadIdx.x; e < nrec; e += 256) {
+        const int c = e / ns, sb = e % ns;
+        const size_t m = (size_t)c * nb + s0 + sb;
         sxd[sb * NCP + c] = G.xd[m];
         if constexpr (HAS45) {
             const uint4 p0 = *reinterpret_cast<const uint4 *>(G.xq8s + m * 8);
@@ -564,16 +379,31 @@ __device__ __forceinline__ void kq_stage(const KqGroup &G, int8_t *sxq, float *s
     }
 }
 
-// One segment's work-group: rows wg*RG*16 .. +RG*16 of the segment's matrix, K split KS ways across waves.
-// xch: [RG][2][KS][3 NC][64] exchange floats. HAS45 / HAS6: the staging's pair sets (this segment's type reads
-// its own).
-template <int TYPE, int NC, int KS, int PF, bool HAS45, bool HAS6>
-__device__ __forceinline__ void kq_full_run(const KqGroup &G, const KqSeg &sg, int wg, int8_t *sxq, float *sxd,
-                                            uint32_t *sxm, float *xch) {
-    constexpr int RG = 4 / KS;
+// The exchange slot of one wave: KSW blocks (one per K slice) of NCH chains x NI chain owners, the block stride
+// padded to NI modulo 64 floats so both the writes (by slice) and the owners' reads hit distinct banks.
+template <int NCH, int KSW>
+struct KqXch {
+    static constexpr int NI = 64 / KSW;
+    static constexpr int S = NCH * NI + (((NI - NCH * NI) % 64) + 64) % 64;
+    static constexpr int FLOATS = KSW > 1 ? KSW * S : 1;
+};
+
+template <int NC>
+constexpr int kq_nch_max() { return 3 * NC; }
+
+// One wave's rows of one segment: the products of its K slice each round, the in-order chains, the lane
+// reduction ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)) [+ (m0+m2)+(m1+m3)] (kdot.rs:1-18) and the store.
+template <int TYPE, int NC, int KSW, int PF, bool HAS45, bool HAS6>
+__device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, int wg, int8_t *sxq, float *sxd,
+                                            uint32_t *sxm, float *xw) {
+    constexpr int RW = 16 / KSW;                        // rows per wave
     constexpr int NCP = (NC + 3) / 4 * 4;
     constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
     constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), POFF = Q6 && HAS45 ? 4 : 0;
+    constexpr int NCH = (Q6 ? 2 : 3) * NC;              // f32 chains of one (row, lane pair): j, j+4, min j
+    constexpr int NO = KSW > 1 ? (NCH + KSW - 1) / KSW : NCH; // chains this thread keeps
+    using X = KqXch<3 * NC, KSW>;                       // slot sized for the largest NCH of the kernel
+    constexpr int NI = X::NI;
     MfArgs a{};
     a.qa = sg.qa;
     a.qb = sg.qb;
@@ -582,170 +412,210 @@ __device__ __forceinline__ void kq_full_run(const KqGroup &G, const KqSeg &sg, i
     a.rows = sg.rows;
     a.nb = G.nb;
     const int nb = G.nb;
-    const int t = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const int rg = wid / KS, w = wid % KS;
-    const int g = t >> 4, j = (t >> 2) & 3, r = t & 3;
-    int row = (wg * RG + rg) * 16 + 4 * g + r;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int b = lane >> 2, r = lane & 3, j = b & 3, q = b >> 2;
+    const int rg = q / KSW, ks = q % KSW;
+    const int idx = (rg * 4 + j) * 4 + r; // chain owner index within the wave (0..NI-1)
+    const int row0 = (wg * 4 + wid) * RW;
+    int row = row0 + rg * 4 + r;
     const bool valid = row < a.rows;
     if (!valid) row = a.rows - 1;
-    const size_t rowsb = (size_t)row * nb;
+    const size_t tile0 = (size_t)(row >> 2) * nb; // this row group's first tile
+    const int rr = row & 3;
+    WRegs<TYPE> wr[PF];
 
     // the first PF rounds of weights fly while the activations are staged
-    WRegs<TYPE> wr[PF];
 #pragma unroll
-    for (int p = 0; p < PF; p++) load_w<TYPE>(wr[p], a, rowsb + min(w + p * KS, nb - 1), j);
-    kq_stage<NC, HAS45, HAS6>(G, sxq, sxd, sxm);
+    for (int p = 0; p < PF; p++) load_w<TYPE>(wr[p], a, tile0 + min(p * KSW + ks, nb - 1), rr, j);
+    const int chk = G.chk;
+    kq_stage<NC, HAS45, HAS6>(G, sxq, sxd, sxm, 0, chk < nb ? chk : nb);
     __syncthreads();
+    if (row0 >= a.rows && chk >= nb) return; // no barrier follows (with chunks, idle waves keep the barriers)
+    int s0 = 0; // first super-block of the staged chunk
 
-    float acc0[NC], acc1[NC], accm[NC]; // lane j, lane j+4, min lane j
+    float acc[NO];
 #pragma unroll
-    for (int i = 0; i < NC; i++) acc0[i] = acc1[i] = accm[i] = 0.0f;
-    int parity = 0;
-    const int nr = (nb + KS - 1) / KS; // rounds of KS super-blocks (wave w takes super-block round*KS + w)
+    for (int i = 0; i < NO; i++) acc[i] = 0.0f;
+    const int nr = (nb + KSW - 1) / KSW; // rounds
 
-    auto round_body = [&](WRegs<TYPE> &wv, const int round, const bool prefetch) {
-        const int sb = round * KS + w;
+    auto round_body = [&](WRegs<TYPE> &wv, const int rd, const bool prefetch) {
+        const int sb = rd * KSW + ks;
         const int sbc = sb < nb ? sb : nb - 1;
-        float pr0[NC], pr1[NC], pm[NC];
+        float pr[3][NC];
 #pragma unroll
-        for (int c = 0; c < NC; c++) pm[c] = 0.0f;
-        const int8_t *xq = sxq + (size_t)sbc * NC * KQ_XS;
-        const float *xd = sxd + sbc * NCP;
-        const uint32_t *xm = sxm + (sbc * NP + POFF) * NCP;
+        for (int c = 0; c < NC; c++) pr[2][c] = 0.0f;
+        const int ls = sbc - s0; // LDS slot
+        const int8_t *xq = sxq + (size_t)ls * NC * KQ_XS;
+        const float *xd = sxd + ls * NCP;
+        const uint32_t *xm = sxm + (ls * NP + POFF) * NCP;
         if constexpr (Q6)
-            sb_products<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr0, pr1, pm);
+            sb_products<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr[0], pr[1], pr[2]);
         else
-            sb_products_split<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr0, pr1, pm);
+            sb_products_split<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr[0], pr[1], pr[2]);
         if (prefetch) {
-            load_w<TYPE>(wv, a, rowsb + min(sb + PF * KS, nb - 1), j);
-            __builtin_amdgcn_sched_barrier(0); // issue the refill here, not after the later rounds' compute
+            // the refill goes into the registers just consumed: every use of the old values stays above it, so
+            // the ring keeps its registers across the loop's back edge (no copies, no drain of the loads in flight)
+            __builtin_amdgcn_sched_barrier(0);
+            load_w<TYPE>(wv, a, tile0 + min(sb + PF * KSW, nb - 1), rr, j);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        const int live = nb - round * KS < KS ? nb - round * KS : KS; // super-blocks in this round
-        if constexpr (KS == 1) {
+        if constexpr (KSW == 1) {
 #pragma unroll
-            for (int c = 0; c < NC; c++) {
-                acc0[c] += pr0[c];
-                acc1[c] += pr1[c];
-                if constexpr (!Q6) accm[c] += pm[c];
-            }
+            for (int k = 0; k < NCH; k++) acc[k] += pr[k / NC][k % NC];
         } else {
-            float *x = xch + (size_t)(rg * 2 + parity) * KS * 3 * NC * 64; // [KS][3 NC][64]
+            const int live = nb - rd * KSW < KSW ? nb - rd * KSW : KSW; // super-blocks in this round
 #pragma unroll
-            for (int c = 0; c < NC; c++) {
-                x[(w * 3 * NC + c) * 64 + t] = pr0[c];
-                x[(w * 3 * NC + NC + c) * 64 + t] = pr1[c];
-                x[(w * 3 * NC + 2 * NC + c) * 64 + t] = pm[c];
-            }
-            __syncthreads();
+            for (int k = 0; k < NCH; k++) xw[ks * X::S + k * NI + idx] = pr[k / NC][k % NC];
+            __asm__ volatile("" ::: "memory");
 #pragma unroll
-            for (int w2 = 0; w2 < KS; w2++) {
-                if (w2 < live) {
+            for (int m = 0; m < NO; m++) {
+                const int k = ks + KSW * m;
+                if (k < NCH) {
 #pragma unroll
-                    for (int c = 0; c < NC; c++) {
-                        acc0[c] += x[(w2 * 3 * NC + c) * 64 + t];
-                        acc1[c] += x[(w2 * 3 * NC + NC + c) * 64 + t];
-                        if constexpr (!Q6) accm[c] += x[(w2 * 3 * NC + 2 * NC + c) * 64 + t];
-                    }
+                    for (int k2 = 0; k2 < KSW; k2++)
+                        if (k2 < live) acc[m] += xw[k2 * X::S + k * NI + idx];
                 }
             }
-            parity ^= 1;
+            __asm__ volatile("" ::: "memory");
+        }
+    };
+    // the next staging chunk when round rd starts past the staged one (chunks hold whole groups of PF rounds)
+    auto next_chunk = [&](const int rd) {
+        if (rd * KSW >= s0 + chk) { // uniform across the work-group
+            __syncthreads();
+            s0 += chk;
+            kq_stage<NC, HAS45, HAS6>(G, sxq, sxd, sxm, s0, nb - s0 < chk ? nb - s0 : chk);
+            __syncthreads();
         }
     };
     const int nfull = nr / PF * PF;
     for (int rd = 0; rd < nfull; rd += PF) {
+        next_chunk(rd);
 #pragma unroll
         for (int p = 0; p < PF; p++) round_body(wr[p], rd + p, true);
     }
+    if (nfull < nr) next_chunk(nfull);
 #pragma unroll
     for (int p = 0; p < PF; p++)
         if (nfull + p < nr) round_body(wr[p], nfull + p, false);
 
-    if (w != 0) return; // every wave of a row group holds the same chain; wave 0 writes
+    if constexpr (KSW == 1) {
+        // lanes j and j+4 are in one thread; j sits at lane 16g + 4j + r: xor 8 pairs j with j^2, xor 4 with j^1
 #pragma unroll
-    for (int col = 0; col < NC; col++) {
-        float v = acc0[col] + acc1[col]; // l_j + l_{j+4}
-        v = v + __shfl_xor(v, 8);
-        v = v + __shfl_xor(v, 4);
-        if constexpr (!Q6) {
-            float m = accm[col];
-            m = m + __shfl_xor(m, 8); // m0+m2, m1+m3
-            m = m + __shfl_xor(m, 4);
-            v = v + m;
+        for (int col = 0; col < NC; col++) {
+            float v = acc[col] + acc[NC + col]; // l_j + l_{j+4}
+            v = v + __shfl_xor(v, 8);
+            v = v + __shfl_xor(v, 4);
+            if constexpr (!Q6) {
+                float m = acc[2 * NC + col];
+                m = m + __shfl_xor(m, 8); // m0+m2, m1+m3
+                m = m + __shfl_xor(m, 4);
+                v = v + m;
+            }
+            if (j == 0 && valid) {
+                const size_t o = (size_t)col * a.rows + row;
+                sg.y[o] = sg.resid ? sg.resid[o] + v : v;
+            }
         }
-        if (j == 0 && valid) {
-            const size_t o = (size_t)col * a.rows + row;
-            sg.y[o] = sg.resid ? sg.resid[o] + v : v;
+    } else {
+        // every owner's final chains to the slot [chain][owner], then one lane per (row, column) output
+#pragma unroll
+        for (int m = 0; m < NO; m++) {
+            const int k = ks + KSW * m;
+            if (k < NCH) xw[k * NI + idx] = acc[m];
+        }
+        __asm__ volatile("" ::: "memory");
+        if (lane < RW * NC) {
+            const int col = lane / RW, rw = lane % RW;
+            const int orow = row0 + rw;
+            const int base = (rw >> 2) * 16 + (rw & 3); // idx of lane pair 0 of this row
+            float a0[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) a0[jj] = xw[col * NI + base + 4 * jj] + xw[(NC + col) * NI + base + 4 * jj];
+            float v = (a0[0] + a0[2]) + (a0[1] + a0[3]);
+            if constexpr (!Q6) {
+                const float *m = xw + (2 * NC + col) * NI + base;
+                v = v + ((m[0] + m[8]) + (m[4] + m[12]));
+            }
+            if (orow < a.rows) {
+                const size_t o = (size_t)col * a.rows + orow;
+                sg.y[o] = sg.resid ? sg.resid[o] + v : v;
+            }
         }
     }
 }
 
-template <int T0, int T1, int NC, int KS, int PF>
-__global__ void __launch_bounds__(256) kq_group_kernel(KqGroup G) {
-    constexpr int RG = 4 / KS;
+template <int T0, int T1, int NC, int KSW, int PF>
+__global__ void __launch_bounds__(256) kq_wave_kernel(KqGroup G) {
     constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
     constexpr bool HAS45 = T0 != AQ_TYPE_Q6_K || T1 != AQ_TYPE_Q6_K;
     constexpr int NCP = (NC + 3) / 4 * 4;
+    using X = KqXch<3 * NC, KSW>;
     extern __shared__ __align__(16) uint8_t kq_lds[];
-    __shared__ float xch[(KS > 1 ? RG : 1) * (KS > 1 ? 2 : 1) * KS * 3 * NC * 64];
+    __shared__ float xch[4 * X::FLOATS];
     int si = 0; // this work-group's segment (uniform)
     while (si + 1 < G.nseg && (int)blockIdx.x >= G.seg[si].wg_end) si++;
     const KqSeg &sg = G.seg[si];
     const int wg = (int)blockIdx.x - (si ? G.seg[si - 1].wg_end : 0);
+    const int ns = G.chk < G.nb ? G.chk : G.nb; // super-blocks staged at a time
     int8_t *sxq = reinterpret_cast<int8_t *>(kq_lds);
-    float *sxd = reinterpret_cast<float *>(kq_lds + (size_t)G.nb * NC * KQ_XS);
-    uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)G.nb * NCP);
+    float *sxd = reinterpret_cast<float *>(kq_lds + (size_t)ns * NC * KQ_XS);
+    uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)ns * NCP);
+    float *xw = xch + (threadIdx.x >> 6) * X::FLOATS;
     if (T0 == T1 || sg.type == T0)
-        kq_full_run<T0, NC, KS, PF, HAS45, HAS6>(G, sg, wg, sxq, sxd, sxm, xch);
+        kq_wave_run<T0, NC, KSW, PF, HAS45, HAS6>(G, sg, wg, sxq, sxd, sxm, xw);
     else
-        kq_full_run<T1, NC, KS, PF, HAS45, HAS6>(G, sg, wg, sxq, sxd, sxm, xch);
-}
-
-template <int TYPE, int NC, int KS>
-int launch_ks(const MfArgs &args, hipStream_t stream) {
-    // prefetch depth and chunk (CH a multiple of KS * PF; two chunk buffers in LDS), from a sweep on MI355X of the
-    // 27B shapes at N = 1, 4: fewer registers and smaller chunks beat deeper prefetch at this occupancy
-    constexpr int PF = KS == 1 ? 4 : 2;
-    constexpr int CH = KS * PF;
-    constexpr int ROWS = 64 / KS;
-    const dim3 grid((unsigned)((args.rows + ROWS - 1) / ROWS)), block(256);
-    hipLaunchKernelGGL((kq_mfma_kernel<TYPE, NC, KS, PF, CH>), grid, block, 0, stream, args);
-    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_mfma launch");
-}
-
-// The chunked kernel (activations staged a chunk at a time): the fallback when the whole-K staging does not fit
-// the CU's LDS. K is split across waves when the rows alone give too few waves to keep HBM busy.
-template <int TYPE, int NC>
-int launch_chunked_nc(const MfArgs &args, hipStream_t stream) {
-    const int waves = (args.rows + 15) / 16;
-    if (waves >= 2048 || args.nb < 8) return launch_ks<TYPE, NC, 1>(args, stream);
-    if (waves >= 1024) return launch_ks<TYPE, NC, 2>(args, stream);
-    return launch_ks<TYPE, NC, 4>(args, stream);
-}
-
-template <int TYPE>
-int launch_chunked(const MfArgs &args, size_t ncols, hipStream_t stream) {
-    switch (ncols) {
-    case 1: return launch_chunked_nc<TYPE, 1>(args, stream);
-    case 2: return launch_chunked_nc<TYPE, 2>(args, stream);
-    case 3: return launch_chunked_nc<TYPE, 3>(args, stream);
-    case 4: return launch_chunked_nc<TYPE, 4>(args, stream);
-    case 5: return launch_chunked_nc<TYPE, 5>(args, stream);
-    case 6: return launch_chunked_nc<TYPE, 6>(args, stream);
-    case 7: return launch_chunked_nc<TYPE, 7>(args, stream);
-    case 8: return launch_chunked_nc<TYPE, 8>(args, stream);
-    default: return fail(AQ_EINVAL, "kq_mfma: ncols must be 1..8");
-    }
+        kq_wave_run<T1, NC, KSW, PF, HAS45, HAS6>(G, sg, wg, sxq, sxd, sxm, xw);
 }
 
 constexpr int KQ_LDS_MAX = 160 * 1024 - 512; // a CU's LDS, less a margin
+constexpr int KQ_PF = 4;                      // prefetch depth in rounds
 
-template <int NC>
-constexpr size_t kq_xch_bytes() { return (size_t)2 * 2 * 2 * 3 * NC * 64 * 4; } // the same for KS = 2 and KS = 4
+template <int NC, int KSW>
+constexpr size_t kq_xch_bytes() { return (size_t)4 * KqXch<3 * NC, KSW>::FLOATS * 4; }
 
-template <int T0, int T1, int NC, int KS>
-int launch_group_ks(KqGroup G, size_t lds, hipStream_t stream) {
-    constexpr int PF = 2;
-    constexpr int ROWS = 64 / KS;
+// Host mirror of the kernel's LDS use: the four waves' exchange slots, and the staging per super-block.
+inline size_t kq_xch_bytes_rt(int nc, int ksw) {
+    if (ksw == 1) return 4 * 4;
+    const int nch = 3 * nc, ni = 64 / ksw;
+    const int s = nch * ni + (((ni - nch * ni) % 64) + 64) % 64;
+    return (size_t)4 * ksw * s * 4;
+}
+inline size_t kq_sb_lds_bytes(int nc, bool has45, bool has6) {
+    const int ncp = (nc + 3) / 4 * 4, np = (has45 ? 4 : 0) + (has6 ? 8 : 0);
+    return (size_t)nc * KQ_XS + (size_t)ncp * 4 + (size_t)np * ncp * 4;
+}
+
+// K slices per wave: two, or four when that is what gives the grid about two waves per SIMD (2048 waves). (One
+// slice per wave would need no exchange, but the compiler then copies the prefetch ring at the loop's back edge,
+// which drains every load in flight once per PF rounds.)
+inline int kq_pick_ksw(int rows, int nb) {
+    const long w2 = ((long)rows + 7) / 8;
+    if (nb < 4 || w2 >= 2048) return 2;
+    return 4;
+}
+
+// Super-blocks per activation staging chunk: all of K when the work-group's LDS stays within the budget that
+// leaves room for three work-groups per CU (two above four columns), else the largest multiple of KSW * PF that
+// does (the waves then meet at a barrier between chunks).
+inline int kq_pick_chunk(int nb, int nc, bool has45, bool has6, int ksw) {
+    const size_t budget = (size_t)(nc <= 4 ? 52 : 76) * 1024;
+    const size_t x = kq_xch_bytes_rt(nc, ksw), per = kq_sb_lds_bytes(nc, has45, has6);
+    if (x + per * nb <= budget) return nb;
+    const int unit = ksw * KQ_PF;
+    const int c = (int)((budget - x) / per) / unit * unit;
+    return c < unit ? unit : c;
+}
+
+template <int T0, int T1, int NC, int KSW>
+int launch_wave_ks(KqGroup G, hipStream_t stream) {
+    constexpr int ROWS = 4 * (16 / KSW); // rows per work-group
+    constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
+    constexpr bool HAS45 = T0 != AQ_TYPE_Q6_K || T1 != AQ_TYPE_Q6_K;
+    G.chk = kq_pick_chunk(G.nb, NC, HAS45, HAS6, KSW);
+    const size_t lds = kq_sb_lds_bytes(NC, HAS45, HAS6) * (size_t)(G.chk < G.nb ? G.chk : G.nb);
+    constexpr size_t xch = kq_xch_bytes<NC, KSW>();
+    AQ_REQUIRE(lds + xch <= (size_t)KQ_LDS_MAX, "kq_mfma: activation staging exceeds LDS");
     int wgs = 0;
     for (int i = 0; i < G.nseg; i++) {
         wgs += (G.seg[i].rows + ROWS - 1) / ROWS;
@@ -754,63 +624,38 @@ int launch_group_ks(KqGroup G, size_t lds, hipStream_t stream) {
     if (lds > 64 * 1024) {
         static bool raised = false; // once per instantiation: allow dynamic LDS up to the CU's size
         if (!raised) {
-            const void *fn = reinterpret_cast<const void *>(&kq_group_kernel<T0, T1, NC, KS, PF>);
+            const void *fn = reinterpret_cast<const void *>(&kq_wave_kernel<T0, T1, NC, KSW, KQ_PF>);
             AQ_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)(KQ_LDS_MAX - kq_xch_bytes<NC>())));
+                                       (int)(KQ_LDS_MAX - kq_xch_bytes<NC, KSW>())));
             raised = true;
         }
     }
-    hipLaunchKernelGGL((kq_group_kernel<T0, T1, NC, KS, PF>), dim3((unsigned)wgs), dim3(256), lds, stream, G);
-    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_mfma launch");
+    hipLaunchKernelGGL((kq_wave_kernel<T0, T1, NC, KSW, KQ_PF>), dim3((unsigned)wgs), dim3(256), lds, stream, G);
+    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_wave launch");
 }
 
-// Returns 1 (nothing launched) when the whole-K staging does not fit. The split from a sweep on MI355X of the 27B
-// shapes: long rows (K >= 12288) and tall groups at N > 1 split K in two, the rest in four.
 template <int T0, int T1, int NC>
-int launch_group_nc(const KqGroup &G, int rows, hipStream_t stream) {
-    constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
-    constexpr bool HAS45 = T0 != AQ_TYPE_Q6_K || T1 != AQ_TYPE_Q6_K;
-    const size_t lds = kq_full_lds_bytes(G.nb, NC, HAS45, HAS6);
-    if (lds + kq_xch_bytes<NC>() > (size_t)KQ_LDS_MAX) return 1;
-    if (G.nb >= 48 || (NC > 1 && rows >= 12288)) return launch_group_ks<T0, T1, NC, 2>(G, lds, stream);
-    return launch_group_ks<T0, T1, NC, 4>(G, lds, stream);
+int launch_wave_nc(const KqGroup &G, int rows, hipStream_t stream) {
+    if (kq_pick_ksw(rows, G.nb) == 2) return launch_wave_ks<T0, T1, NC, 2>(G, stream);
+    return launch_wave_ks<T0, T1, NC, 4>(G, stream);
 }
 
 template <int T0, int T1>
-int launch_group_t(const KqGroup &G, int rows, size_t ncols, hipStream_t stream) {
+int launch_wave_t(const KqGroup &G, int rows, size_t ncols, hipStream_t stream) {
     switch (ncols) {
-    case 1: return launch_group_nc<T0, T1, 1>(G, rows, stream);
-    case 2: return launch_group_nc<T0, T1, 2>(G, rows, stream);
-    case 3: return launch_group_nc<T0, T1, 3>(G, rows, stream);
-    case 4: return launch_group_nc<T0, T1, 4>(G, rows, stream);
-    case 5: return launch_group_nc<T0, T1, 5>(G, rows, stream);
-    case 6: return launch_group_nc<T0, T1, 6>(G, rows, stream);
-    case 7: return launch_group_nc<T0, T1, 7>(G, rows, stream);
-    case 8: return launch_group_nc<T0, T1, 8>(G, rows, stream);
+    case 1: return launch_wave_nc<T0, T1, 1>(G, rows, stream);
+    case 2: return launch_wave_nc<T0, T1, 2>(G, rows, stream);
+    case 3: return launch_wave_nc<T0, T1, 3>(G, rows, stream);
+    case 4: return launch_wave_nc<T0, T1, 4>(G, rows, stream);
+    case 5: return launch_wave_nc<T0, T1, 5>(G, rows, stream);
+    case 6: return launch_wave_nc<T0, T1, 6>(G, rows, stream);
+    case 7: return launch_wave_nc<T0, T1, 7>(G, rows, stream);
+    case 8: return launch_wave_nc<T0, T1, 8>(G, rows, stream);
     default: return fail(AQ_EINVAL, "kq_mfma: ncols must be 1..8");
     }
 }
 
-MfArgs single_args(const Weight &w, const Act &x, float *y, const float *resid) {
-    MfArgs args{};
-    args.qa = w.qa;
-    args.qb = w.qb;
-    args.sc = w.sc;
-    args.dm = w.dm;
-    args.rows = (int)w.rows;
-    args.nb = (int)w.nb;
-    args.xqs = x.qs;
-    args.xd = x.d;
-    args.xbs = x.bs;
-    args.xq8s = x.q8s;
-    args.xcol = x.n;
-    args.y = y;
-    args.resid = resid;
-    return args;
-}
-
-// One launch over segments [i0, i1) of at most two K-quant types; the chunked kernel per segment if the staging
-// does not fit.
+// One launch over segments [i0, i1) of at most two K-quant types.
 int launch_run(const Weight *const *ws, float *const *ys, const float *const *resids, int i0, int i1, const Act &x,
                size_t ncols, hipStream_t stream) {
     KqGroup G{};
@@ -837,25 +682,13 @@ int launch_run(const Weight *const *ws, float *const *ys, const float *const *re
         t0 = w.type < t0 ? w.type : t0;
         t1 = w.type > t1 ? w.type : t1;
     }
-    int rc = 1;
     constexpr int Q4 = AQ_TYPE_Q4_K, Q5 = AQ_TYPE_Q5_K, Q6 = AQ_TYPE_Q6_K;
-    if (t0 == Q4 && t1 == Q4) rc = launch_group_t<Q4, Q4>(G, rows, ncols, stream);
-    else if (t0 == Q5 && t1 == Q5) rc = launch_group_t<Q5, Q5>(G, rows, ncols, stream);
-    else if (t0 == Q6 && t1 == Q6) rc = launch_group_t<Q6, Q6>(G, rows, ncols, stream);
-    else if (t0 == Q4 && t1 == Q5) rc = launch_group_t<Q4, Q5>(G, rows, ncols, stream);
-    else if (t0 == Q4 && t1 == Q6) rc = launch_group_t<Q4, Q6>(G, rows, ncols, stream);
-    else if (t0 == Q5 && t1 == Q6) rc = launch_group_t<Q5, Q6>(G, rows, ncols, stream);
-    if (rc != 1) return rc;
-    for (int i = i0; i < i1; i++) {
-        const MfArgs args = single_args(*ws[i], x, ys[i], resids ? resids[i] : nullptr);
-        switch (ws[i]->type) {
-        case Q4: rc = launch_chunked<Q4>(args, ncols, stream); break;
-        case Q5: rc = launch_chunked<Q5>(args, ncols, stream); break;
-        default: rc = launch_chunked<Q6>(args, ncols, stream); break;
-        }
-        if (rc) return rc;
-    }
-    return 0;
+    if (t0 == Q4 && t1 == Q4) return launch_wave_t<Q4, Q4>(G, rows, ncols, stream);
+    if (t0 == Q5 && t1 == Q5) return launch_wave_t<Q5, Q5>(G, rows, ncols, stream);
+    if (t0 == Q6 && t1 == Q6) return launch_wave_t<Q6, Q6>(G, rows, ncols, stream);
+    if (t0 == Q4 && t1 == Q5) return launch_wave_t<Q4, Q5>(G, rows, ncols, stream);
+    if (t0 == Q4 && t1 == Q6) return launch_wave_t<Q4, Q6>(G, rows, ncols, stream);
+    return launch_wave_t<Q5, Q6>(G, rows, ncols, stream);
 }
 
 } // namespace
@@ -868,6 +701,7 @@ int launch_kq_group(const Weight *const *ws, float *const *ys, const float *cons
         AQ_REQUIRE(is_kquant(ws[i]->type), "kq_mfma: not a K-quant type");
         AQ_REQUIRE(ws[i]->nb == ws[0]->nb, "kq_mfma: grouped matrices must share K");
         AQ_REQUIRE(ws[i]->cols == x.n, "kq_mfma: activation length != weight columns");
+        AQ_REQUIRE(ws[i]->rows >= 1 && ws[i]->rows <= (1u << 30), "kq_mfma: rows");
     }
     // consecutive runs of at most KQ_MAXSEG matrices and two types per launch
     int i0 = 0;

@@ -53,16 +53,16 @@ __global__ void __launch_bounds__(256) kq_matmul_kernel(KqArgs a) {
     for (int c = 0; c < NC; c++) acc[c] = accm[c] = 0.0f;
 
     for (int sb = 0; sb < nb; sb++) {
-        const size_t wsb = (size_t)row * nb + sb;
+        const size_t wsb = (size_t)row * nb + sb; // row-major block index (the debug lane-sum output)
         // ---------------------------------------------------------------- weights of this super-block
-        const uint4 qa = *reinterpret_cast<const uint4 *>(a.qa + wsb * 128 + lane_slot(l) * 16);
+        const uint4 qa = *reinterpret_cast<const uint4 *>(a.qa + kq_qa_off(row, sb, nb, l));
         uint32_t code[8]; // 4 unsigned codes per sub-block s, lane l's positions
         int scl[8];       // the integer scale of each of lane l's 8 sub-blocks
         int mn0 = 0, mn1 = 0;
         int off_sc0 = 0, off_sc1 = 0; // Q6_K: scales of groups 2l, 2l+1 (the -32 fold)
         float dw, dminw = 0.0f;
         if constexpr (TYPE == AQ_TYPE_Q4_K || TYPE == AQ_TYPE_Q5_K) {
-            const uint32_t *s12 = reinterpret_cast<const uint32_t *>(a.sc + wsb * 16 + 4);
+            const uint32_t *s12 = reinterpret_cast<const uint32_t *>(a.sc + kq_sc_off(row, sb, nb) + 4);
             const uint32_t q0 = s12[0], q1 = s12[1], q2 = s12[2];
             const uint32_t sc_lo = q0 & 0x3F3F3F3Fu;                                  // sc[0..3]
             const uint32_t mn_lo = q1 & 0x3F3F3F3Fu;                                  // mn[0..3]
@@ -79,7 +79,7 @@ __global__ void __launch_bounds__(256) kq_matmul_kernel(KqArgs a) {
             mn1 = (mnw >> (16 * (l & 1) + 8)) & 0xFF;
             const uint32_t w4[4] = {qa.x, qa.y, qa.z, qa.w};
             uint32_t qh = 0;
-            if constexpr (TYPE == AQ_TYPE_Q5_K) qh = *reinterpret_cast<const uint32_t *>(a.qb + wsb * 32 + lane_slot(l) * 4);
+            if constexpr (TYPE == AQ_TYPE_Q5_K) qh = *reinterpret_cast<const uint32_t *>(a.qb + kq_qb5_off(row, sb, nb, l));
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 code[2 * j] = w4[j] & 0x0F0F0F0Fu;
@@ -89,12 +89,12 @@ __global__ void __launch_bounds__(256) kq_matmul_kernel(KqArgs a) {
                     code[2 * j + 1] |= ((qh >> (2 * j + 1)) & 0x01010101u) << 4;
                 }
             }
-            const uint32_t dmw = *reinterpret_cast<const uint32_t *>(a.sc + wsb * 16);
+            const uint32_t dmw = *reinterpret_cast<const uint32_t *>(a.sc + kq_sc_off(row, sb, nb));
             dw = half_bits_to_float((uint16_t)(dmw & 0xFFFF));
             dminw = half_bits_to_float((uint16_t)(dmw >> 16));
         } else { // Q6_K
-            const uint2 qh2 = *reinterpret_cast<const uint2 *>(a.qb + wsb * 64 + lane_slot(l) * 8);
-            const uint4 s16 = *reinterpret_cast<const uint4 *>(a.sc + wsb * 16);
+            const uint2 qh2 = *reinterpret_cast<const uint2 *>(a.qb + kq_qb6_off(row, sb, nb, l));
+            const uint4 s16 = *reinterpret_cast<const uint4 *>(a.sc + kq_sc_off(row, sb, nb));
             const uint32_t sw[4] = {s16.x, s16.y, s16.z, s16.w};
             const uint32_t ql[4] = {qa.x, qa.y, qa.z, qa.w}; // (h, jj) = 0:(0,0) 1:(0,1) 2:(1,0) 3:(1,1)
             const uint32_t qhw[2] = {qh2.x, qh2.y};
@@ -112,7 +112,7 @@ __global__ void __launch_bounds__(256) kq_matmul_kernel(KqArgs a) {
             const int g0 = 2 * l, g1 = 2 * l + 1;
             off_sc0 = (int)(int8_t)((sw[g0 >> 2] >> (8 * (g0 & 3))) & 0xFF);
             off_sc1 = (int)(int8_t)((sw[g1 >> 2] >> (8 * (g1 & 3))) & 0xFF);
-            dw = half_bits_to_float(*reinterpret_cast<const uint16_t *>(a.dm + wsb * 2));
+            dw = half_bits_to_float(*reinterpret_cast<const uint16_t *>(a.dm + kq_dm_off(row, sb, nb)));
         }
         // ---------------------------------------------------------------- every activation column
 #pragma unroll
@@ -261,10 +261,11 @@ __global__ void __launch_bounds__(256) q8_matmul_kernel(Q8Args a) {
 
 // ---------------------------------------------------------------------------------------------- repack
 // One thread per block: ggml bytes <-> planes (to_planes selects the direction).
-__global__ void repack_kernel(int type, size_t nblocks, uint8_t *ggml, uint8_t *qa, uint8_t *qb, uint8_t *sc,
-                              uint8_t *dm, bool to_planes) {
+__global__ void repack_kernel(int type, size_t nblocks, size_t nb, uint8_t *ggml, uint8_t *qa, uint8_t *qb,
+                              uint8_t *sc, uint8_t *dm, bool to_planes) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
+    const size_t row = i / nb, sb = i % nb; // ggml block i = row * nb + sb
     auto mv = [&](uint8_t *plane_byte, uint8_t *ggml_byte) {
         if (to_planes)
             *plane_byte = *ggml_byte;
@@ -276,27 +277,27 @@ __global__ void repack_kernel(int type, size_t nblocks, uint8_t *ggml, uint8_t *
     case AQ_TYPE_Q5_K: {
         const bool q5 = type == AQ_TYPE_Q5_K;
         uint8_t *g = ggml + i * (q5 ? 176 : 144);
-        for (int b = 0; b < 16; b++) mv(sc + i * 16 + b, g + b); // d, dmin, 12 scale bytes
+        for (int b = 0; b < 16; b++) mv(sc + kq_sc_off(row, sb, nb) + b, g + b); // d, dmin, 12 scale bytes
         if (q5)
             for (int l = 0; l < 8; l++)
-                for (int b = 0; b < 4; b++) mv(qb + i * 32 + lane_slot(l) * 4 + b, g + 16 + 4 * l + b);
+                for (int b = 0; b < 4; b++) mv(qb + kq_qb5_off(row, sb, nb, l) + b, g + 16 + 4 * l + b);
         uint8_t *qs = g + (q5 ? 48 : 16);
         for (int l = 0; l < 8; l++)
             for (int j = 0; j < 4; j++)
-                for (int b = 0; b < 4; b++) mv(qa + i * 128 + lane_slot(l) * 16 + j * 4 + b, qs + 32 * j + 4 * l + b);
+                for (int b = 0; b < 4; b++) mv(qa + kq_qa_off(row, sb, nb, l) + j * 4 + b, qs + 32 * j + 4 * l + b);
         break;
     }
     case AQ_TYPE_Q6_K: {
         uint8_t *g = ggml + i * 210;
         for (int l = 0; l < 8; l++)
             for (int h = 0; h < 2; h++) {
-                const int sl = lane_slot(l);
                 for (int jj = 0; jj < 2; jj++)
-                    for (int b = 0; b < 4; b++) mv(qa + i * 128 + sl * 16 + (h * 2 + jj) * 4 + b, g + h * 64 + jj * 32 + 4 * l + b);
-                for (int b = 0; b < 4; b++) mv(qb + i * 64 + sl * 8 + h * 4 + b, g + 128 + h * 32 + 4 * l + b);
+                    for (int b = 0; b < 4; b++)
+                        mv(qa + kq_qa_off(row, sb, nb, l) + (h * 2 + jj) * 4 + b, g + h * 64 + jj * 32 + 4 * l + b);
+                for (int b = 0; b < 4; b++) mv(qb + kq_qb6_off(row, sb, nb, l) + h * 4 + b, g + 128 + h * 32 + 4 * l + b);
             }
-        for (int b = 0; b < 16; b++) mv(sc + i * 16 + b, g + 192 + b);
-        for (int b = 0; b < 2; b++) mv(dm + i * 2 + b, g + 208 + b);
+        for (int b = 0; b < 16; b++) mv(sc + kq_sc_off(row, sb, nb) + b, g + 192 + b);
+        for (int b = 0; b < 2; b++) mv(dm + kq_dm_off(row, sb, nb) + b, g + 208 + b);
         break;
     }
     case AQ_TYPE_Q8_0: {
@@ -492,8 +493,8 @@ int launch_kq_isums(const Weight &w, const Act &x, int32_t *lanes, int32_t *mins
 int launch_repack(Weight &w, const uint8_t *ggml_dev, bool to_planes, hipStream_t stream) {
     const size_t nblocks = w.rows * w.nb;
     const unsigned grid = (unsigned)((nblocks + 255) / 256);
-    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, stream, w.type, nblocks, const_cast<uint8_t *>(ggml_dev),
-                       w.qa, w.qb, w.sc, w.dm, to_planes);
+    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, stream, w.type, nblocks, w.nb,
+                       const_cast<uint8_t *>(ggml_dev), w.qa, w.qb, w.sc, w.dm, to_planes);
     return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "repack launch");
 }
 

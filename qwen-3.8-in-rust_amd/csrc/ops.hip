@@ -20,11 +20,10 @@ __global__ void __launch_bounds__(256) embed_q4k_kernel(Weight w, const uint32_t
     const size_t i = blockIdx.y, sb = blockIdx.x;
     size_t row = ids[i];
     if (row >= w.rows) row = w.rows - 1; // ids are validated by the host; keep every access in bounds regardless
-    const size_t wsb = row * w.nb + sb;
     const int e = threadIdx.x, s = e >> 5, p = e & 31, l = p >> 2, b = p & 3;
-    const uint8_t byte = w.qa[wsb * 128 + lane_slot(l) * 16 + (s >> 1) * 4 + b];
+    const uint8_t byte = w.qa[kq_qa_off(row, sb, w.nb, l) + (s >> 1) * 4 + b];
     const int q = (s & 1) ? (byte >> 4) : (byte & 0xF);
-    const uint8_t *rec = w.sc + wsb * 16;
+    const uint8_t *rec = w.sc + kq_sc_off(row, sb, w.nb);
     const float d = f16_to_f32((uint16_t)(rec[0] | (rec[1] << 8)));
     const float dmin = f16_to_f32((uint16_t)(rec[2] | (rec[3] << 8)));
     const uint8_t *sc12 = rec + 4;

@@ -38,7 +38,7 @@ static int alloc_weight(Weight &w, int type, size_t rows, size_t cols, int devic
     case AQ_TYPE_Q4_0: w.qa_bytes = 16; w.qb_bytes = 0; w.sc_bytes = 0; w.dm_bytes = 2; break;
     default: w.qa_bytes = 4; w.qb_bytes = 0; w.sc_bytes = 0; w.dm_bytes = 0; break;
     }
-    const size_t nbl = rows * w.nb;
+    const size_t nbl = (is_kquant(type) ? (rows + 3) / 4 * 4 : rows) * w.nb; // K-quant tiles hold 4 rows
     const size_t sa = align256(nbl * w.qa_bytes), sb = align256(nbl * w.qb_bytes), ss = align256(nbl * w.sc_bytes),
                  sd = align256(nbl * w.dm_bytes);
     w.total = sa + sb + ss + sd;
