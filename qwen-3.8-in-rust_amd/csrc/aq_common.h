@@ -125,8 +125,9 @@ int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const f
 int launch_kq_isums(const Weight &w, const Act &x, int32_t *lanes, int32_t *mins, hipStream_t stream);
 // The matrix-core K-quant kernel (kq_mfma.hip); launch_matmul routes K-quant weights here.
 int launch_kq_mfma(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
-// n K-quant matrices of one K that read the same activations (y_i = W_i x [+ resid_i]), as few launches as their
-// types allow (up to three matrices and two types per launch). resids may be null.
+// n matrices that read the same activations (y_i = W_i x [+ resid_i]): K-quants of one K, as few launches as
+// their types allow (up to three matrices and two types per launch), then at most two F32 matrices that join the
+// last launch. resids may be null.
 int launch_kq_group(const Weight *const *ws, float *const *ys, const float *const *resids, int n, const Act &x,
                     size_t ncols, hipStream_t stream);
 // The v_dot4 K-quant kernel (matmul.hip), kept as the second implementation the tests compare against.

@@ -22,6 +22,9 @@
 //    rounds deep; activations are staged in LDS (all of K, or chunks of it) once per work-group.
 #include "aq_common.h"
 
+#include <map>
+#include <mutex>
+
 namespace aq {
 namespace {
 
@@ -317,17 +320,19 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
 // DeltaNet qkv and z projections): the work-groups are laid out segment after segment, each segment with its own
 // weights, output and K-quant type (one of the kernel's two types), so the staging and the launch are shared.
 constexpr int KQ_XS = 272;
-constexpr int KQ_MAXSEG = 3;
+constexpr int KQ_MAXSEG = 5; // up to three K-quant segments plus two F32 ones
 
 struct KqSeg {
     const uint8_t *qa, *qb, *sc, *dm;
     float *y;
     const float *resid;
     int rows, type, wg_end; // wg_end: one past this segment's last work-group
+    int nwg;                // this segment's work-groups
 };
 struct KqGroup {
     KqSeg seg[KQ_MAXSEG];
     int nseg, nb;
+    const float *xf; // the f32 activation rows (F32 segments)
     int chk; // super-blocks per activation staging chunk: nb, or a multiple of KSW * PF
     const int8_t *xqs;
     const float *xd;
@@ -391,17 +396,22 @@ struct KqXch {
 template <int NC>
 constexpr int kq_nch_max() { return 3 * NC; }
 
-// One wave's rows of one segment: the products of its K slice each round, the in-order chains, the lane
-// reduction ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)) [+ (m0+m2)+(m1+m3)] (kdot.rs:1-18) and the store.
+// One wave's share of one segment: tiles of RW = 16 / KSW rows, the wave's tiles being gw, gw + nw, ... (gw the
+// wave's index within the segment, nw the segment's waves). The rounds of all its tiles form one stream, so the
+// weight ring runs on across tile boundaries. Per round: the products of the K slice, handed to the chain owners
+// through the wave's LDS slot; per tile: the lane reduction ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)) [+ (m0+m2)+(m1+m3)]
+// (kdot.rs:1-18) and the store. With chunked staging (G.chk < nb) every wave runs exactly one tile (idle ones on
+// clamped rows), because all waves of the work-group meet at the chunk barriers.
 template <int TYPE, int NC, int KSW, int PF, bool HAS45, bool HAS6>
 __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, int wg, int8_t *sxq, float *sxd,
                                             uint32_t *sxm, float *xw) {
-    constexpr int RW = 16 / KSW;                        // rows per wave
+    static_assert(KSW == 2 || KSW == 4, "K slices per wave");
+    constexpr int RW = 16 / KSW;                        // rows per tile
     constexpr int NCP = (NC + 3) / 4 * 4;
     constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
     constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), POFF = Q6 && HAS45 ? 4 : 0;
     constexpr int NCH = (Q6 ? 2 : 3) * NC;              // f32 chains of one (row, lane pair): j, j+4, min j
-    constexpr int NO = KSW > 1 ? (NCH + KSW - 1) / KSW : NCH; // chains this thread keeps
+    constexpr int NO = (NCH + KSW - 1) / KSW;           // chains this thread keeps
     using X = KqXch<3 * NC, KSW>;                       // slot sized for the largest NCH of the kernel
     constexpr int NI = X::NI;
     MfArgs a{};
@@ -416,30 +426,81 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
     const int b = lane >> 2, r = lane & 3, j = b & 3, q = b >> 2;
     const int rg = q / KSW, ks = q % KSW;
     const int idx = (rg * 4 + j) * 4 + r; // chain owner index within the wave (0..NI-1)
-    const int row0 = (wg * 4 + wid) * RW;
-    int row = row0 + rg * 4 + r;
-    const bool valid = row < a.rows;
-    if (!valid) row = a.rows - 1;
-    const size_t tile0 = (size_t)(row >> 2) * nb; // this row group's first tile
-    const int rr = row & 3;
+    const int chk = G.chk;
+    const int ntile = (a.rows + RW - 1) / RW;
+    const int gw = wg * 4 + wid, nw = sg.nwg * 4;
+    int mt = gw < ntile ? (ntile - 1 - gw) / nw + 1 : 0; // tiles of this wave
+    if (chk < nb) mt = 1;                                 // chunked: one tile per wave (idle waves included)
+    const int nr = (nb + KSW - 1) / KSW;                  // rounds per tile
+    const int nit = mt * nr;
+    // this thread's weight row in tile k of the wave (clamped into the matrix), and its row group's first tile
+    auto tile_row = [&](int k) {
+        const int rw0 = (gw + k * nw) * RW;
+        const int rr_ = rw0 + rg * 4 + r;
+        return rr_ < a.rows ? rr_ : a.rows - 1;
+    };
+    // the prefetch cursor: tile pk (clamped to the wave's last tile), round prd
+    int pk = 0, prd = 0;
+    size_t ptile0 = (size_t)(tile_row(0) >> 2) * nb;
+    int prr = tile_row(0) & 3;
+    auto issue = [&](WRegs<TYPE> &wv) {
+        load_w<TYPE>(wv, a, ptile0 + min(prd * KSW + ks, nb - 1), prr, j);
+        if (++prd == nr) {
+            prd = 0;
+            if (pk + 1 < mt) {
+                pk++;
+                const int row = tile_row(pk);
+                ptile0 = (size_t)(row >> 2) * nb;
+                prr = row & 3;
+            }
+        }
+    };
     WRegs<TYPE> wr[PF];
 
     // the first PF rounds of weights fly while the activations are staged
 #pragma unroll
-    for (int p = 0; p < PF; p++) load_w<TYPE>(wr[p], a, tile0 + min(p * KSW + ks, nb - 1), rr, j);
-    const int chk = G.chk;
+    for (int p = 0; p < PF; p++) issue(wr[p]);
     kq_stage<NC, HAS45, HAS6>(G, sxq, sxd, sxm, 0, chk < nb ? chk : nb);
     __syncthreads();
-    if (row0 >= a.rows && chk >= nb) return; // no barrier follows (with chunks, idle waves keep the barriers)
+    if (nit == 0) return; // no barrier follows (with chunks every wave has a tile)
     int s0 = 0; // first super-block of the staged chunk
 
     float acc[NO];
 #pragma unroll
     for (int i = 0; i < NO; i++) acc[i] = 0.0f;
-    const int nr = (nb + KSW - 1) / KSW; // rounds
+    int ck = 0, crd = 0; // the compute cursor: tile, round
 
-    auto round_body = [&](WRegs<TYPE> &wv, const int rd, const bool prefetch) {
-        const int sb = rd * KSW + ks;
+    // a finished tile: every owner's final chains to the slot [chain][owner], then one lane per (row, column)
+    auto finish_tile = [&]() {
+#pragma unroll
+        for (int m = 0; m < NO; m++) {
+            const int k = ks + KSW * m;
+            if (k < NCH) xw[k * NI + idx] = acc[m];
+            acc[m] = 0.0f;
+        }
+        __asm__ volatile("" ::: "memory");
+        if (lane < RW * NC) {
+            const int col = lane / RW, rw = lane % RW;
+            const int orow = (gw + ck * nw) * RW + rw;
+            const int base = (rw >> 2) * 16 + (rw & 3); // idx of lane pair 0 of this row
+            float a0[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) a0[jj] = xw[col * NI + base + 4 * jj] + xw[(NC + col) * NI + base + 4 * jj];
+            float v = (a0[0] + a0[2]) + (a0[1] + a0[3]);
+            if constexpr (!Q6) {
+                const float *m = xw + (2 * NC + col) * NI + base;
+                v = v + ((m[0] + m[8]) + (m[4] + m[12]));
+            }
+            if (orow < a.rows) {
+                const size_t o = (size_t)col * a.rows + orow;
+                sg.y[o] = sg.resid ? sg.resid[o] + v : v;
+            }
+        }
+        __asm__ volatile("" ::: "memory");
+    };
+
+    auto round_body = [&](WRegs<TYPE> &wv, const bool prefetch) {
+        const int sb = crd * KSW + ks;
         const int sbc = sb < nb ? sb : nb - 1;
         float pr[3][NC];
 #pragma unroll
@@ -456,92 +517,122 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
             // the refill goes into the registers just consumed: every use of the old values stays above it, so
             // the ring keeps its registers across the loop's back edge (no copies, no drain of the loads in flight)
             __builtin_amdgcn_sched_barrier(0);
-            load_w<TYPE>(wv, a, tile0 + min(sb + PF * KSW, nb - 1), rr, j);
+            issue(wv);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (KSW == 1) {
+        const int live = nb - crd * KSW < KSW ? nb - crd * KSW : KSW; // super-blocks in this round
 #pragma unroll
-            for (int k = 0; k < NCH; k++) acc[k] += pr[k / NC][k % NC];
-        } else {
-            const int live = nb - rd * KSW < KSW ? nb - rd * KSW : KSW; // super-blocks in this round
+        for (int k = 0; k < NCH; k++) xw[ks * X::S + k * NI + idx] = pr[k / NC][k % NC];
+        __asm__ volatile("" ::: "memory");
 #pragma unroll
-            for (int k = 0; k < NCH; k++) xw[ks * X::S + k * NI + idx] = pr[k / NC][k % NC];
-            __asm__ volatile("" ::: "memory");
+        for (int m = 0; m < NO; m++) {
+            const int k = ks + KSW * m;
+            if (k < NCH) {
 #pragma unroll
-            for (int m = 0; m < NO; m++) {
-                const int k = ks + KSW * m;
-                if (k < NCH) {
-#pragma unroll
-                    for (int k2 = 0; k2 < KSW; k2++)
-                        if (k2 < live) acc[m] += xw[k2 * X::S + k * NI + idx];
-                }
+                for (int k2 = 0; k2 < KSW; k2++)
+                    if (k2 < live) acc[m] += xw[k2 * X::S + k * NI + idx];
             }
-            __asm__ volatile("" ::: "memory");
+        }
+        __asm__ volatile("" ::: "memory");
+        if (++crd == nr) { // uniform across the wave
+            finish_tile();
+            crd = 0;
+            ck++;
         }
     };
-    // the next staging chunk when round rd starts past the staged one (chunks hold whole groups of PF rounds)
-    auto next_chunk = [&](const int rd) {
-        if (rd * KSW >= s0 + chk) { // uniform across the work-group
+    // the next staging chunk when round crd starts past the staged one (chunks hold whole groups of PF rounds;
+    // chunked launches run one tile per wave, so the round counter is the item counter)
+    auto next_chunk = [&]() {
+        if (crd * KSW >= s0 + chk) { // uniform across the work-group
             __syncthreads();
             s0 += chk;
             kq_stage<NC, HAS45, HAS6>(G, sxq, sxd, sxm, s0, nb - s0 < chk ? nb - s0 : chk);
             __syncthreads();
         }
     };
-    const int nfull = nr / PF * PF;
-    for (int rd = 0; rd < nfull; rd += PF) {
-        next_chunk(rd);
+    const int nfull = nit / PF * PF;
+    for (int i = 0; i < nfull; i += PF) {
+        next_chunk();
 #pragma unroll
-        for (int p = 0; p < PF; p++) round_body(wr[p], rd + p, true);
+        for (int p = 0; p < PF; p++) round_body(wr[p], true);
     }
-    if (nfull < nr) next_chunk(nfull);
+    if (nfull < nit) next_chunk();
 #pragma unroll
     for (int p = 0; p < PF; p++)
-        if (nfull + p < nr) round_body(wr[p], nfull + p, false);
+        if (nfull + p < nit) round_body(wr[p], false);
+}
 
-    if constexpr (KSW == 1) {
-        // lanes j and j+4 are in one thread; j sits at lane 16g + 4j + r: xor 8 pairs j with j^2, xor 4 with j^1
+// An F32 segment (the DeltaNet ssm_alpha / ssm_beta rows, dot.rs:180-200 via matvec.rs:270-279): one row per wave;
+// lane l takes 32-element blocks l, l + 64, ...: each block's partial is a left-to-right sum from 0 (product, then
+// add), written to LDS; then lane c chains column c's partials block by block, and the reference's `acc + part`
+// with the absent tail adds 0.0f when n is a multiple of 32. `part` holds 4 x NC x ceil(n / 32) floats.
+template <int NC>
+__device__ __forceinline__ void kq_f32_run(const KqGroup &G, const KqSeg &sg, int wg, float *part) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int row = wg * 4 + wid;
+    if (row >= sg.rows) return;
+    const int n = (int)G.xcol, nblk = (n + 31) / 32;
+    float *pw = part + (size_t)wid * NC * nblk;
+    const float *w = reinterpret_cast<const float *>(sg.qa) + (size_t)row * n;
+    for (int b = lane; b < nblk; b += 64) {
+        const int e0 = b * 32, ne = n - e0 < 32 ? n - e0 : 32;
+        if (ne == 32) {
+            float wv[32];
 #pragma unroll
-        for (int col = 0; col < NC; col++) {
-            float v = acc[col] + acc[NC + col]; // l_j + l_{j+4}
-            v = v + __shfl_xor(v, 8);
-            v = v + __shfl_xor(v, 4);
-            if constexpr (!Q6) {
-                float m = acc[2 * NC + col];
-                m = m + __shfl_xor(m, 8); // m0+m2, m1+m3
-                m = m + __shfl_xor(m, 4);
-                v = v + m;
+            for (int u = 0; u < 8; u++) {
+                const float4 f = *reinterpret_cast<const float4 *>(w + e0 + 4 * u);
+                wv[4 * u] = f.x, wv[4 * u + 1] = f.y, wv[4 * u + 2] = f.z, wv[4 * u + 3] = f.w;
             }
-            if (j == 0 && valid) {
-                const size_t o = (size_t)col * a.rows + row;
-                sg.y[o] = sg.resid ? sg.resid[o] + v : v;
+            // up to four columns' chains interleaved (independent sums, each still left to right)
+#pragma unroll
+            for (int c0 = 0; c0 < NC; c0 += 4) {
+                constexpr int G4 = NC < 4 ? NC : 4;
+                float xv[G4][32];
+#pragma unroll
+                for (int g = 0; g < G4; g++) {
+                    const float *xr = G.xf + (size_t)(c0 + g < NC ? c0 + g : NC - 1) * n + e0;
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        const float4 f = *reinterpret_cast<const float4 *>(xr + 4 * u);
+                        xv[g][4 * u] = f.x, xv[g][4 * u + 1] = f.y, xv[g][4 * u + 2] = f.z, xv[g][4 * u + 3] = f.w;
+                    }
+                }
+                float pt[G4];
+#pragma unroll
+                for (int g = 0; g < G4; g++) pt[g] = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 32; e++)
+#pragma unroll
+                    for (int g = 0; g < G4; g++) pt[g] += wv[e] * xv[g][e];
+#pragma unroll
+                for (int g = 0; g < G4; g++)
+                    if (c0 + g < NC) pw[(c0 + g) * nblk + b] = pt[g];
+            }
+        } else {
+            for (int c = 0; c < NC; c++) {
+                const float *xr = G.xf + (size_t)c * n + e0;
+                float pt = 0.0f;
+                for (int e = 0; e < ne; e++) pt += w[e0 + e] * xr[e];
+                pw[c * nblk + b] = pt;
             }
         }
-    } else {
-        // every owner's final chains to the slot [chain][owner], then one lane per (row, column) output
+    }
+    __asm__ volatile("" ::: "memory"); // the wave's partials are in LDS before its chain lanes read them
+    if (lane < NC) {
+        const float *pc = pw + lane * nblk;
+        float acc = 0.0f;
+        int b = 0;
+        for (; b + 16 <= nblk; b += 16) { // 16 reads in flight, the sum still in block order
+            float v[16];
 #pragma unroll
-        for (int m = 0; m < NO; m++) {
-            const int k = ks + KSW * m;
-            if (k < NCH) xw[k * NI + idx] = acc[m];
-        }
-        __asm__ volatile("" ::: "memory");
-        if (lane < RW * NC) {
-            const int col = lane / RW, rw = lane % RW;
-            const int orow = row0 + rw;
-            const int base = (rw >> 2) * 16 + (rw & 3); // idx of lane pair 0 of this row
-            float a0[4];
+            for (int u = 0; u < 16; u++) v[u] = pc[b + u];
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) a0[jj] = xw[col * NI + base + 4 * jj] + xw[(NC + col) * NI + base + 4 * jj];
-            float v = (a0[0] + a0[2]) + (a0[1] + a0[3]);
-            if constexpr (!Q6) {
-                const float *m = xw + (2 * NC + col) * NI + base;
-                v = v + ((m[0] + m[8]) + (m[4] + m[12]));
-            }
-            if (orow < a.rows) {
-                const size_t o = (size_t)col * a.rows + orow;
-                sg.y[o] = sg.resid ? sg.resid[o] + v : v;
-            }
+            for (int u = 0; u < 16; u++) acc += v[u];
         }
+        for (; b < nblk; b++) acc += pc[b];
+        if (n % 32 == 0) acc = acc + 0.0f;
+        const size_t o = (size_t)lane * sg.rows + row;
+        sg.y[o] = sg.resid ? sg.resid[o] + acc : acc;
     }
 }
 
@@ -557,6 +648,10 @@ __global__ void __launch_bounds__(256) kq_wave_kernel(KqGroup G) {
     while (si + 1 < G.nseg && (int)blockIdx.x >= G.seg[si].wg_end) si++;
     const KqSeg &sg = G.seg[si];
     const int wg = (int)blockIdx.x - (si ? G.seg[si - 1].wg_end : 0);
+    if (sg.type == AQ_TYPE_F32) { // uniform: F32 work-groups stage nothing and meet no barrier
+        kq_f32_run<NC>(G, sg, wg, reinterpret_cast<float *>(kq_lds));
+        return;
+    }
     const int ns = G.chk < G.nb ? G.chk : G.nb; // super-blocks staged at a time
     int8_t *sxq = reinterpret_cast<int8_t *>(kq_lds);
     float *sxd = reinterpret_cast<float *>(kq_lds + (size_t)ns * NC * KQ_XS);
@@ -586,13 +681,22 @@ inline size_t kq_sb_lds_bytes(int nc, bool has45, bool has6) {
     return (size_t)nc * KQ_XS + (size_t)ncp * 4 + (size_t)np * ncp * 4;
 }
 
-// K slices per wave: two, or four when that is what gives the grid about two waves per SIMD (2048 waves). (One
-// slice per wave would need no exchange, but the compiler then copies the prefetch ring at the loop's back edge,
-// which drains every load in flight once per PF rounds.)
-inline int kq_pick_ksw(int rows, int nb) {
-    const long w2 = ((long)rows + 7) / 8;
-    if (nb < 4 || w2 >= 2048) return 2;
-    return 4;
+// K slices per wave: four (tiles of 4 rows, so work divides finely over the waves), two for K below 4 super-blocks.
+inline int kq_pick_ksw(int nb) { return nb < 4 ? 2 : 4; }
+
+// Work-groups of `fn` (256 threads, `lds` dynamic bytes) resident on the whole device at once.
+inline int kq_capacity(const void *fn, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<const void *, size_t>, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(fn, lds);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess)
+        return 0;
+    return cache[key] = per_cu * cus;
 }
 
 // Super-blocks per activation staging chunk: all of K when the work-group's LDS stays within the budget that
@@ -607,28 +711,58 @@ inline int kq_pick_chunk(int nb, int nc, bool has45, bool has6, int ksw) {
     return c < unit ? unit : c;
 }
 
+// Grid: one tile per wave when all tiles fit the device in one pass (or the staging is chunked); otherwise a
+// persistent grid of exactly the resident work-groups, shared between the segments by weight bytes, each wave then
+// streaming several tiles.
 template <int T0, int T1, int NC, int KSW>
 int launch_wave_ks(KqGroup G, hipStream_t stream) {
-    constexpr int ROWS = 4 * (16 / KSW); // rows per work-group
+    constexpr int RW = 16 / KSW; // rows per tile
     constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
     constexpr bool HAS45 = T0 != AQ_TYPE_Q6_K || T1 != AQ_TYPE_Q6_K;
     G.chk = kq_pick_chunk(G.nb, NC, HAS45, HAS6, KSW);
     const size_t lds = kq_sb_lds_bytes(NC, HAS45, HAS6) * (size_t)(G.chk < G.nb ? G.chk : G.nb);
     constexpr size_t xch = kq_xch_bytes<NC, KSW>();
     AQ_REQUIRE(lds + xch <= (size_t)KQ_LDS_MAX, "kq_mfma: activation staging exceeds LDS");
-    int wgs = 0;
-    for (int i = 0; i < G.nseg; i++) {
-        wgs += (G.seg[i].rows + ROWS - 1) / ROWS;
-        G.seg[i].wg_end = wgs;
-    }
+    const void *fn = reinterpret_cast<const void *>(&kq_wave_kernel<T0, T1, NC, KSW, KQ_PF>);
     if (lds > 64 * 1024) {
         static bool raised = false; // once per instantiation: allow dynamic LDS up to the CU's size
         if (!raised) {
-            const void *fn = reinterpret_cast<const void *>(&kq_wave_kernel<T0, T1, NC, KSW, KQ_PF>);
-            AQ_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)(KQ_LDS_MAX - kq_xch_bytes<NC, KSW>())));
+            AQ_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(KQ_LDS_MAX - xch)));
             raised = true;
         }
+    }
+    long tiles = 0, f32_wgs = 0;
+    double bytes = 0.0;
+    for (int i = 0; i < G.nseg; i++) {
+        const KqSeg &sg = G.seg[i];
+        if (sg.type == AQ_TYPE_F32) {
+            AQ_REQUIRE((size_t)4 * NC * ((G.xcol + 31) / 32) * 4 <= lds, "kq_mfma: F32 partials exceed the LDS");
+            f32_wgs += (sg.rows + 3) / 4; // four rows per work-group, partials in the staging LDS
+            continue;
+        }
+        const long t = (sg.rows + RW - 1) / RW;
+        tiles += t;
+        bytes += (double)t * block_bytes(sg.type);
+    }
+    const long cap = kq_capacity(fn, lds) - f32_wgs;
+    const bool persistent = G.chk >= G.nb && cap >= G.nseg && tiles > 4 * cap;
+    int wgs = 0;
+    for (int i = 0; i < G.nseg; i++) {
+        KqSeg &sg = G.seg[i];
+        long n;
+        if (sg.type == AQ_TYPE_F32) {
+            n = (sg.rows + 3) / 4;
+        } else {
+            const long t = (sg.rows + RW - 1) / RW, need = (t + 3) / 4;
+            n = need;
+            if (persistent) {
+                n = (long)((double)cap * ((double)t * block_bytes(sg.type)) / bytes);
+                n = n < 1 ? 1 : (n > need ? need : n);
+            }
+        }
+        sg.nwg = (int)n;
+        wgs += (int)n;
+        sg.wg_end = wgs;
     }
     hipLaunchKernelGGL((kq_wave_kernel<T0, T1, NC, KSW, KQ_PF>), dim3((unsigned)wgs), dim3(256), lds, stream, G);
     return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_wave launch");
@@ -636,7 +770,8 @@ int launch_wave_ks(KqGroup G, hipStream_t stream) {
 
 template <int T0, int T1, int NC>
 int launch_wave_nc(const KqGroup &G, int rows, hipStream_t stream) {
-    if (kq_pick_ksw(rows, G.nb) == 2) return launch_wave_ks<T0, T1, NC, 2>(G, stream);
+    (void)rows;
+    if (kq_pick_ksw(G.nb) == 2) return launch_wave_ks<T0, T1, NC, 2>(G, stream);
     return launch_wave_ks<T0, T1, NC, 4>(G, stream);
 }
 
@@ -666,6 +801,7 @@ int launch_run(const Weight *const *ws, float *const *ys, const float *const *re
     G.xbs = x.bs;
     G.xq8s = x.q8s;
     G.xcol = x.n;
+    G.xf = x.f32;
     int t0 = 99, t1 = 0, rows = 0;
     for (int i = i0; i < i1; i++) {
         const Weight &w = *ws[i];
@@ -678,6 +814,7 @@ int launch_run(const Weight *const *ws, float *const *ys, const float *const *re
         sg.resid = resids ? resids[i] : nullptr;
         sg.rows = (int)w.rows;
         sg.type = w.type;
+        if (w.type == AQ_TYPE_F32) continue;
         rows += (int)w.rows;
         t0 = w.type < t0 ? w.type : t0;
         t1 = w.type > t1 ? w.type : t1;
@@ -697,17 +834,20 @@ int launch_kq_group(const Weight *const *ws, float *const *ys, const float *cons
                     size_t ncols, hipStream_t stream) {
     AQ_REQUIRE(n >= 1 && ws && ys, "kq_mfma: no matrices");
     AQ_REQUIRE(ncols >= 1 && ncols <= 8, "kq_mfma: ncols must be 1..8");
+    int nq = 0; // the K-quant matrices come first; F32 ones (at most two) ride in the last launch
+    while (nq < n && ws[nq]->type != AQ_TYPE_F32) nq++;
+    AQ_REQUIRE(nq >= 1 && n - nq <= 2, "kq_mfma: K-quant matrices first, then at most two F32 ones");
     for (int i = 0; i < n; i++) {
-        AQ_REQUIRE(is_kquant(ws[i]->type), "kq_mfma: not a K-quant type");
-        AQ_REQUIRE(ws[i]->nb == ws[0]->nb, "kq_mfma: grouped matrices must share K");
+        AQ_REQUIRE(i < nq ? is_kquant(ws[i]->type) : ws[i]->type == AQ_TYPE_F32, "kq_mfma: matrix types");
+        AQ_REQUIRE(ws[i]->nb == ws[0]->nb || ws[i]->type == AQ_TYPE_F32, "kq_mfma: grouped matrices must share K");
         AQ_REQUIRE(ws[i]->cols == x.n, "kq_mfma: activation length != weight columns");
         AQ_REQUIRE(ws[i]->rows >= 1 && ws[i]->rows <= (1u << 30), "kq_mfma: rows");
     }
-    // consecutive runs of at most KQ_MAXSEG matrices and two types per launch
+    // consecutive runs of at most three K-quant matrices and two types per launch
     int i0 = 0;
-    while (i0 < n) {
+    while (i0 < nq) {
         int i1 = i0 + 1, ta = ws[i0]->type, tb = ta;
-        while (i1 < n && i1 - i0 < KQ_MAXSEG) {
+        while (i1 < nq && i1 - i0 < 3) {
             const int t = ws[i1]->type;
             if (t != ta && t != tb) {
                 if (ta != tb) break;
@@ -715,6 +855,7 @@ int launch_kq_group(const Weight *const *ws, float *const *ys, const float *cons
             }
             i1++;
         }
+        if (i1 == nq) i1 = n; // the F32 segments join the last launch
         const int rc = launch_run(ws, ys, resids, i0, i1, x, ncols, stream);
         if (rc) return rc;
         i0 = i1;

@@ -246,16 +246,148 @@ __global__ void __launch_bounds__(256) q8_matmul_kernel(Q8Args a) {
         const int orow = (int)blockIdx.x * RPB + rr;
         if (orow < a.rows) {
             float acc = 0.0f;
-            if (a.type == AQ_TYPE_F32) {
-                // dot.rs:180-200: full blocks, then `acc + part` with the tail's partial (0.0f when there is none)
-                for (int b = 0; b < nb; b++) acc += prods[(rr * nb + b) * NC + c];
-                if (a.n % 32 == 0) acc = acc + 0.0f;
-            } else {
-                for (int b = 0; b < nb; b++) acc += prods[(rr * nb + b) * NC + c];
+            const float *pc = prods + (size_t)rr * nb * NC + c;
+            int b = 0;
+            for (; b + 16 <= nb; b += 16) { // 16 reads in flight, the sum still in block order
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) v[u] = pc[(b + u) * NC];
+#pragma unroll
+                for (int u = 0; u < 16; u++) acc += v[u];
             }
+            for (; b < nb; b++) acc += pc[b * NC];
+            // dot.rs:180-200 (F32): full blocks, then `acc + part` with the tail's partial (0.0f when there is none)
+            if (a.type == AQ_TYPE_F32 && a.n % 32 == 0) acc = acc + 0.0f;
             const size_t o = (size_t)c * a.rows + orow;
             a.y[o] = a.resid ? a.resid[o] + acc : acc;
         }
+    }
+}
+
+// ------------------------------------------------------------------------------------ Q8_0 / Q4_0 by waves
+// dot.rs:29-66 per 32-block: isum = the exact integer dot of the codes (Q4_0: codes q - 8, taken as
+// sum(q*x) - 8*sum(x)), then acc += (dw * dx) * float(isum) block after block: one chain per (row, column).
+// A wave owns RPW rows; lane (r, ks) = KS*r + ks (KS = 64 / RPW) computes, in round rd, block KS*rd + ks of row r
+// for every column. The KS products of a (row, column) go through the wave's LDS slot to its chain owner, lane
+// RPW*c + r, which adds them in block order (no work-group barrier: one wave's LDS accesses execute in order).
+// Weights stream through a register ring Q8W_PF rounds deep; the activations (codes, f32 scales, Q4_0 code sums)
+// are staged in LDS once per work-group. Few rows per wave keep short matrices (5120 rows) at several waves per
+// SIMD.
+constexpr int Q8W_PF = 4;
+
+template <int TYPE>
+struct Q8Regs {
+    uint4 c0, c1; // Q8_0: 32 codes; Q4_0: c0 = 16 bytes of nibbles
+    uint32_t d;   // f16 scale bits
+};
+
+template <int TYPE, int NC, int RPW>
+__global__ void __launch_bounds__(256) q8_wave_kernel(Q8Args a) {
+    extern __shared__ __align__(16) uint8_t q8_lds[];
+    constexpr bool Q4 = TYPE == AQ_TYPE_Q4_0;
+    constexpr int KS = 64 / RPW;
+    const int nb = a.nb32;
+    int8_t *sx = reinterpret_cast<int8_t *>(q8_lds);                   // [nb][NC][32]
+    float *sxd = reinterpret_cast<float *>(q8_lds + (size_t)nb * NC * 32); // [nb][NC]
+    int32_t *sxs = reinterpret_cast<int32_t *>(sxd + (size_t)nb * NC);   // [nb][NC]
+    float *xch = reinterpret_cast<float *>(sxs + (size_t)nb * NC);       // [4 waves][NC][RPW rows][KS]
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int r = lane / KS, ks = lane % KS;
+    const int row0 = ((int)blockIdx.x * 4 + wid) * RPW;
+    int row = row0 + r;
+    if (row >= a.rows) row = a.rows - 1;
+    const size_t rowb = (size_t)row * nb;
+    auto load = [&](Q8Regs<TYPE> &w, int blk) {
+        const size_t wb = rowb + (blk < nb ? blk : nb - 1);
+        if constexpr (Q4) {
+            w.c0 = *reinterpret_cast<const uint4 *>(a.qa + wb * 16);
+        } else {
+            w.c0 = *reinterpret_cast<const uint4 *>(a.qa + wb * 32);
+            w.c1 = *reinterpret_cast<const uint4 *>(a.qa + wb * 32 + 16);
+        }
+        w.d = *reinterpret_cast<const uint16_t *>(a.dm + wb * 2);
+    };
+    Q8Regs<TYPE> wr[Q8W_PF];
+#pragma unroll
+    for (int p = 0; p < Q8W_PF; p++) load(wr[p], p * KS + ks);
+    for (int e = (int)threadIdx.x; e < nb * NC * 2; e += 256) {
+        const int rec = e >> 1, half = e & 1, c = rec / nb, blk = rec - c * nb;
+        *reinterpret_cast<uint4 *>(sx + ((size_t)blk * NC + c) * 32 + half * 16) =
+            *reinterpret_cast<const uint4 *>(a.xq + (size_t)c * a.n + (size_t)blk * 32 + half * 16);
+    }
+    for (int e = (int)threadIdx.x; e < nb * NC; e += 256) {
+        const int c = e / nb, blk = e - c * nb;
+        sxd[blk * NC + c] = a.xd[(size_t)c * nb + blk];
+        if constexpr (Q4) sxs[blk * NC + c] = a.xs[(size_t)c * nb + blk];
+    }
+    __syncthreads();
+    if (row0 >= a.rows) return; // no barrier follows
+    float *xw = xch + (size_t)wid * NC * 64;
+    const int oc = lane / RPW, orr = lane % RPW; // as a chain owner (lane < RPW * NC): column oc, row orr
+    float acc = 0.0f;
+    const int nr = (nb + KS - 1) / KS;
+
+    auto round_body = [&](Q8Regs<TYPE> &w, const int rd, const bool prefetch) {
+        const int blk = rd * KS + ks, blkc = blk < nb ? blk : nb - 1;
+        uint32_t wq[8];
+        if constexpr (Q4) {
+            const uint32_t c4[4] = {w.c0.x, w.c0.y, w.c0.z, w.c0.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                wq[i] = c4[i] & 0x0F0F0F0Fu;            // elements 4i .. 4i+3
+                wq[i + 4] = (c4[i] >> 4) & 0x0F0F0F0Fu; // elements 16 + 4i ..
+            }
+        } else {
+            wq[0] = w.c0.x, wq[1] = w.c0.y, wq[2] = w.c0.z, wq[3] = w.c0.w;
+            wq[4] = w.c1.x, wq[5] = w.c1.y, wq[6] = w.c1.z, wq[7] = w.c1.w;
+        }
+        const float dw = half_bits_to_float((uint16_t)w.d);
+        float pr[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const uint4 *xp = reinterpret_cast<const uint4 *>(sx + ((size_t)blkc * NC + c) * 32);
+            const uint4 x0 = xp[0], x1 = xp[1];
+            const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            int isum = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) isum = dot4(wq[i], xs[i], isum);
+            if constexpr (Q4) isum -= 8 * sxs[blkc * NC + c];
+            pr[c] = (dw * sxd[blkc * NC + c]) * (float)isum;
+        }
+        if (prefetch) {
+            __builtin_amdgcn_sched_barrier(0);
+            load(w, blk + Q8W_PF * KS);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int c = 0; c < NC; c++) xw[(c * RPW + r) * KS + ks] = pr[c];
+        __asm__ volatile("" ::: "memory");
+        if (lane < RPW * NC) {
+            const int live = nb - rd * KS < KS ? nb - rd * KS : KS;
+            const float *pv = xw + (oc * RPW + orr) * KS;
+#pragma unroll
+            for (int u0 = 0; u0 < KS; u0 += 16) { // 16 reads in flight, the sum in block order
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) v[u] = pv[u0 + u];
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    if (u0 + u < live) acc += v[u];
+            }
+        }
+        __asm__ volatile("" ::: "memory");
+    };
+    const int nfull = nr / Q8W_PF * Q8W_PF;
+    for (int rd = 0; rd < nfull; rd += Q8W_PF) {
+#pragma unroll
+        for (int p = 0; p < Q8W_PF; p++) round_body(wr[p], rd + p, true);
+    }
+#pragma unroll
+    for (int p = 0; p < Q8W_PF; p++)
+        if (nfull + p < nr) round_body(wr[p], nfull + p, false);
+    if (lane < RPW * NC && row0 + orr < a.rows) {
+        const size_t o = (size_t)oc * a.rows + row0 + orr;
+        a.y[o] = a.resid ? a.resid[o] + acc : acc;
     }
 }
 
@@ -433,7 +565,31 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
         hipLaunchKernelGGL((f32_matmul_kernel<NC>), dim3((unsigned)args.rows), dim3(256), lds, stream, args);
         return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "f32_matmul launch");
     }
-    // rows per block chosen so the LDS products fit in 64 KiB
+    {
+        // the wave kernel: activations staged in LDS
+        const size_t lds = (size_t)args.nb32 * NC * (32 + 8) + (size_t)4 * NC * 64 * 4;
+        if (lds <= 64 * 1024) {
+            // rows per wave: the most that still give the grid about four waves per SIMD
+            const int rpw = args.rows >= 16384 ? 4 : (args.rows >= 8192 ? 2 : 1);
+            const dim3 grid((unsigned)((args.rows + 4 * rpw - 1) / (4 * rpw)));
+            const bool q4 = args.type == AQ_TYPE_Q4_0;
+#define AQ_Q8W(R)                                                                                             \
+    if (q4)                                                                                                   \
+        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q4_0, NC, R>), grid, dim3(256), lds, stream, args);          \
+    else                                                                                                      \
+        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q8_0, NC, R>), grid, dim3(256), lds, stream, args);
+            if (rpw == 4) {
+                AQ_Q8W(4)
+            } else if (rpw == 2) {
+                AQ_Q8W(2)
+            } else {
+                AQ_Q8W(1)
+            }
+#undef AQ_Q8W
+            return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "q8_wave launch");
+        }
+    }
+    // longer rows: rows per block chosen so the LDS products fit in 64 KiB
     const size_t per_row = (size_t)args.nb32 * NC * sizeof(float);
     int rpb = 16;
     while (rpb > 1 && per_row * rpb > 64 * 1024) rpb /= 2;

@@ -412,6 +412,8 @@ struct aq_state {
              *shifted = nullptr;
     void *amax_scratch = nullptr;
     uint32_t *pinned = nullptr; // host, 64 words
+    aq::DnArgs *commit_args = nullptr; // device: the commit's DnArgs per DeltaNet slot, for par = 0 then par = 1
+    int n_dn = 0;
     bool spec_ready = false;
     aq_spec_stats stats{};
     std::vector<void *> allocs;
@@ -508,10 +510,19 @@ int mm(aq_state *s, const Weight &w, const Act &x, size_t t, float *y, const flo
     return launch_matmul(w, x, t, y, resid, s->stream);
 }
 
-// Several matrices over the same activations: one grouped launch when all are K-quants of one K.
+// Several matrices over the same activations: one grouped launch when they are K-quants of one K, optionally
+// followed by (at most two) F32 matrices.
 int mm_multi(aq_state *s, int n, const Weight *const *ws, float *const *ys, const Act &x, size_t t) {
-    bool grouped = true;
-    for (int i = 0; i < n; i++) grouped = grouped && is_kquant(ws[i]->type) && ws[i]->nb == ws[0]->nb;
+    bool grouped = is_kquant(ws[0]->type);
+    int nf = 0;
+    for (int i = 0; i < n; i++) {
+        if (ws[i]->type == AQ_TYPE_F32) {
+            nf++;
+            continue;
+        }
+        grouped = grouped && nf == 0 && is_kquant(ws[i]->type) && ws[i]->nb == ws[0]->nb;
+    }
+    grouped = grouped && nf <= 2;
     if (grouped) return launch_kq_group(ws, ys, nullptr, n, x, t, s->stream);
     for (int i = 0; i < n; i++) {
         const int rc = mm(s, *ws[i], x, t, ys[i]);
@@ -592,22 +603,16 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
     float *av = mode == VERIFY ? s->sv_a[dn_slot] : s->a;
     float *bv = mode == VERIFY ? s->sv_b[dn_slot] : s->b;
     {
-        const Weight *ws[2] = {&L.qkv, &L.gate_z};
-        float *ys[2] = {mixed, s->z};
-        if ((rc = mm_multi(s, 2, ws, ys, s->act_h, t))) return rc;
+        // qkv, z and the ssm_alpha / ssm_beta gate pre-activations in one launch (the gates kept for the commit)
+        const Weight *ws[4] = {&L.qkv, &L.gate_z, &L.alpha, &L.beta};
+        float *ys[4] = {mixed, s->z, av, bv};
+        if ((rc = mm_multi(s, 4, ws, ys, s->act_h, t))) return rc;
     }
-    AQ_REQUIRE(L.alpha.type == AQ_TYPE_F32 && L.beta.type == AQ_TYPE_F32,
-               "DeltaNet: ssm_alpha / ssm_beta must be F32 in this build");
     DnArgs d;
     d.mixed = mixed;
     d.z = s->z;
-    d.a = av; // ssm_alpha / ssm_beta projections computed inside the DeltaNet kernel, kept here
+    d.a = av;
     d.b = bv;
-    d.x = s->act_h.f32;
-    d.x_stride = s->act_h.n;
-    d.w_alpha = reinterpret_cast<const float *>(L.alpha.qa);
-    d.w_beta = reinterpret_cast<const float *>(L.beta.qa);
-    d.hidden = (int)c.hidden;
     d.conv_src = s->par ? s->conv1[dn_slot] : s->conv0[dn_slot];
     d.conv_dst = mode == VERIFY ? nullptr : (s->par ? s->conv0[dn_slot] : s->conv1[dn_slot]);
     d.conv_w = L.conv_w;
@@ -967,6 +972,43 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
     }
     if (!rc && hipHostMalloc((void **)&s->pinned, 64 * 4, hipHostMallocDefault) != hipSuccess)
         rc = fail(AQ_ENOMEM, "state: pinned");
+    // the commit of a speculative round, one launch for every DeltaNet layer: the kept-row count is info[2]
+    s->n_dn = n_dn;
+    if (!rc && spec_k > 0 && n_dn > 0) {
+        std::vector<DnArgs> ca(2 * (size_t)n_dn);
+        int dn = 0;
+        for (uint32_t li = 0; li < c.n_layer; li++) {
+            const DevLayer &L = m->layers[li];
+            if (L.attention) continue;
+            for (int par = 0; par < 2; par++) {
+                DnArgs &d = ca[(size_t)par * n_dn + dn];
+                d.mixed = s->sv_mixed[dn];
+                d.a = s->sv_a[dn];
+                d.b = s->sv_b[dn];
+                d.conv_src = par ? s->conv1[dn] : s->conv0[dn];
+                d.conv_dst = par ? s->conv0[dn] : s->conv1[dn];
+                d.conv_w = L.conv_w;
+                d.ssm_a = L.ssm_a;
+                d.dt_bias = L.dt_bias;
+                d.ssm_norm = L.ssm_norm;
+                d.eps = c.rms_eps;
+                d.qscale = m->qscale;
+                d.rec = s->rec[dn];
+                d.write_state = 1;
+                d.t = 1;
+                d.t_dev = s->info + 2;
+                d.nk = (int)c.dn_n_k_heads;
+                d.nv = (int)c.dn_n_v_heads;
+                d.dk = (int)c.dn_head_dim_k;
+                d.dv = (int)c.dn_head_dim_v;
+                d.kernel = (int)c.dn_conv_kernel;
+            }
+            dn++;
+        }
+        AQ_S(dalloc(s, ca.size() * sizeof(DnArgs), (void **)&s->commit_args));
+        if (!rc && hipMemcpy(s->commit_args, ca.data(), ca.size() * sizeof(DnArgs), hipMemcpyHostToDevice) != hipSuccess)
+            rc = fail(AQ_EHIP, "state: commit arguments");
+    }
     // The clears and table uploads above ran on the null stream, which the state's non-blocking stream does not
     // wait for: finish them before the first kernel on that stream can read the buffers.
     if (!rc && hipDeviceSynchronize() != hipSuccess) rc = fail(AQ_EHIP, "state: setup sync");
@@ -1067,41 +1109,23 @@ int aq_spec_round(aq_state *s, uint32_t x_p, uint32_t *emitted, uint32_t *n_emit
     AQ_HIP(hipMemcpyAsync(s->pinned, s->info, 3 * 4, hipMemcpyDeviceToHost, s->stream));
     AQ_HIP(hipMemcpyAsync(s->pinned + 16, s->emitted, t * 4, hipMemcpyDeviceToHost, s->stream));
     AQ_HIP(hipEventRecord(s->ev[1], s->stream));
-    AQ_HIP(hipStreamSynchronize(s->stream));
+    // commit (replaces spec.rs:396-415's restore + replay): every DeltaNet layer's state advances by the kept rows
+    // (info[2], read on the device) from the saved inputs, in one launch that runs while the host reads keep
+    if (s->n_dn > 0) {
+        DnArgs like;
+        like.nk = (int)m->cfg.dn_n_k_heads;
+        like.nv = (int)m->cfg.dn_n_v_heads;
+        like.dk = (int)m->cfg.dn_head_dim_k;
+        like.dv = (int)m->cfg.dn_head_dim_v;
+        if ((rc = launch_dn_core_multi(s->commit_args + (size_t)s->par * s->n_dn, like, s->n_dn, s->stream)))
+            return rc;
+    }
+    AQ_HIP(hipEventSynchronize(s->ev[1]));
     const uint32_t mm_ = s->pinned[0], ne = s->pinned[1], keep = s->pinned[2];
     AQ_REQUIRE(keep >= 1 && keep <= t && ne == keep, "aq_spec_round: inconsistent acceptance");
-    // commit (replaces spec.rs:396-415's restore + replay): the DeltaNet state advances by the kept rows from
-    // the saved inputs; the KV caches forget the rejected rows.
-    int dn = 0;
-    for (uint32_t li = 0; li < m->cfg.n_layer; li++) {
-        const DevLayer &L = m->layers[li];
-        if (L.attention) {
-            s->kv[li].len = p + keep;
-            continue;
-        }
-        DnArgs d;
-        d.mixed = s->sv_mixed[dn];
-        d.a = s->sv_a[dn];
-        d.b = s->sv_b[dn];
-        d.conv_src = s->par ? s->conv1[dn] : s->conv0[dn];
-        d.conv_dst = s->par ? s->conv0[dn] : s->conv1[dn];
-        d.conv_w = L.conv_w;
-        d.ssm_a = L.ssm_a;
-        d.dt_bias = L.dt_bias;
-        d.ssm_norm = L.ssm_norm;
-        d.eps = m->cfg.rms_eps;
-        d.qscale = m->qscale;
-        d.rec = s->rec[dn];
-        d.write_state = 1;
-        d.t = (int)keep;
-        d.nk = (int)m->cfg.dn_n_k_heads;
-        d.nv = (int)m->cfg.dn_n_v_heads;
-        d.dk = (int)m->cfg.dn_head_dim_k;
-        d.dv = (int)m->cfg.dn_head_dim_v;
-        d.kernel = (int)m->cfg.dn_conv_kernel;
-        if ((rc = launch_dn_core(d, s->stream))) return rc;
-        dn++;
-    }
+    // the KV caches forget the rejected rows
+    for (uint32_t li = 0; li < m->cfg.n_layer; li++)
+        if (m->layers[li].attention) s->kv[li].len = p + keep;
     s->par ^= 1;
     s->pos = p + keep;
     AQ_HIP(hipEventRecord(s->ev[2], s->stream));

@@ -57,8 +57,11 @@ struct DnArgs {
     // raw mode (the isolated recurrence): q, k (t x nk*dk), v (t x nv*dv), g, beta (t x nv) used as given
     int raw = 0;
     const float *rq = nullptr, *rk = nullptr, *rv = nullptr, *rg = nullptr, *rbeta = nullptr;
+    const uint32_t *t_dev = nullptr; // multi launch: the row count, read on the device (1..8)
 };
 int launch_dn_core(const DnArgs &a, hipStream_t stream);
+// n DnArgs (device array, commit form: saved gates, no output), all with the head shape of `like`: one launch.
+int launch_dn_core_multi(const DnArgs *args_dev, const DnArgs &like, int n, hipStream_t stream);
 
 struct AttnArgs {
     const float *qg = nullptr;          // t x (2*nh*hd): per head [q | gate]

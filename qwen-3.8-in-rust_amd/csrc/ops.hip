@@ -84,9 +84,12 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float *x, size_t x_s
 }
 
 // The same, for rows of float4s (the model's shapes), 512 threads: each thread keeps its float4s of x and w in
-// registers from the first load to the output; the squares go to LDS transposed (chain l's terms contiguous, so the
-// 8 chain lanes read them as float4s); with Q8_K output, wave w holds whole 256-blocks (its float4s are block
-// w + 8r, lane order), so the quantiser runs on registers.
+// registers from the first load to the output; the squares go to LDS transposed (chain l's terms contiguous); the 8
+// chain lanes add 24 terms from registers while the next 24 are read, so only the adds (about 4.5 cycles each) are
+// on the critical path, not the LDS latency. Work-group (row, slice) computes the whole chain of its row and then
+// writes only its slice of the normalised row (whole 256-blocks), so the quantiser work spreads over the slices'
+// work-groups; with Q8_K output, wave w holds whole 256-blocks (its float4s are block w + 8r, lane order), so the
+// quantiser runs on registers.
 constexpr int RN_THREADS = 512, RN_ROUNDS = 8; // n <= 4 * 512 * 8
 
 __host__ __device__ inline int rn_chain_stride(int n) { // floats per chain row in LDS: 4 (mod 32), 16-byte rows
@@ -94,12 +97,17 @@ __host__ __device__ inline int rn_chain_stride(int n) { // floats per chain row 
     return (clen + 31) / 32 * 32 + 4;
 }
 
+template <int PL>
 __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x, size_t x_stride, const float *w,
                                                                  float eps, int n, float *y, size_t y_stride, Act qa,
                                                                  int kind, size_t col0, size_t eoff, int act_f32) {
     extern __shared__ float sm[]; // 8 chains of squares, 16 floats, then (Q8_0 output only) the normalised row
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int n4 = n >> 2, n8 = n / 8 * 8, clen = n8 / 8, cs = rn_chain_stride(n);
+    // this work-group's slice of the output: float4s [o0, o1), whole 256-blocks
+    const int nslice = gridDim.y, nblk = n4 / 64;
+    const int o0 = nslice > 1 ? (int)blockIdx.y * nblk / nslice * 64 : 0;
+    const int o1 = nslice > 1 ? ((int)blockIdx.y + 1) * nblk / nslice * 64 : n4;
     float *sq = sm, *red = sm + 8 * cs, *xs = red + 16;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)row * x_stride);
     const float4 *w4 = reinterpret_cast<const float4 *>(w);
@@ -125,31 +133,63 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
         }
     }
     __syncthreads();
-    if (tid < 8) { // chain tid: x[tid]^2 + x[tid + 8]^2 + ... in order, read a float4 at a time, 8 float4s ahead
+    if constexpr (PL > 0) {
+        // chain w runs in wave w: lane m holds the chain's terms PL*m .. PL*m + PL - 1 in registers; the running sum
+        // moves one lane up after each lane's terms (DPP wave shift), so lane 63 ends with the whole chain, summed in
+        // order with every term an add of a register (no LDS read on the chain's path)
+        const int wave = tid >> 6;
+        float acc = 0.0f;
+        if (wave < 8) {
+            const float *c = sq + wave * cs + PL * lane;
+            float r[PL];
+#pragma unroll
+            for (int k = 0; k < PL; k++) r[k] = PL * lane + k < clen ? c[k] : 0.0f;
+#pragma unroll 4
+            for (int m = 0; m < 64; m++) {
+                if (m > 0) acc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
+                                                                                      0x138, 0xF, 0xF, false));
+#pragma unroll
+                for (int k = 0; k < PL; k++) acc += r[k];
+            }
+        }
+        if (lane == 63 && wave < 8) red[wave] = acc;
+    } else if (tid < 8) { // chain tid, 6 float4s per batch from LDS, two batches in flight
         const float *c = sq + tid * cs;
         const float4 *c4 = reinterpret_cast<const float4 *>(c);
         const int nq = clen / 4;
         float acc = 0.0f;
-        if (nq > 0) {
-            float4 b[8];
+        constexpr int B = 6; // at most 15 LDS reads may be waited for one by one (the counter's width)
+        // whole double batches without guards (a guard per term costs a branch), then the remaining float4s
+        const int nfull = nq / (2 * B) * (2 * B);
+        auto rd = [&](float4 *buf, int v0) {
 #pragma unroll
-            for (int k = 0; k < 8; k++) b[k] = c4[k < nq ? k : nq - 1];
-            for (int v0 = 0; v0 < nq; v0 += 8) {
-                float4 nb[8];
+            for (int k = 0; k < B; k++) buf[k] = c4[v0 + k];
+        };
+        auto add = [&](const float4 *buf) {
 #pragma unroll
-                for (int k = 0; k < 8; k++) nb[k] = c4[v0 + 8 + k < nq ? v0 + 8 + k : nq - 1];
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    if (v0 + k < nq) {
-                        acc += b[k].x;
-                        acc += b[k].y;
-                        acc += b[k].z;
-                        acc += b[k].w;
-                    }
-                }
-#pragma unroll
-                for (int k = 0; k < 8; k++) b[k] = nb[k];
+            for (int k = 0; k < B; k++) {
+                acc += buf[k].x;
+                acc += buf[k].y;
+                acc += buf[k].z;
+                acc += buf[k].w;
             }
+        };
+        if (nfull > 0) {
+            float4 ba[B], bb[B];
+            rd(ba, 0);
+            for (int v0 = 0; v0 < nfull; v0 += 2 * B) {
+                rd(bb, v0 + B);
+                add(ba);
+                if (v0 + 2 * B < nfull) rd(ba, v0 + 2 * B);
+                add(bb);
+            }
+        }
+        for (int v = nfull; v < nq; v++) {
+            const float4 f = c4[v];
+            acc += f.x;
+            acc += f.y;
+            acc += f.z;
+            acc += f.w;
         }
         for (int u = nq * 4; u < clen; u++) acc += c[u];
         red[tid] = acc;
@@ -167,7 +207,8 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
 #pragma unroll
     for (int r = 0; r < RN_ROUNDS; r++) {
         const int i4 = tid + r * RN_THREADS;
-        if (i4 < n4) { // n4 is a multiple of 64 when the output is Q8_K: the condition is wave-uniform there
+        // n4 is a multiple of 64 when the output is Q8_K: the conditions are wave-uniform there
+        if (i4 < n4 && i4 >= o0 && i4 < o1) {
             const float v[4] = {(xv[r].x * inv) * wv[r].x, (xv[r].y * inv) * wv[r].y, (xv[r].z * inv) * wv[r].z,
                                 (xv[r].w * inv) * wv[r].w};
             const float4 v4 = make_float4(v[0], v[1], v[2], v[3]);
@@ -179,7 +220,8 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
     }
     if (kind == QK_Q80) {
         __syncthreads();
-        for (int blk = tid; blk < n / 32; blk += RN_THREADS) q8_0_block_store(qa, col0 + row, eoff / 32 + blk, xs + blk * 32);
+        for (int blk = o0 / 8 + tid; blk < o1 / 8; blk += RN_THREADS)
+            q8_0_block_store(qa, col0 + row, eoff / 32 + blk, xs + blk * 32);
     }
 }
 
@@ -238,13 +280,13 @@ constexpr int DN_BLK_MAX = 256; // 32-blocks of the alpha/beta rows (hidden <= 8
 constexpr int DN_THREADS = 512; // waves 0-3 hold state columns (dv <= 256); 4 and 5 run the per-row sums
 
 template <int DK, int DV>
-__global__ void __launch_bounds__(DN_THREADS) dn_core_kernel(DnArgs a) {
+__device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const int t) {
     static_assert(DK <= 256 && DV <= 256 && DN_THREADS >= 384 && DN_TMAX * 8 <= 64, "DeltaNet work-group shape");
     __shared__ float sq[DN_TMAX][DK], sk[DN_TMAX][DK], sv[DN_TMAX][DV], sz[DN_TMAX][DV], so[DN_TMAX][DV];
     __shared__ float part[2][DN_TMAX][DN_BLK_MAX];
     __shared__ float rdec[DN_TMAX], rbeta[DN_TMAX], rq[DN_TMAX], rk[DN_TMAX], ro[DN_TMAX];
-    const int p = blockIdx.x, j = threadIdx.x, lane = j & 63, wave = j >> 6;
-    const int kh = p % a.nk, t = a.t;
+    const int j = threadIdx.x, lane = j & 63, wave = j >> 6;
+    const int kh = p % a.nk;
     const int kd = a.nk * DK, vd = a.nv * DV, cd = 2 * kd + vd;
     const bool has_v = j < DV;
     const bool gated = a.out && !a.raw;
@@ -490,6 +532,21 @@ __global__ void __launch_bounds__(DN_THREADS) dn_core_kernel(DnArgs a) {
             for (int i = 0; i < t; i++)
                 a.out[(size_t)i * vd + p * DV + j] = (a.ssm_norm[j] * (so[i][j] * ro[i])) * sz[i][j];
     }
+}
+
+template <int DK, int DV>
+__global__ void __launch_bounds__(DN_THREADS) dn_core_kernel(DnArgs a) {
+    dn_core_body<DK, DV>(a, (int)blockIdx.x, a.t);
+}
+
+// Several layers' heads in one launch (the commit of every DeltaNet layer after a speculative round): work-group
+// (p, y) runs head p of args[y]; the row count is read on the device when t_dev is set.
+template <int DK, int DV>
+__global__ void __launch_bounds__(DN_THREADS) dn_core_multi_kernel(const DnArgs *args) {
+    const DnArgs &a = args[blockIdx.y];
+    const int t = a.t_dev ? (int)*a.t_dev : a.t;
+    if (t < 1 || t > DN_TMAX) return; // uniform: a row count the host validates before it is used
+    dn_core_body<DK, DV>(a, (int)blockIdx.x, t);
 }
 
 // ---------------------------------------------------------------------------------------------- attention
@@ -752,8 +809,25 @@ int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, s
     const size_t vshmem = ((size_t)8 * rn_chain_stride((int)n) + 16 + (q.kind == QK_Q80 ? n : 0)) * sizeof(float);
     if (vec && vshmem <= 65536) {
         const size_t shmem = vshmem;
-        hipLaunchKernelGGL(rmsnorm_vec_kernel, dim3((unsigned)t), dim3(RN_THREADS), shmem, stream, x, x_stride, w, eps,
-                           (int)n, y_f32, y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0);
+        // slices of whole 256-blocks (about five blocks each) when the row is made of them
+        const int nblk = n % 256 == 0 ? (int)(n / 256) : 0;
+        const unsigned slices = nblk >= 8 ? (unsigned)((nblk + 4) / 5) : 1;
+        // chain terms per lane in the register chain (the smallest built count that holds a chain), else LDS
+        const int clen = (int)(n / 8), need = (clen + 63) / 64;
+        const int pls[] = {1, 2, 4, 6, 8, 10, 12, 16};
+        int pl = 0;
+        for (int c : pls)
+            if (!pl && c >= need) pl = c;
+        const dim3 grid((unsigned)t, slices);
+        switch (pl) {
+#define AQ_RN(P)                                                                                              \
+    case P:                                                                                                   \
+        hipLaunchKernelGGL((rmsnorm_vec_kernel<P>), grid, dim3(RN_THREADS), shmem, stream, x, x_stride, w, eps, (int)n, \
+                           y_f32, y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0);              \
+        break;
+            AQ_RN(0) AQ_RN(1) AQ_RN(2) AQ_RN(4) AQ_RN(6) AQ_RN(8) AQ_RN(10) AQ_RN(12) AQ_RN(16)
+#undef AQ_RN
+        }
         return launched("rmsnorm");
     }
     const size_t shmem = (2 * n + 16) * sizeof(float);
@@ -811,6 +885,24 @@ int launch_dn_core(const DnArgs &a, hipStream_t stream) {
                                         std::to_string(a.dv));
     }
     return launched("deltanet");
+}
+
+int launch_dn_core_multi(const DnArgs *args_dev, const DnArgs &like, int n, hipStream_t stream) {
+    AQ_REQUIRE(n >= 1 && args_dev, "deltanet: no layers");
+    AQ_REQUIRE(!like.raw && !like.x && !like.out, "deltanet multi: commit form only (saved gates, no output)");
+    const int key = like.dk * 1000 + like.dv;
+    switch (key) {
+#define AQ_DN(K, V)                                                                                           \
+    case K * 1000 + V:                                                                                        \
+        hipLaunchKernelGGL((dn_core_multi_kernel<K, V>), dim3((unsigned)like.nv, (unsigned)n), dim3(DN_THREADS), 0, \
+                           stream, args_dev);                                                                 \
+        break;
+        AQ_DN(8, 8) AQ_DN(16, 16) AQ_DN(32, 32) AQ_DN(64, 64) AQ_DN(128, 128) AQ_DN(128, 256) AQ_DN(64, 128)
+#undef AQ_DN
+    default: return fail(AQ_EUNSUP, "deltanet: head dims (k, v) not built: " + std::to_string(like.dk) + ", " +
+                                        std::to_string(like.dv));
+    }
+    return launched("deltanet multi");
 }
 
 int launch_attention(const AttnArgs &a, hipStream_t stream) {
