@@ -65,14 +65,14 @@ def kernel_roofline(ctx, k):
     achieved = traffic_alg / (us * 1e-6) / 1e9
     for w in ws:
         w.free()
-    return {"kernel": f"kq_mfma_kernel Q4_K {rows}x{cols} N={n}", "us_per_launch": round(us, 3),
+    return {"kernel": f"kq_wave_kernel Q4_K {rows}x{cols} N={n}", "us_per_launch": round(us, 3),
             "bytes_per_launch": traffic_alg, "achieved_GBs": achieved}
 
 
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from its committed counter summary (FETCH_SIZE + WRITE_SIZE,
     scaled by a device copy of known size), or None."""
-    path = os.path.join(ROOT, "profiles", "kq_mfma_q4k_17408x5120_n4.md")
+    path = os.path.join(ROOT, "profiles", "kq_wave_q4k_17408x5120_n4.md")
     if not os.path.exists(path):
         return None
     for line in open(path):

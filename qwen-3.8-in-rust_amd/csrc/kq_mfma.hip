@@ -73,20 +73,21 @@ struct WRegs {
 };
 
 // Tile `tile` (= (row >> 2) * nb + sb), row r = row & 3 within it, lane pair j (tiled planes, aq_common.h): the
-// 16 (j, r) threads of a matrix-core block read contiguous 256-byte runs.
+// 16 (j, r) threads of a matrix-core block read contiguous 256-byte runs. Offsets are 32-bit (every plane is below
+// 4 GiB), so the loads take the uniform plane base plus one 32-bit lane offset.
 template <int TYPE>
-__device__ __forceinline__ void load_w(WRegs<TYPE> &w, const MfArgs &a, size_t tile, int r, int j) {
-    const int jr = j * 4 + r;
-    const uint8_t *qa = a.qa + tile * 512 + jr * 16;
+__device__ __forceinline__ void load_w(WRegs<TYPE> &w, const MfArgs &a, uint32_t tile, int r, int j) {
+    const uint32_t jr = (uint32_t)(j * 4 + r);
+    const uint8_t *qa = a.qa + (tile * 512u + jr * 16u);
     w.qa0 = *reinterpret_cast<const uint4 *>(qa);       // lane j
     w.qa1 = *reinterpret_cast<const uint4 *>(qa + 256); // lane j + 4
-    w.sc = *reinterpret_cast<const uint4 *>(a.sc + tile * 64 + r * 16);
+    w.sc = *reinterpret_cast<const uint4 *>(a.sc + (tile * 64u + (uint32_t)r * 16u));
     if constexpr (TYPE == AQ_TYPE_Q5_K) {
-        const uint2 h = *reinterpret_cast<const uint2 *>(a.qb + tile * 128 + jr * 8);
+        const uint2 h = *reinterpret_cast<const uint2 *>(a.qb + (tile * 128u + jr * 8u));
         w.qb = make_uint4(h.x, h.y, 0, 0);
     } else if constexpr (TYPE == AQ_TYPE_Q6_K) {
-        w.qb = *reinterpret_cast<const uint4 *>(a.qb + tile * 256 + jr * 16);
-        w.d6 = *reinterpret_cast<const uint16_t *>(a.dm + tile * 8 + r * 2);
+        w.qb = *reinterpret_cast<const uint4 *>(a.qb + (tile * 256u + jr * 16u));
+        w.d6 = *reinterpret_cast<const uint16_t *>(a.dm + (tile * 8u + (uint32_t)r * 2u));
     }
 }
 
@@ -439,18 +440,21 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
         const int rr_ = rw0 + rg * 4 + r;
         return rr_ < a.rows ? rr_ : a.rows - 1;
     };
-    // the prefetch cursor: tile pk (clamped to the wave's last tile), round prd
+    // the prefetch cursor: tile pk (clamped to the wave's last tile), round prd; ptile = this thread's row group's
+    // first tile plus its K slice, so a round's tile is ptile + prd * KSW (clamped to the row's last super-block)
     int pk = 0, prd = 0;
-    size_t ptile0 = (size_t)(tile_row(0) >> 2) * nb;
+    uint32_t ptile = (uint32_t)(tile_row(0) >> 2) * (uint32_t)nb + (uint32_t)ks, plast = ptile - ks + nb - 1;
     int prr = tile_row(0) & 3;
     auto issue = [&](WRegs<TYPE> &wv) {
-        load_w<TYPE>(wv, a, ptile0 + min(prd * KSW + ks, nb - 1), prr, j);
+        const uint32_t tl = ptile + (uint32_t)(prd * KSW);
+        load_w<TYPE>(wv, a, tl < plast ? tl : plast, prr, j);
         if (++prd == nr) {
             prd = 0;
             if (pk + 1 < mt) {
                 pk++;
                 const int row = tile_row(pk);
-                ptile0 = (size_t)(row >> 2) * nb;
+                ptile = (uint32_t)(row >> 2) * (uint32_t)nb + (uint32_t)ks;
+                plast = ptile - ks + nb - 1;
                 prr = row & 3;
             }
         }
