@@ -385,6 +385,72 @@ __device__ __forceinline__ void kq_stage(const KqGroup &G, int8_t *sxq, float *s
     }
 }
 
+// kq_stage split in two for the first chunk: the loads into registers (every load issued, clamped into the
+// activations, so the compiler's wait counts stay exact), then, after the first weight loads are issued, the LDS
+// writes. Waiting for a record then waits only for what was issued before it. Five records per 16-thread group
+// (80 records: 4 columns of K = 5120), held in named registers.
+template <bool HAS45, bool HAS6>
+struct KqStageRegs {
+    uint4 r0, r1, r2, r3, r4;
+    float d;
+    uint4 q8, b0, b1;
+};
+constexpr int KQ_STAGE_REGS = 5 * 16; // records the register staging holds
+
+__device__ __forceinline__ uint4 kq_rec_load(const KqGroup &G, int i, int ns, int nrec) {
+    const int rc = min((int)(threadIdx.x >> 4) + 16 * i, nrec - 1);
+    const int c = rc / ns, sb = rc - c * ns;
+    return *reinterpret_cast<const uint4 *>(G.xqs + (size_t)c * G.xcol + (size_t)sb * 256 + (threadIdx.x & 15) * 16);
+}
+template <int NC>
+__device__ __forceinline__ void kq_rec_store(int8_t *sxq, const uint4 v, int i, int ns, int nrec) {
+    // past the end a thread rewrites the last record with the bytes it loaded from there: no branches
+    const int rc = min((int)(threadIdx.x >> 4) + 16 * i, nrec - 1);
+    const int c = rc / ns, sb = rc - c * ns;
+    *reinterpret_cast<uint4 *>(sxq + ((size_t)sb * NC + c) * KQ_XS + (threadIdx.x & 15) * 16) = v;
+}
+template <int NC, bool HAS45, bool HAS6>
+__device__ __forceinline__ void kq_stage_load(const KqGroup &G, KqStageRegs<HAS45, HAS6> &R, int ns) {
+    const int nb = G.nb, nrec = ns * NC;
+    R.r0 = kq_rec_load(G, 0, ns, nrec);
+    R.r1 = kq_rec_load(G, 1, ns, nrec);
+    R.r2 = kq_rec_load(G, 2, ns, nrec);
+    R.r3 = kq_rec_load(G, 3, ns, nrec);
+    R.r4 = kq_rec_load(G, 4, ns, nrec);
+    const int e = min((int)threadIdx.x, nrec - 1), c = e / ns, sb = e % ns;
+    const size_t m = (size_t)c * nb + sb;
+    R.d = G.xd[m];
+    if constexpr (HAS45) R.q8 = *reinterpret_cast<const uint4 *>(G.xq8s + m * 8);
+    if constexpr (HAS6) {
+        R.b0 = reinterpret_cast<const uint4 *>(G.xbs + m * 16)[0];
+        R.b1 = reinterpret_cast<const uint4 *>(G.xbs + m * 16)[1];
+    }
+}
+template <int NC, bool HAS45, bool HAS6>
+__device__ __forceinline__ void kq_stage_store(const KqStageRegs<HAS45, HAS6> &R, int8_t *sxq, float *sxd,
+                                               uint32_t *sxm, int ns) {
+    constexpr int NCP = (NC + 3) / 4 * 4;
+    constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), P6 = HAS45 ? 4 : 0;
+    const int nrec = ns * NC;
+    kq_rec_store<NC>(sxq, R.r0, 0, ns, nrec);
+    kq_rec_store<NC>(sxq, R.r1, 1, ns, nrec);
+    kq_rec_store<NC>(sxq, R.r2, 2, ns, nrec);
+    kq_rec_store<NC>(sxq, R.r3, 3, ns, nrec);
+    kq_rec_store<NC>(sxq, R.r4, 4, ns, nrec);
+    const int e = min((int)threadIdx.x, nrec - 1), c = e / ns, sb = e % ns;
+    sxd[sb * NCP + c] = R.d;
+    if constexpr (HAS45) {
+        const uint32_t pv[4] = {R.q8.x, R.q8.y, R.q8.z, R.q8.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) sxm[(sb * NP + q) * NCP + c] = pv[q];
+    }
+    if constexpr (HAS6) {
+        const uint32_t pv[8] = {R.b0.x, R.b0.y, R.b0.z, R.b0.w, R.b1.x, R.b1.y, R.b1.z, R.b1.w};
+#pragma unroll
+        for (int q = 0; q < 8; q++) sxm[(sb * NP + P6 + q) * NCP + c] = pv[q];
+    }
+}
+
 // The exchange slot of one wave: KSW blocks (one per K slice) of NCH chains x NI chain owners, the block stride
 // padded to NI modulo 64 floats so both the writes (by slice) and the owners' reads hit distinct banks.
 template <int NCH, int KSW>
@@ -461,10 +527,22 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
     };
     WRegs<TYPE> wr[PF];
 
-    // the first PF rounds of weights fly while the activations are staged
+    // the first chunk's activations: loaded into registers ahead of the first PF rounds of weights when they fit
+    // (then writing them to LDS waits only for them), else staged after those weights are issued
+    const int ns0 = chk < nb ? chk : nb;
+    if (ns0 * NC <= KQ_STAGE_REGS) { // uniform
+        KqStageRegs<HAS45, HAS6> R;
+        kq_stage_load<NC>(G, R, ns0);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int p = 0; p < PF; p++) issue(wr[p]);
-    kq_stage<NC, HAS45, HAS6>(G, sxq, sxd, sxm, 0, chk < nb ? chk : nb);
+        for (int p = 0; p < PF; p++) issue(wr[p]);
+        __builtin_amdgcn_sched_barrier(0);
+        kq_stage_store<NC>(R, sxq, sxd, sxm, ns0);
+    } else {
+#pragma unroll
+        for (int p = 0; p < PF; p++) issue(wr[p]);
+        kq_stage<NC, HAS45, HAS6>(G, sxq, sxd, sxm, 0, ns0);
+    }
     __syncthreads();
     if (nit == 0) return; // no barrier follows (with chunks every wave has a tile)
     int s0 = 0; // first super-block of the staged chunk
@@ -517,24 +595,39 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
             sb_products<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr[0], pr[1], pr[2]);
         else
             sb_products_split<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr[0], pr[1], pr[2]);
+        // every product is final here (the empty asm pins its computation above the refill), so no use of the
+        // consumed weight registers sinks below it
+#pragma unroll
+        for (int k = 0; k < NCH; k++) __asm__ volatile("" : "+v"(pr[k / NC][k % NC]));
         if (prefetch) {
-            // the refill goes into the registers just consumed: every use of the old values stays above it, so
-            // the ring keeps its registers across the loop's back edge (no copies, no drain of the loads in flight)
+            // the refill goes into the registers just consumed, so the ring keeps its registers across the loop's
+            // back edge (no copies, no drain of the loads in flight)
             __builtin_amdgcn_sched_barrier(0);
             issue(wv);
             __builtin_amdgcn_sched_barrier(0);
         }
-        const int live = nb - crd * KSW < KSW ? nb - crd * KSW : KSW; // super-blocks in this round
+        const int live = nb - crd * KSW < KSW ? nb - crd * KSW : KSW; // super-blocks in this round (uniform)
 #pragma unroll
         for (int k = 0; k < NCH; k++) xw[ks * X::S + k * NI + idx] = pr[k / NC][k % NC];
         __asm__ volatile("" ::: "memory");
+        if (live == KSW) { // all K slices live: the owners' reads issue together
 #pragma unroll
-        for (int m = 0; m < NO; m++) {
-            const int k = ks + KSW * m;
-            if (k < NCH) {
+            for (int m = 0; m < NO; m++) {
+                const int k = ks + KSW * m;
+                if (k < NCH) {
 #pragma unroll
-                for (int k2 = 0; k2 < KSW; k2++)
-                    if (k2 < live) acc[m] += xw[k2 * X::S + k * NI + idx];
+                    for (int k2 = 0; k2 < KSW; k2++) acc[m] += xw[k2 * X::S + k * NI + idx];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < NO; m++) {
+                const int k = ks + KSW * m;
+                if (k < NCH) {
+#pragma unroll
+                    for (int k2 = 0; k2 < KSW; k2++)
+                        if (k2 < live) acc[m] += xw[k2 * X::S + k * NI + idx];
+                }
             }
         }
         __asm__ volatile("" ::: "memory");
@@ -668,7 +761,7 @@ __global__ void __launch_bounds__(256) kq_wave_kernel(KqGroup G) {
 }
 
 constexpr int KQ_LDS_MAX = 160 * 1024 - 512; // a CU's LDS, less a margin
-constexpr int KQ_PF = 4;                      // prefetch depth in rounds
+constexpr int KQ_PF = 2;                      // prefetch depth in rounds (more costs a wave per SIMD)
 
 template <int NC, int KSW>
 constexpr size_t kq_xch_bytes() { return (size_t)4 * KqXch<3 * NC, KSW>::FLOATS * 4; }
