@@ -22,6 +22,7 @@
 //    rounds deep; activations are staged in LDS (all of K, or chunks of it) once per work-group.
 #include "aq_common.h"
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 
@@ -659,19 +660,19 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
         if (nfull + p < nit) round_body(wr[p], false);
 }
 
-// An F32 segment (the DeltaNet ssm_alpha / ssm_beta rows, dot.rs:180-200 via matvec.rs:270-279): one row per wave;
-// lane l takes 32-element blocks l, l + 64, ...: each block's partial is a left-to-right sum from 0 (product, then
-// add), written to LDS; then lane c chains column c's partials block by block, and the reference's `acc + part`
-// with the absent tail adds 0.0f when n is a multiple of 32. `part` holds 4 x NC x ceil(n / 32) floats.
+// An F32 segment (the DeltaNet ssm_alpha / ssm_beta rows, dot.rs:180-200 via matvec.rs:270-279): one row per
+// work-group, so it is done long before the K-quant work-groups beside it. Thread t takes 32-element blocks t,
+// t + 256, ...: each block's partial is a left-to-right sum from 0 (product, then add), two columns at a time,
+// written to LDS; after the work-group's barrier lane c chains column c's partials block by block, and the
+// reference's `acc + part` with the absent tail adds 0.0f when n is a multiple of 32. `part` holds NC x ceil(n / 32)
+// floats.
 template <int NC>
 __device__ __forceinline__ void kq_f32_run(const KqGroup &G, const KqSeg &sg, int wg, float *part) {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const int row = wg * 4 + wid;
-    if (row >= sg.rows) return;
+    const int row = wg;
+    if (row >= sg.rows) return; // uniform: no barrier is met
     const int n = (int)G.xcol, nblk = (n + 31) / 32;
-    float *pw = part + (size_t)wid * NC * nblk;
     const float *w = reinterpret_cast<const float *>(sg.qa) + (size_t)row * n;
-    for (int b = lane; b < nblk; b += 64) {
+    for (int b = (int)threadIdx.x; b < nblk; b += (int)blockDim.x) {
         const int e0 = b * 32, ne = n - e0 < 32 ? n - e0 : 32;
         if (ne == 32) {
             float wv[32];
@@ -680,13 +681,14 @@ __device__ __forceinline__ void kq_f32_run(const KqGroup &G, const KqSeg &sg, in
                 const float4 f = *reinterpret_cast<const float4 *>(w + e0 + 4 * u);
                 wv[4 * u] = f.x, wv[4 * u + 1] = f.y, wv[4 * u + 2] = f.z, wv[4 * u + 3] = f.w;
             }
-            // up to four columns' chains interleaved (independent sums, each still left to right)
+            // two columns' sums interleaved (independent chains, each still left to right); one pair at a time
+            // keeps the registers below the K-quant path's
+#pragma unroll 1
+            for (int c0 = 0; c0 < NC; c0 += 2) {
+                constexpr int G2 = NC < 2 ? NC : 2;
+                float xv[G2][32];
 #pragma unroll
-            for (int c0 = 0; c0 < NC; c0 += 4) {
-                constexpr int G4 = NC < 4 ? NC : 4;
-                float xv[G4][32];
-#pragma unroll
-                for (int g = 0; g < G4; g++) {
+                for (int g = 0; g < G2; g++) {
                     const float *xr = G.xf + (size_t)(c0 + g < NC ? c0 + g : NC - 1) * n + e0;
 #pragma unroll
                     for (int u = 0; u < 8; u++) {
@@ -694,29 +696,29 @@ __device__ __forceinline__ void kq_f32_run(const KqGroup &G, const KqSeg &sg, in
                         xv[g][4 * u] = f.x, xv[g][4 * u + 1] = f.y, xv[g][4 * u + 2] = f.z, xv[g][4 * u + 3] = f.w;
                     }
                 }
-                float pt[G4];
+                float pt[G2];
 #pragma unroll
-                for (int g = 0; g < G4; g++) pt[g] = 0.0f;
+                for (int g = 0; g < G2; g++) pt[g] = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 32; e++)
 #pragma unroll
-                    for (int g = 0; g < G4; g++) pt[g] += wv[e] * xv[g][e];
+                    for (int g = 0; g < G2; g++) pt[g] += wv[e] * xv[g][e];
 #pragma unroll
-                for (int g = 0; g < G4; g++)
-                    if (c0 + g < NC) pw[(c0 + g) * nblk + b] = pt[g];
+                for (int g = 0; g < G2; g++)
+                    if (c0 + g < NC) part[(c0 + g) * nblk + b] = pt[g];
             }
         } else {
             for (int c = 0; c < NC; c++) {
                 const float *xr = G.xf + (size_t)c * n + e0;
                 float pt = 0.0f;
                 for (int e = 0; e < ne; e++) pt += w[e0 + e] * xr[e];
-                pw[c * nblk + b] = pt;
+                part[c * nblk + b] = pt;
             }
         }
     }
-    __asm__ volatile("" ::: "memory"); // the wave's partials are in LDS before its chain lanes read them
-    if (lane < NC) {
-        const float *pc = pw + lane * nblk;
+    __syncthreads();
+    if (threadIdx.x < NC) {
+        const float *pc = part + threadIdx.x * nblk;
         float acc = 0.0f;
         int b = 0;
         for (; b + 16 <= nblk; b += 16) { // 16 reads in flight, the sum still in block order
@@ -728,7 +730,7 @@ __device__ __forceinline__ void kq_f32_run(const KqGroup &G, const KqSeg &sg, in
         }
         for (; b < nblk; b++) acc += pc[b];
         if (n % 32 == 0) acc = acc + 0.0f;
-        const size_t o = (size_t)lane * sg.rows + row;
+        const size_t o = (size_t)threadIdx.x * sg.rows + row;
         sg.y[o] = sg.resid ? sg.resid[o] + acc : acc;
     }
 }
@@ -745,7 +747,7 @@ __global__ void __launch_bounds__(256) kq_wave_kernel(KqGroup G) {
     while (si + 1 < G.nseg && (int)blockIdx.x >= G.seg[si].wg_end) si++;
     const KqSeg &sg = G.seg[si];
     const int wg = (int)blockIdx.x - (si ? G.seg[si - 1].wg_end : 0);
-    if (sg.type == AQ_TYPE_F32) { // uniform: F32 work-groups stage nothing and meet no barrier
+    if (sg.type == AQ_TYPE_F32) { // uniform: F32 work-groups stage nothing and meet only their own barrier
         kq_f32_run<NC>(G, sg, wg, reinterpret_cast<float *>(kq_lds));
         return;
     }
@@ -808,9 +810,10 @@ inline int kq_pick_chunk(int nb, int nc, bool has45, bool has6, int ksw) {
     return c < unit ? unit : c;
 }
 
-// Grid: one tile per wave when all tiles fit the device in one pass (or the staging is chunked); otherwise a
-// persistent grid of exactly the resident work-groups, shared between the segments by weight bytes, each wave then
-// streaming several tiles.
+// Grid: one tile per wave while the tiles are fewer than KQ_PERSIST tiles per resident wave (or the staging is
+// chunked): work-groups past the resident ones start as others end; otherwise a persistent grid of exactly the
+// resident work-groups, shared between the segments by weight bytes, each wave then streaming several tiles.
+constexpr int KQ_PERSIST = 1;
 template <int T0, int T1, int NC, int KSW>
 int launch_wave_ks(KqGroup G, hipStream_t stream) {
     constexpr int RW = 16 / KSW; // rows per tile
@@ -833,8 +836,8 @@ int launch_wave_ks(KqGroup G, hipStream_t stream) {
     for (int i = 0; i < G.nseg; i++) {
         const KqSeg &sg = G.seg[i];
         if (sg.type == AQ_TYPE_F32) {
-            AQ_REQUIRE((size_t)4 * NC * ((G.xcol + 31) / 32) * 4 <= lds, "kq_mfma: F32 partials exceed the LDS");
-            f32_wgs += (sg.rows + 3) / 4; // four rows per work-group, partials in the staging LDS
+            AQ_REQUIRE((size_t)NC * ((G.xcol + 31) / 32) * 4 <= lds, "kq_mfma: F32 partials exceed the LDS");
+            f32_wgs += sg.rows; // one row per work-group, partials in the staging LDS
             continue;
         }
         const long t = (sg.rows + RW - 1) / RW;
@@ -842,13 +845,16 @@ int launch_wave_ks(KqGroup G, hipStream_t stream) {
         bytes += (double)t * block_bytes(sg.type);
     }
     const long cap = kq_capacity(fn, lds) - f32_wgs;
-    const bool persistent = G.chk >= G.nb && cap >= G.nseg && tiles > 4 * cap;
+    const bool persistent = G.chk >= G.nb && cap >= G.nseg && tiles > KQ_PERSIST * 4 * cap;
+    // the F32 segments' work-groups take the lowest indices: dispatched first, they are done early and free their
+    // slots for the K-quant work-groups past the resident ones
+    std::stable_partition(G.seg, G.seg + G.nseg, [](const KqSeg &sg) { return sg.type == AQ_TYPE_F32; });
     int wgs = 0;
     for (int i = 0; i < G.nseg; i++) {
         KqSeg &sg = G.seg[i];
         long n;
         if (sg.type == AQ_TYPE_F32) {
-            n = (sg.rows + 3) / 4;
+            n = sg.rows;
         } else {
             const long t = (sg.rows + RW - 1) / RW, need = (t + 3) / 4;
             n = need;

@@ -14,6 +14,10 @@
 // on v_dot4_i32_i8; the activation tile is re-read from L2 by every row of the wave (it is tiny and hot).
 #include "aq_common.h"
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 namespace aq {
 namespace {
 
@@ -271,9 +275,13 @@ __global__ void __launch_bounds__(256) q8_matmul_kernel(Q8Args a) {
 // for every column. The KS products of a (row, column) go through the wave's LDS slot to its chain owner, lane
 // RPW*c + r, which adds them in block order (no work-group barrier: one wave's LDS accesses execute in order).
 // Weights stream through a register ring Q8W_PF rounds deep; the activations (codes, f32 scales, Q4_0 code sums)
-// are staged in LDS once per work-group. Few rows per wave keep short matrices (5120 rows) at several waves per
-// SIMD.
+// are staged in LDS once per work-group (4 to 16 waves: the most that still let the whole grid be resident at once),
+// so the staging (~31 KB at K = 6144, 4 columns) is shared by up to 16 * RPW rows. Few rows per wave keep short
+// matrices (5120 rows) at several waves per SIMD.
 constexpr int Q8W_PF = 4;
+// the block record of the staged codes: NC columns of 32 bytes plus 16, so the 16 blocks that one LDS access of
+// 16 lanes reads start in 16 different 4-bank groups
+constexpr int q8w_xs(int nc) { return nc * 32 + 16; }
 
 template <int TYPE>
 struct Q8Regs {
@@ -282,18 +290,20 @@ struct Q8Regs {
 };
 
 template <int TYPE, int NC, int RPW>
-__global__ void __launch_bounds__(256) q8_wave_kernel(Q8Args a) {
+__global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
     extern __shared__ __align__(16) uint8_t q8_lds[];
     constexpr bool Q4 = TYPE == AQ_TYPE_Q4_0;
     constexpr int KS = 64 / RPW;
     const int nb = a.nb32;
-    int8_t *sx = reinterpret_cast<int8_t *>(q8_lds);                   // [nb][NC][32]
-    float *sxd = reinterpret_cast<float *>(q8_lds + (size_t)nb * NC * 32); // [nb][NC]
-    int32_t *sxs = reinterpret_cast<int32_t *>(sxd + (size_t)nb * NC);   // [nb][NC]
-    float *xch = reinterpret_cast<float *>(sxs + (size_t)nb * NC);       // [4 waves][NC][RPW rows][KS]
+    constexpr int XS = q8w_xs(NC);                                    // bytes per block record (NC columns)
+    int8_t *sx = reinterpret_cast<int8_t *>(q8_lds);                   // [nb][XS]: column c at c * 32
+    float *sxd = reinterpret_cast<float *>(q8_lds + (size_t)nb * XS);  // [NC][nb]
+    int32_t *sxs = reinterpret_cast<int32_t *>(sxd + (size_t)nb * NC); // [NC][nb]
+    float *xch = reinterpret_cast<float *>(sxs + (size_t)nb * NC);     // [waves][NC][RPW rows][KS]
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int r = lane / KS, ks = lane % KS;
-    const int row0 = ((int)blockIdx.x * 4 + wid) * RPW;
+    const int nwv = (int)(blockDim.x >> 6); // waves per work-group
+    const int row0 = ((int)blockIdx.x * nwv + wid) * RPW;
     int row = row0 + r;
     if (row >= a.rows) row = a.rows - 1;
     const size_t rowb = (size_t)row * nb;
@@ -308,17 +318,47 @@ __global__ void __launch_bounds__(256) q8_wave_kernel(Q8Args a) {
         w.d = *reinterpret_cast<const uint16_t *>(a.dm + wb * 2);
     };
     Q8Regs<TYPE> wr[Q8W_PF];
+    const int NT = (int)blockDim.x;
+    const int nh = nb * NC * 2; // 16-byte halves of the activation code blocks
+    auto half_src = [&](int e) {
+        const int rec = e >> 1, c = rec / nb, blk = rec - c * nb;
+        return reinterpret_cast<const uint4 *>(a.xq + (size_t)c * a.n + (size_t)blk * 32 + (e & 1) * 16);
+    };
+    auto half_dst = [&](int e) {
+        const int rec = e >> 1, c = rec / nb, blk = rec - c * nb;
+        return reinterpret_cast<uint4 *>(sx + (size_t)blk * XS + c * 32 + (e & 1) * 16);
+    };
+    const int ns = nb * NC; // block scales (and Q4_0 code sums) of the activations
+    if (nh <= 3 * NT && ns <= 2 * NT) { // uniform: the activations fit a few registers per thread
+        // loaded ahead of the first weights (every load issued, clamped), written after them: the LDS writes wait
+        // only for the activations
+        const int e0 = min((int)threadIdx.x, nh - 1), e1 = min((int)threadIdx.x + NT, nh - 1),
+                  e2 = min((int)threadIdx.x + 2 * NT, nh - 1);
+        const int s0 = min((int)threadIdx.x, ns - 1), s1 = min((int)threadIdx.x + NT, ns - 1);
+        const uint4 h0 = *half_src(e0), h1 = *half_src(e1), h2 = *half_src(e2);
+        const float xd0 = a.xd[s0], xd1 = a.xd[s1];
+        const int32_t xs0 = Q4 ? a.xs[s0] : 0, xs1 = Q4 ? a.xs[s1] : 0;
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int p = 0; p < Q8W_PF; p++) load(wr[p], p * KS + ks);
-    for (int e = (int)threadIdx.x; e < nb * NC * 2; e += 256) {
-        const int rec = e >> 1, half = e & 1, c = rec / nb, blk = rec - c * nb;
-        *reinterpret_cast<uint4 *>(sx + ((size_t)blk * NC + c) * 32 + half * 16) =
-            *reinterpret_cast<const uint4 *>(a.xq + (size_t)c * a.n + (size_t)blk * 32 + half * 16);
-    }
-    for (int e = (int)threadIdx.x; e < nb * NC; e += 256) {
-        const int c = e / nb, blk = e - c * nb;
-        sxd[blk * NC + c] = a.xd[(size_t)c * nb + blk];
-        if constexpr (Q4) sxs[blk * NC + c] = a.xs[(size_t)c * nb + blk];
+        for (int p = 0; p < Q8W_PF; p++) load(wr[p], p * KS + ks);
+        __builtin_amdgcn_sched_barrier(0);
+        *half_dst(e0) = h0; // past the end: the last entry again, with its own bytes
+        *half_dst(e1) = h1;
+        *half_dst(e2) = h2;
+        sxd[s0] = xd0; // same [column][block] order as the activations
+        sxd[s1] = xd1;
+        if constexpr (Q4) {
+            sxs[s0] = xs0;
+            sxs[s1] = xs1;
+        }
+    } else {
+#pragma unroll
+        for (int p = 0; p < Q8W_PF; p++) load(wr[p], p * KS + ks);
+        for (int e = (int)threadIdx.x; e < nh; e += NT) *half_dst(e) = *half_src(e);
+        for (int e = (int)threadIdx.x; e < nb * NC; e += NT) {
+            sxd[e] = a.xd[e];
+            if constexpr (Q4) sxs[e] = a.xs[e];
+        }
     }
     __syncthreads();
     if (row0 >= a.rows) return; // no barrier follows
@@ -345,14 +385,14 @@ __global__ void __launch_bounds__(256) q8_wave_kernel(Q8Args a) {
         float pr[NC];
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            const uint4 *xp = reinterpret_cast<const uint4 *>(sx + ((size_t)blkc * NC + c) * 32);
+            const uint4 *xp = reinterpret_cast<const uint4 *>(sx + (size_t)blkc * XS + c * 32);
             const uint4 x0 = xp[0], x1 = xp[1];
             const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             int isum = 0;
 #pragma unroll
             for (int i = 0; i < 8; i++) isum = dot4(wq[i], xs[i], isum);
-            if constexpr (Q4) isum -= 8 * sxs[blkc * NC + c];
-            pr[c] = (dw * sxd[blkc * NC + c]) * (float)isum;
+            if constexpr (Q4) isum -= 8 * sxs[c * nb + blkc];
+            pr[c] = (dw * sxd[c * nb + blkc]) * (float)isum;
         }
         if (prefetch) {
             __builtin_amdgcn_sched_barrier(0);
@@ -557,6 +597,22 @@ __global__ void __launch_bounds__(256) f32_matmul_kernel(Q8Args a) {
     }
 }
 
+// Work-groups of `fn` (`threads` threads, `lds` dynamic bytes) resident on the whole device at once.
+inline long q8_capacity(const void *fn, int threads, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::tuple<const void *, int, size_t>, long> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_tuple(fn, threads, lds);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) != hipSuccess)
+        return 0;
+    return cache[key] = (long)per_cu * cus;
+}
+
 template <int NC>
 int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
     if (args.type == AQ_TYPE_F32) {
@@ -567,17 +623,37 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
     }
     {
         // the wave kernel: activations staged in LDS
-        const size_t lds = (size_t)args.nb32 * NC * (32 + 8) + (size_t)4 * NC * 64 * 4;
-        if (lds <= 64 * 1024) {
-            // rows per wave: the most that still give the grid about four waves per SIMD
-            const int rpw = args.rows >= 16384 ? 4 : (args.rows >= 8192 ? 2 : 1);
-            const dim3 grid((unsigned)((args.rows + 4 * rpw - 1) / (4 * rpw)));
+        const size_t stage = (size_t)args.nb32 * (q8w_xs(NC) + NC * 8), xw = (size_t)NC * 64 * 4; // per wave
+        if (stage + 4 * xw <= 64 * 1024) {
+            // rows per wave: the most that still give the grid about four waves per SIMD (one column: two rows
+            // from 4096, measured faster for the MTP's Q4_0 matrices)
+            const int rpw = args.rows >= 16384 ? 4 : (args.rows >= 8192 || (NC == 1 && args.rows >= 4096) ? 2 : 1);
             const bool q4 = args.type == AQ_TYPE_Q4_0;
+            const void *k4[2] = {(const void *)&q8_wave_kernel<AQ_TYPE_Q8_0, NC, 4>,
+                                 (const void *)&q8_wave_kernel<AQ_TYPE_Q4_0, NC, 4>};
+            const void *k2[2] = {(const void *)&q8_wave_kernel<AQ_TYPE_Q8_0, NC, 2>,
+                                 (const void *)&q8_wave_kernel<AQ_TYPE_Q4_0, NC, 2>};
+            const void *k1[2] = {(const void *)&q8_wave_kernel<AQ_TYPE_Q8_0, NC, 1>,
+                                 (const void *)&q8_wave_kernel<AQ_TYPE_Q4_0, NC, 1>};
+            const void *fn = (rpw == 4 ? k4 : rpw == 2 ? k2 : k1)[q4 ? 1 : 0];
+            // waves per work-group: the largest of 16, 8, 4 whose grid is resident in one pass
+            int nwv = 4;
+            for (int w : {16, 8}) {
+                const size_t lds = stage + w * xw;
+                const long grid = (args.rows + (long)w * rpw - 1) / ((long)w * rpw);
+                if (lds <= 64 * 1024 && grid <= q8_capacity(fn, 64 * w, lds)) {
+                    nwv = w;
+                    break;
+                }
+            }
+            const size_t lds = stage + nwv * xw;
+            const int rpg = nwv * rpw; // rows per work-group
+            const dim3 grid((unsigned)((args.rows + rpg - 1) / rpg)), block(64 * nwv);
 #define AQ_Q8W(R)                                                                                             \
     if (q4)                                                                                                   \
-        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q4_0, NC, R>), grid, dim3(256), lds, stream, args);          \
+        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q4_0, NC, R>), grid, block, lds, stream, args);              \
     else                                                                                                      \
-        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q8_0, NC, R>), grid, dim3(256), lds, stream, args);
+        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q8_0, NC, R>), grid, block, lds, stream, args);
             if (rpw == 4) {
                 AQ_Q8W(4)
             } else if (rpw == 2) {
