@@ -587,6 +587,10 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
         a.base = kv->len;
         a.stride = kv->stride;
         a.out = s->act_att.f32;
+        // the o projection reads Q8_K: each head's output row (head_dim 256) is quantised by the attention kernel
+        const bool q8k = quant_kind_for(L.o.type) == QK_Q8K && c.head_dim == 256;
+        a.out_q8k = q8k ? 1 : 0;
+        a.q8k = s->act_att;
         a.t = (int)t;
         a.nh = (int)c.n_head;
         a.nkv = (int)c.n_head_kv;
@@ -594,9 +598,11 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
         a.rd = (int)c.rope_dim;
         if ((rc = launch_attention(a, s->stream))) return rc;
         kv->len += t;
-        Needs no;
-        no.add(L.o);
-        if ((rc = quantize_act(s, s->act_att, t, no))) return rc;
+        if (!q8k) {
+            Needs no;
+            no.add(L.o);
+            if ((rc = quantize_act(s, s->act_att, t, no))) return rc;
+        }
         return mm(s, L.o, s->act_att, t, y_out, resid);
     }
     float *mixed = mode == VERIFY ? s->sv_mixed[dn_slot] : s->mixed;
@@ -624,6 +630,10 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
     d.rec = s->rec[dn_slot];
     d.write_state = mode == VERIFY ? 0 : 1;
     d.out = s->act_vd.f32;
+    // ssm_out reads Q8_0: each head's output rows are whole 32-blocks, quantised by the DeltaNet kernel itself
+    const bool q80 = quant_kind_for(L.ssm_out.type) == QK_Q80 && c.dn_head_dim_v % 32 == 0;
+    d.out_q80 = q80 ? 1 : 0;
+    d.q80 = s->act_vd;
     d.t = (int)t;
     d.nk = (int)c.dn_n_k_heads;
     d.nv = (int)c.dn_n_v_heads;
@@ -631,9 +641,11 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
     d.dv = (int)c.dn_head_dim_v;
     d.kernel = (int)c.dn_conv_kernel;
     if ((rc = launch_dn_core(d, s->stream))) return rc;
-    Needs no;
-    no.add(L.ssm_out);
-    if ((rc = quantize_act(s, s->act_vd, t, no))) return rc;
+    if (!q80) {
+        Needs no;
+        no.add(L.ssm_out);
+        if ((rc = quantize_act(s, s->act_vd, t, no))) return rc;
+    }
     return mm(s, L.ssm_out, s->act_vd, t, y_out, resid);
 }
 

@@ -53,6 +53,8 @@ struct DnArgs {
     float *rec = nullptr; // nv x dk x dv recurrent state
     int write_state = 0;
     float *out = nullptr; // t x vd gated-norm output (null: none)
+    int out_q80 = 0;      // also the Q8_0 form of `out` into q80 (its rows = the t rows; vd and dv multiples of 32)
+    Act q80;
     int t = 0, nk = 0, nv = 0, dk = 0, dv = 0, kernel = 0;
     // raw mode (the isolated recurrence): q, k (t x nk*dk), v (t x nv*dv), g, beta (t x nv) used as given
     int raw = 0;
@@ -75,6 +77,8 @@ struct AttnArgs {
     size_t base = 0;             // cache rows before row 0
     size_t stride = 0;           // nkv*hd
     float *out = nullptr;        // t x nh*hd
+    int out_q8k = 0; // also the Q8_K form of `out` into q8k (head_dim 256: one head row = one 256-block)
+    Act q8k;
     int t = 0, nh = 0, nkv = 0, hd = 0, rd = 0;
 };
 // Norm + RoPE of q and k, K/V appended at cache rows base..base+t, then per (head, row) softmax attention over

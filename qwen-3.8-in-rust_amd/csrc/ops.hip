@@ -529,8 +529,18 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
         }
         __syncthreads();
         if (has_v)
-            for (int i = 0; i < t; i++)
-                a.out[(size_t)i * vd + p * DV + j] = (a.ssm_norm[j] * (so[i][j] * ro[i])) * sz[i][j];
+            for (int i = 0; i < t; i++) {
+                const float v = (a.ssm_norm[j] * (so[i][j] * ro[i])) * sz[i][j];
+                a.out[(size_t)i * vd + p * DV + j] = v;
+                so[i][j] = v; // this thread's own element: read just above
+            }
+        if (a.out_q80) { // uniform: the head's rows are whole 32-blocks of the Q8_0 form (quant.rs quantize_q8_0)
+            __syncthreads();
+            for (int task = j; task < t * (DV / 32); task += DN_THREADS) {
+                const int i = task / (DV / 32), blk = task % (DV / 32);
+                q8_0_block_store(a.q80, i, (size_t)p * (DV / 32) + blk, &so[i][blk * 32]);
+            }
+        }
     }
 }
 
@@ -672,7 +682,16 @@ __global__ void __launch_bounds__(256) attn_core_kernel(AttnArgs a) {
         }
         for (; tt < len; tt++) acc += sc[tt] * vc[tt * a.stride];
         const float gate = a.qg[(size_t)i * 2 * a.nh * hd + (size_t)h * 2 * hd + hd + d];
-        a.out[(size_t)i * a.nh * hd + (size_t)h * hd + d] = acc * sigmoid_f(gate);
+        const float o = acc * sigmoid_f(gate);
+        a.out[(size_t)i * a.nh * hd + (size_t)h * hd + d] = o;
+        if (a.out_q8k) qs[d] = o; // q is no longer read
+    }
+    if (a.out_q8k) { // uniform: this head's output row is block h of row i's Q8_K form (hd == 256)
+        __syncthreads();
+        if (tid < 64) {
+            const float v[4] = {qs[4 * tid], qs[4 * tid + 1], qs[4 * tid + 2], qs[4 * tid + 3]};
+            q8k_block_store(a.q8k, i, h, v, tid);
+        }
     }
 }
 
@@ -867,6 +886,9 @@ int launch_dn_core(const DnArgs &a, hipStream_t stream) {
         AQ_REQUIRE(a.kernel == 4, "deltanet: conv kernel must be 4 in this build");
         AQ_REQUIRE(a.mixed && a.a && a.b && a.conv_src && a.conv_w && a.ssm_a && a.dt_bias, "deltanet: inputs");
         AQ_REQUIRE(!a.out || (a.z && a.ssm_norm), "deltanet: output needs z and ssm_norm");
+        AQ_REQUIRE(!a.out_q80 || (a.out && a.dv % 32 == 0 && a.q80.q0 && a.q80.n == (size_t)a.nv * a.dv &&
+                                  a.q80.ncols >= (size_t)a.t),
+                   "deltanet: Q8_0 output needs whole 32-blocks and a buffer of t rows of nv * dv");
     } else {
         AQ_REQUIRE(a.rq && a.rk && a.rv && a.rg && a.rbeta, "deltanet: raw inputs");
     }
@@ -914,6 +936,8 @@ int launch_attention(const AttnArgs &a, hipStream_t stream) {
     if (rc) return rc;
     const size_t shmem = (a.hd + a.base + a.t + 32) * sizeof(float);
     AQ_REQUIRE(shmem <= 160 * 1024, "attention: context too long for one work-group's LDS");
+    AQ_REQUIRE(!a.out_q8k || (a.hd == 256 && a.q8k.qs && a.q8k.n == (size_t)a.nh * 256 && a.q8k.ncols >= (size_t)a.t),
+               "attention: Q8_K output needs head_dim 256 and a buffer of t rows of nh * 256");
     hipLaunchKernelGGL(attn_core_kernel, dim3((unsigned)a.nh, (unsigned)a.t), dim3(256), shmem, stream, a);
     return launched("attention");
 }
