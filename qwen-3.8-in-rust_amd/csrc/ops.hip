@@ -133,7 +133,37 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
         }
     }
     __syncthreads();
-    if constexpr (PL > 0) {
+    if constexpr (PL < 0) {
+        // all 8 chains in wave 0, each on its own SIMD pass: chain c in lanes 8c..8c+7, lane 8c+j holds the chain's
+        // terms T*j .. T*j + T - 1 in registers (zeros past the chain's end); after each lane's terms the running
+        // sum moves one lane up (DPP row shift), so lane 8c+7 ends with chain c summed in order. One wave on its
+        // SIMD issues an add every pass; chains in 8 waves would share each SIMD between two of them.
+        constexpr int T = -PL;
+        static_assert(T % 4 == 0, "whole float4s of terms per lane");
+        if (tid < 64) {
+            const int c = lane >> 3, j = lane & 7;
+            const float4 *src = reinterpret_cast<const float4 *>(sq + c * cs + T * j);
+            float r[T];
+#pragma unroll
+            for (int k = 0; k < T / 4; k++) {
+                // clen is a multiple of 4 on this path, so a float4 lies wholly inside or outside the chain
+                const float4 f = T * j + 4 * k < clen ? src[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                r[4 * k] = f.x;
+                r[4 * k + 1] = f.y;
+                r[4 * k + 2] = f.z;
+                r[4 * k + 3] = f.w;
+            }
+            float acc = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                if (m > 0) acc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
+                                                                                      0x111, 0xF, 0xF, false));
+#pragma unroll
+                for (int k = 0; k < T; k++) acc += r[k];
+            }
+            if (j == 7) red[c] = acc;
+        }
+    } else if constexpr (PL > 0) {
         // chain w runs in wave w: lane m holds the chain's terms PL*m .. PL*m + PL - 1 in registers; the running sum
         // moves one lane up after each lane's terms (DPP wave shift), so lane 63 ends with the whole chain, summed in
         // order with every term an add of a register (no LDS read on the chain's path)
@@ -831,10 +861,15 @@ int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, s
         // slices of whole 256-blocks (about five blocks each) when the row is made of them
         const int nblk = n % 256 == 0 ? (int)(n / 256) : 0;
         const unsigned slices = nblk >= 8 ? (unsigned)((nblk + 4) / 5) : 1;
-        // chain terms per lane in the register chain (the smallest built count that holds a chain), else LDS
-        const int clen = (int)(n / 8), need = (clen + 63) / 64;
+        // chain terms per lane: 8 lanes per chain in one wave when a chain is whole float4s and fits (negative
+        // counts), else one wave per chain (the smallest built count that holds a chain), else LDS
+        const int clen = (int)(n / 8), need8 = (clen + 7) / 8, need = (clen + 63) / 64;
+        const int t8s[] = {4, 8, 16, 24, 32, 48, 64, 80, 96};
         const int pls[] = {1, 2, 4, 6, 8, 10, 12, 16};
         int pl = 0;
+        if (clen % 4 == 0)
+            for (int c : t8s)
+                if (!pl && c >= need8) pl = -c;
         for (int c : pls)
             if (!pl && c >= need) pl = c;
         const dim3 grid((unsigned)t, slices);
@@ -845,6 +880,7 @@ int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, s
                            y_f32, y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0);              \
         break;
             AQ_RN(0) AQ_RN(1) AQ_RN(2) AQ_RN(4) AQ_RN(6) AQ_RN(8) AQ_RN(10) AQ_RN(12) AQ_RN(16)
+            AQ_RN(-4) AQ_RN(-8) AQ_RN(-16) AQ_RN(-24) AQ_RN(-32) AQ_RN(-48) AQ_RN(-64) AQ_RN(-80) AQ_RN(-96)
 #undef AQ_RN
         }
         return launched("rmsnorm");
