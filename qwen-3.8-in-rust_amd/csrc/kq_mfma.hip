@@ -810,10 +810,13 @@ inline int kq_pick_chunk(int nb, int nc, bool has45, bool has6, int ksw) {
     return c < unit ? unit : c;
 }
 
-// Grid: one tile per wave while the tiles are fewer than KQ_PERSIST tiles per resident wave (or the staging is
-// chunked): work-groups past the resident ones start as others end; otherwise a persistent grid of exactly the
-// resident work-groups, shared between the segments by weight bytes, each wave then streaming several tiles.
-constexpr int KQ_PERSIST = 1;
+// Grid. One tile per wave, work-groups past the resident ones starting as others end, when the tiles fit the
+// resident waves, when the staging is chunked, when F32 segments are present (their work-groups end early and
+// free their slots) or when there are more than KQ_DYN tiles per resident wave (the dispatcher then balances the
+// long stream over CUs that run at unequal speed). Otherwise a persistent grid: the resident work-groups shared
+// between the segments by weight bytes, then trimmed so that every wave of a segment streams the same number of
+// tiles (no wave runs a tile more than the others while the rest of the device idles).
+constexpr int KQ_DYN = 8;
 template <int T0, int T1, int NC, int KSW>
 int launch_wave_ks(KqGroup G, hipStream_t stream) {
     constexpr int RW = 16 / KSW; // rows per tile
@@ -845,7 +848,7 @@ int launch_wave_ks(KqGroup G, hipStream_t stream) {
         bytes += (double)t * block_bytes(sg.type);
     }
     const long cap = kq_capacity(fn, lds) - f32_wgs;
-    const bool persistent = G.chk >= G.nb && cap >= G.nseg && tiles > KQ_PERSIST * 4 * cap;
+    const bool persistent = G.chk >= G.nb && f32_wgs == 0 && cap >= G.nseg && tiles > 4 * cap && tiles <= KQ_DYN * 4 * cap;
     // the F32 segments' work-groups take the lowest indices: dispatched first, they are done early and free their
     // slots for the K-quant work-groups past the resident ones
     std::stable_partition(G.seg, G.seg + G.nseg, [](const KqSeg &sg) { return sg.type == AQ_TYPE_F32; });
@@ -861,6 +864,8 @@ int launch_wave_ks(KqGroup G, hipStream_t stream) {
             if (persistent) {
                 n = (long)((double)cap * ((double)t * block_bytes(sg.type)) / bytes);
                 n = n < 1 ? 1 : (n > need ? need : n);
+                const long per = (t + 4 * n - 1) / (4 * n); // tiles per wave
+                n = (t + 4 * per - 1) / (4 * per);
             }
         }
         sg.nwg = (int)n;
