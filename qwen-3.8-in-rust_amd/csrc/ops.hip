@@ -289,29 +289,31 @@ __global__ void __launch_bounds__(256) swiglu_q80_kernel(const float *g, const f
 }
 
 // ------------------------------------------------------------------------------------------ Gated DeltaNet
-// One work-group of 256 threads per V head p (K head p % nk, gated_deltanet.rs:172). Per row
+// One work-group of 512 threads per V head p (K head p % nk, gated_deltanet.rs:172). Per row
 // (gated_deltanet.rs:261-375, deltanet.rs:19-86, conv.rs:11-36):
 //   conv step + SiLU of the head's q/k/v channels; l2norm(q), l2norm(k) (eps 1e-6, sequential sums);
 //   q *= 1/sqrt(dk); g = ssm_a * softplus(a + dt_bias); beta = sigmoid(b);
 //   S *= exp(g); kv = sum_k S[k][v] k[k]; delta = (v - kv) beta; S[k][v] += k[k] delta; o = sum_k S[k][v] q[k];
 //   y = (w * (o * inv_rms(o))) * silu(z)  (rmsnorm.rs:37-46).
 // Only the recurrence is sequential over rows, so everything else runs for all rows at once, each sum still in
-// one lane in the reference's order:
+// the reference's order:
 //   A  every thread: conv + SiLU of whole channels over all rows, silu(z), and the 32-element alpha/beta partials
-//      (dot.rs:180-200); the state column of thread j (S[.][j], registers) is loaded meanwhile;
-//   B  wave 0: the 2t l2norm sums; wave 1: the 2t alpha/beta block chains, then the gates per row;
+//      (dot.rs:180-200);
+//   B  waves 4 and 6: the 2t l2norm sums, 8 lanes per sum; waves 5 and 7: the alpha / beta block chains, then the
+//      decays / betas per row; waves 0-3: the state column of thread j (S[.][j], registers) is loaded meanwhile;
 //   C  thread j < dv: the recurrence of column j, row after row, with no barrier between rows;
-//   D  wave 0: the output RMS of each row (8 lanes of the reduce8 pattern per row); every thread: gated output.
+//   D  wave 0: the output RMS of each row (8 lanes of the reduce8 pattern per row); thread j < dv: the gated
+//      output, and its Q8_0 form per half wave.
 // The state is written back only when asked (write_state); the conv windows go to conv_dst (a second buffer, so
 // work-groups sharing a K head never read a window another one has already advanced): v channels by every head,
 // q/k channels by head p == kh.
 constexpr int DN_TMAX = 8;      // rows per DeltaNet launch
 constexpr int DN_BLK_MAX = 256; // 32-blocks of the alpha/beta rows (hidden <= 8192)
-constexpr int DN_THREADS = 512; // waves 0-3 hold state columns (dv <= 256); 4 and 5 run the per-row sums
+constexpr int DN_THREADS = 512; // waves 0-3 hold state columns (dv <= 256); 4-6 run the per-row sums
 
 template <int DK, int DV>
 __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const int t) {
-    static_assert(DK <= 256 && DV <= 256 && DN_THREADS >= 384 && DN_TMAX * 8 <= 64, "DeltaNet work-group shape");
+    static_assert(DK <= 256 && DV <= 256 && DN_THREADS >= 448 && DN_TMAX * 2 <= 16, "DeltaNet work-group shape");
     __shared__ float sq[DN_TMAX][DK], sk[DN_TMAX][DK], sv[DN_TMAX][DV], sz[DN_TMAX][DV], so[DN_TMAX][DV];
     __shared__ float part[2][DN_TMAX][DN_BLK_MAX];
     __shared__ float rdec[DN_TMAX], rbeta[DN_TMAX], rq[DN_TMAX], rk[DN_TMAX], ro[DN_TMAX];
@@ -320,6 +322,22 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
     const int kd = a.nk * DK, vd = a.nv * DV, cd = 2 * kd + vd;
     const bool has_v = j < DV;
     const bool gated = a.out && !a.raw;
+    // the gate inputs, loaded before phase A so their latency hides behind it: wave 5 computes the decays and
+    // wave 7 the betas (lane i = row i), each in its own wave so neither waits for the other's branch
+    const bool gate_lane = (wave == 5 || wave == 7) && lane < t;
+    const int gr = wave == 5 ? 0 : 1;
+    float gv = 0.0f, gsa = 0.0f, gdt = 0.0f;
+    if (gate_lane) {
+        if (a.raw)
+            gv = (gr == 0 ? a.rg : a.rbeta)[(size_t)lane * a.nv + p];
+        else if (!a.x)
+            gv = (gr == 0 ? a.a : a.b)[(size_t)lane * a.nv + p];
+        if (gr == 0 && !a.raw) {
+            gsa = a.ssm_a[p];
+            gdt = a.dt_bias[p];
+        }
+    }
+    const float nrm_w = gated && has_v ? a.ssm_norm[j] : 0.0f; // phase D's norm weight
 
     // ---- A: channels over all rows
     if (a.raw) {
@@ -429,8 +447,42 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
     }
     __syncthreads();
 
-    // ---- B: norms (wave 4) and gates (wave 5), one sum per lane
-    if (wave == 4 && !a.raw && lane < 2 * t) {
+    // ---- B: norms (waves 4 and 6) and gates (waves 5 and 7)
+    if constexpr (DK % 32 == 0) {
+        // chain c = the sum of squares of q (c even) or k (c odd) of row c / 2, in 8 lanes of wave 4 (chains 0-7) or
+        // 6 (8-15): lane m of the chain holds its terms m*T .. m*T + T - 1 as registers and the running sum moves
+        // one lane up after each lane's terms (DPP row shift), so lane 7 of the group ends with the whole sum,
+        // added in order
+        if ((wave == 4 || wave == 6) && !a.raw) {
+            constexpr int T = DK / 8;
+            const int c = (wave == 4 ? 0 : 8) + (lane >> 3), m = lane & 7, cc = c < 2 * t ? c : 0;
+            const float4 *x4 = reinterpret_cast<const float4 *>((cc & 1) ? sk[cc >> 1] : sq[cc >> 1]) + m * (T / 4);
+            float r[T];
+#pragma unroll
+            for (int u = 0; u < T / 4; u++) {
+                const float4 f = x4[u];
+                r[4 * u] = f.x * f.x;
+                r[4 * u + 1] = f.y * f.y;
+                r[4 * u + 2] = f.z * f.z;
+                r[4 * u + 3] = f.w * f.w;
+            }
+            float ss = 0.0f;
+#pragma unroll
+            for (int st = 0; st < 8; st++) {
+                if (st > 0) ss = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, ss),
+                                                                                      0x111, 0xF, 0xF, false));
+#pragma unroll
+                for (int u = 0; u < T; u++) ss += r[u];
+            }
+            if (m == 7 && c < 2 * t) {
+                const float inv = 1.0f / sqrtf(ss + 1e-6f); // deltanet.rs:19-29 l2norm
+                if (c & 1)
+                    rk[c >> 1] = inv;
+                else
+                    rq[c >> 1] = inv;
+            }
+        }
+    } else if (wave == 4 && !a.raw && lane < 2 * t) { // one sum per lane
         const int i = lane >> 1;
         const float ss = seq_sum<true>((lane & 1) ? sk[i] : sq[i], 0, DK, 1, 0.0f);
         const float inv = 1.0f / sqrtf(ss + 1e-6f); // deltanet.rs:19-29 l2norm
@@ -439,22 +491,18 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
         else
             rq[i] = inv;
     }
-    if (wave == 5 && lane < 2 * t) {
-        const int r = lane / t, i = lane % t;
-        float v;
-        if (a.raw) {
-            v = (r == 0 ? a.rg : a.rbeta)[(size_t)i * a.nv + p];
-        } else if (a.x) {
+    if (gate_lane) {
+        const int i = lane;
+        float v = gv;
+        if (!a.raw && a.x) {
             // dot.rs:180-200: the block chain, `acc + part` with the short tail (0.0f when there is none)
             const int n = a.hidden, nblk = (n + 31) / 32;
-            v = seq_sum<false>(&part[r][i][0], 0, nblk, 1, 0.0f);
+            v = seq_sum<false>(&part[gr][i][0], 0, nblk, 1, 0.0f);
             if (n % 32 == 0) v = v + 0.0f;
-            (r == 0 ? a.a : a.b)[(size_t)i * a.nv + p] = v; // kept for the commit
-        } else {
-            v = (r == 0 ? a.a : a.b)[(size_t)i * a.nv + p];
+            (gr == 0 ? a.a : a.b)[(size_t)i * a.nv + p] = v; // kept for the commit
         }
-        if (r == 0) {
-            const float g = a.raw ? v : a.ssm_a[p] * softplus_f(v + a.dt_bias[p]); // deltanet.rs:32-35 gate_g
+        if (gr == 0) {
+            const float g = a.raw ? v : gsa * softplus_f(v + gdt); // deltanet.rs:32-35 gate_g
             rdec[i] = exp_f(g);
         } else {
             rbeta[i] = a.raw ? v : sigmoid_f(v);
@@ -548,29 +596,27 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
             constexpr int n8 = DV / 8 * 8;
             const int i = lane >> 3, m = lane & 7;
             const float part8 = i < t ? seq_sum<true>(so[i < t ? i : 0], m, n8, 8, 0.0f) : 0.0f;
-            float l8[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) l8[u] = __shfl(part8, (lane & ~7) + u);
+            // reduce8 on the DPP network: lane m + (l_m + l_m+4), then lanes 0, 1 + the pair two up, then lane 0
+            // + lane 1: ((l0 + l4) + (l2 + l6)) + ((l1 + l5) + (l3 + l7))
+            float r8 = part8;
+            r8 = r8 + __int_as_float(dpp_mov<0x104>(__float_as_int(r8))); // row_shl:4
+            r8 = r8 + __int_as_float(dpp_mov<0x102>(__float_as_int(r8))); // row_shl:2
+            r8 = r8 + __int_as_float(dpp_mov<0x101>(__float_as_int(r8))); // row_shl:1
             if (m == 0 && i < t) {
-                float ss = reduce8_f(l8);
+                float ss = r8;
                 for (int e = n8; e < DV; e++) ss += so[i][e] * so[i][e];
                 ro[i] = 1.0f / sqrtf(ss / (float)DV + a.eps);
             }
         }
         __syncthreads();
+        // the gated output, and with out_q80 its Q8_0 form (quant.rs quantize_q8_0): the head's rows are whole
+        // 32-blocks, one per half wave of the state columns (has_v is uniform over each half wave: DV % 32 == 0)
         if (has_v)
             for (int i = 0; i < t; i++) {
-                const float v = (a.ssm_norm[j] * (so[i][j] * ro[i])) * sz[i][j];
+                const float v = (nrm_w * (so[i][j] * ro[i])) * sz[i][j];
                 a.out[(size_t)i * vd + p * DV + j] = v;
-                so[i][j] = v; // this thread's own element: read just above
+                if (a.out_q80) q8_0_block_half(a.q80, i, (size_t)p * (DV / 32) + (j >> 5), v, lane);
             }
-        if (a.out_q80) { // uniform: the head's rows are whole 32-blocks of the Q8_0 form (quant.rs quantize_q8_0)
-            __syncthreads();
-            for (int task = j; task < t * (DV / 32); task += DN_THREADS) {
-                const int i = task / (DV / 32), blk = task % (DV / 32);
-                q8_0_block_store(a.q80, i, (size_t)p * (DV / 32) + blk, &so[i][blk * 32]);
-            }
-        }
     }
 }
 

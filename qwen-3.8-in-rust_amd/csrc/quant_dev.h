@@ -153,6 +153,50 @@ __device__ __forceinline__ void q8k_block_store(const Act &a, size_t col, size_t
     q8k_block_wave(x, lane, a.qs + col * a.n + blk * 256, a.d + m, a.bs + m * 16, a.q8s + m * 8);
 }
 
+// Max / sum of ints over each 32-lane half of a wave (order-free, so exact): every lane gets its half's value. The
+// lanes of a half that is used must all be active.
+__device__ __forceinline__ int half_max_i32(int v, int lane) {
+    v = max(v, dpp_mov<0xB1>(v));
+    v = max(v, dpp_mov<0x4E>(v));
+    v = max(v, dpp_mov<0x124>(v));
+    v = max(v, dpp_mov<0x128>(v));
+    v = max(v, dpp_mov<0x142, 0xA>(v)); // row_bcast:15 into rows 1 and 3: lanes 31 and 63 hold their half's max
+    const int lo = __builtin_amdgcn_readlane(v, 31), hi = __builtin_amdgcn_readlane(v, 63);
+    return lane < 32 ? lo : hi;
+}
+__device__ __forceinline__ int half_sum_i32(int v, int lane) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x124>(v);
+    v += dpp_mov<0x128>(v);
+    v += dpp_mov<0x142, 0xA>(v);
+    const int lo = __builtin_amdgcn_readlane(v, 31), hi = __builtin_amdgcn_readlane(v, 63);
+    return lane < 32 ? lo : hi;
+}
+
+// One Q8_0 block (32 values) per 32-lane half of a wave, lane l of the half holding element l: the d, id, codes
+// and code sum of q8_0_block_store below (a NaN is passed over by the maximum as there). `lane` is the wave lane.
+__device__ __forceinline__ void q8_0_block_half(const Act &a, size_t col, size_t blk, float v, int lane) {
+    const float av = fabsf(v);
+    const int key = half_max_i32(av > 0.0f ? __float_as_int(av) : 0, lane); // |v| >= 0: int order is float order
+    const float dd = __int_as_float(key) / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    const float r = roundf(v * id);
+    const int qi = r > 127.0f ? 127 : (r < -128.0f ? -128 : (int)r);
+    const int sum = half_sum_i32(qi, lane);
+    const int l = lane & 31;
+    a.q0[col * a.n + blk * 32 + l] = (int8_t)qi;
+    if (l == 0) {
+        const _Float16 hd = (_Float16)dd;
+        uint16_t hbits;
+        __builtin_memcpy(&hbits, &hd, 2);
+        const size_t m = col * a.nb32 + blk;
+        a.d0[m] = (float)hd;
+        a.h0[m] = hbits;
+        a.s0[m] = sum;
+    }
+}
+
 // One Q8_0 block (32 values) by one lane. Q8Row::quantize_scalar_into (q8.rs:81-121): d = amax/127 -> f16
 // (round to nearest even), id = d != 0 ? 1/d : 0 from the unrounded d, q = round_half_away(x*id) saturated.
 __device__ __forceinline__ void q8_0_block_store(const Act &a, size_t col, size_t blk, const float *v) {
