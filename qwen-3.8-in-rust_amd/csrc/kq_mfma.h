@@ -816,10 +816,12 @@ inline int kq_capacity(const void *fn, size_t lds) {
 }
 
 // Super-blocks per activation staging chunk: all of K when the work-group's LDS stays within the budget that
-// leaves room for three work-groups per CU (two above four columns), else the largest multiple of KSW * PF that
-// does (the waves then meet at a barrier between chunks).
+// leaves room for two work-groups per CU, else the largest multiple of KSW * PF that does (the waves then meet at a
+// barrier between chunks). Measured on the 5120-row matrices with K = 17408 (N = 4, 1280 tiles, 320 work-groups):
+// a 76 KB budget (chunks of 48 super-blocks, one re-staging) 24.6 / 28.3 us for Q4_K / Q6_K, a 52 KB one (three
+// work-groups per CU, chunks of 32) 25.1 / 29.4 us.
 inline int kq_pick_chunk(int nb, int nc, bool has45, bool has6, int ksw, int pf) {
-    const size_t budget = (size_t)(nc <= 4 ? 52 : 76) * 1024;
+    const size_t budget = (size_t)76 * 1024;
     const size_t x = kq_xch_bytes_rt(nc, ksw), per = kq_sb_lds_bytes(nc, has45, has6);
     if (x + per * nb <= budget) return nb;
     const int unit = ksw * pf;
