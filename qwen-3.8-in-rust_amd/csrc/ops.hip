@@ -695,18 +695,31 @@ __global__ void __launch_bounds__(256) attn_core_kernel(AttnArgs a) {
         const float *kr = a.kcache + tt * a.stride + (size_t)kvh * hd;
         float acc = 0.0f;
         int d = 0;
-        for (; d + 32 <= hd; d += 32) { // 8 loads in flight; the sum stays sequential in d
-            float4 kv4[8];
+        // 16 float4s in flight while the previous 16 are summed (double buffer); the sum stays sequential in d
+        const float4 *k4 = reinterpret_cast<const float4 *>(kr);
+        const int ng = hd / 64;
+        float4 ka[16], kb[16];
+        if (ng > 0) {
 #pragma unroll
-            for (int u = 0; u < 8; u++) kv4[u] = *reinterpret_cast<const float4 *>(kr + d + 4 * u);
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                acc += qs[d + 4 * u] * kv4[u].x;
-                acc += qs[d + 4 * u + 1] * kv4[u].y;
-                acc += qs[d + 4 * u + 2] * kv4[u].z;
-                acc += qs[d + 4 * u + 3] * kv4[u].w;
-            }
+            for (int u = 0; u < 16; u++) ka[u] = k4[u];
         }
+        for (int g = 0; g < ng; g++) {
+            if (g + 1 < ng) {
+#pragma unroll
+                for (int u = 0; u < 16; u++) kb[u] = k4[(g + 1) * 16 + u];
+            }
+            const float *qg = qs + g * 64;
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                acc += qg[4 * u] * ka[u].x;
+                acc += qg[4 * u + 1] * ka[u].y;
+                acc += qg[4 * u + 2] * ka[u].z;
+                acc += qg[4 * u + 3] * ka[u].w;
+            }
+#pragma unroll
+            for (int u = 0; u < 16; u++) ka[u] = kb[u];
+        }
+        d = ng * 64;
         for (; d < hd; d += 8) { // hd % 8 == 0
             const float4 k0 = *reinterpret_cast<const float4 *>(kr + d);
             const float4 k1 = *reinterpret_cast<const float4 *>(kr + d + 4);
@@ -748,15 +761,26 @@ __global__ void __launch_bounds__(256) attn_core_kernel(AttnArgs a) {
     for (int d = tid; d < hd; d += 256) {
         const float *vc = a.vcache + (size_t)kvh * hd + d;
         float acc = 0.0f;
-        size_t tt = 0;
-        for (; tt + 8 <= len; tt += 8) { // 8 loads in flight; the sum stays sequential in tt
-            float v[8];
+        // 16 positions' loads in flight while the previous 16 are summed (double buffer); the sum stays
+        // sequential in tt
+        constexpr int VB = 16;
+        const size_t ng = len / VB;
+        float va[VB], vb[VB];
+        if (ng > 0) {
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = vc[(tt + u) * a.stride];
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc += sc[tt + u] * v[u];
+            for (int u = 0; u < VB; u++) va[u] = vc[(size_t)u * a.stride];
         }
-        for (; tt < len; tt++) acc += sc[tt] * vc[tt * a.stride];
+        for (size_t g = 0; g < ng; g++) {
+            if (g + 1 < ng) {
+#pragma unroll
+                for (int u = 0; u < VB; u++) vb[u] = vc[((g + 1) * VB + u) * a.stride];
+            }
+#pragma unroll
+            for (int u = 0; u < VB; u++) acc += sc[g * VB + u] * va[u];
+#pragma unroll
+            for (int u = 0; u < VB; u++) va[u] = vb[u];
+        }
+        for (size_t tt = ng * VB; tt < len; tt++) acc += sc[tt] * vc[tt * a.stride];
         const float gate = a.qg[(size_t)i * 2 * a.nh * hd + (size_t)h * 2 * hd + hd + d];
         const float o = acc * sigmoid_f(gate);
         a.out[(size_t)i * a.nh * hd + (size_t)h * hd + d] = o;
