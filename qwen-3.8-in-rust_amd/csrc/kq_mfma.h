@@ -326,10 +326,10 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
 // from HBM into a register ring PF rounds deep.
 //
 // The 16 matrix-core blocks of a wave are (q, j): j = the lane pair (j, j+4), q = (row group rg, K slice ks) with
-// KSW K slices per wave (1, 2 or 4) and 4 / KSW row groups of 4 rows: a wave owns 16 / KSW rows and in round rd
-// its K slice ks computes super-block rd * KSW + ks. Tall matrices (gate, up) take KSW = 1; short ones (down,
-// ssm_out: 5120 rows) split K four ways inside the wave, so a wave covers 4 rows and the grid still holds enough
-// waves to keep HBM busy. The f32 chains stay the reference's sequential sums: each round the K slices hand their
+// KSW K slices per wave (2 or 4) and 4 / KSW row groups of 4 rows: a wave owns 16 / KSW rows and in round rd its
+// K slice ks computes super-block rd * KSW + ks. Matrices split K four ways inside the wave, so a wave covers 4 rows
+// and the grid holds enough waves even for the 5120-row ones; K below 4 super-blocks and the lm_head take two
+// slices (kq_pick_ksw). The f32 chains stay the reference's sequential sums: each round the K slices hand their
 // products to the chain owners through the wave's own LDS slot (no work-group barrier; one wave's LDS accesses
 // execute in order), and the owner of a chain adds the KSW products in super-block order.
 //
@@ -797,8 +797,12 @@ inline size_t kq_sb_lds_bytes(int nc, bool has45, bool has6) {
     return (size_t)nc * KQ_XS + (size_t)ncp * 4 + (size_t)np * ncp * 4;
 }
 
-// K slices per wave: four (tiles of 4 rows, so work divides finely over the waves), two for K below 4 super-blocks.
-inline int kq_pick_ksw(int nb) { return nb < 4 ? 2 : 4; }
+// K slices per wave: four (tiles of 4 rows, so work divides finely over the waves), two for K below 4 super-blocks
+// and for the lm_head-sized matrices (at least KQ_TALL_ROWS rows: tiles of 8 rows, a long stream either way).
+// Measured (MI355X, Q6_K 248320 x 5120): N = 1 188 vs 198 us, N = 4 234 vs 247 us with two slices; every shorter
+// matrix is slower with two (Q4_K 10240 x 5120 N = 4 13.3 vs 10.5 us, Q6_K 5120 x 17408 34.1 vs 28.1 us).
+constexpr int KQ_TALL_ROWS = 131072;
+inline int kq_pick_ksw(int nb, int rows) { return nb < 4 || rows >= KQ_TALL_ROWS ? 2 : 4; }
 
 // Work-groups of `fn` (256 threads, `lds` dynamic bytes) resident on the whole device at once.
 inline int kq_capacity(const void *fn, size_t lds) {
@@ -927,8 +931,7 @@ int launch_wave_ks(const KqGroup &G, hipStream_t stream) {
 
 template <int T0, int T1, int NC>
 int launch_wave_nc(const KqGroup &G, int rows, hipStream_t stream) {
-    (void)rows;
-    if (kq_pick_ksw(G.nb) == 2) return launch_wave_ks<T0, T1, NC, 2>(G, stream);
+    if (kq_pick_ksw(G.nb, rows) == 2) return launch_wave_ks<T0, T1, NC, 2>(G, stream);
     return launch_wave_ks<T0, T1, NC, 4>(G, stream);
 }
 
