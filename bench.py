@@ -10,6 +10,9 @@ re-feed the MTP and draft k tokens). `value` = emitted tokens / wall time of the
 Printed as one JSON line, with
   roofline      the dominant kernel (the K-quant verify matmul: Q4_K 17408 x 5120 at N = k+1 = 4, the FFN gate/up
                 shape that carries 38% of the weight bytes) timed with HIP events on its stream, against 8 TB/s;
+  kernels       the matvec (N = 1) and the blocked verify op (N = 2, 4, 6, 8) on the single-op shapes (Q4_K
+                17408 x 5120, Q6_K 5120 x 17408) and the lm_head matvec (Q6_K 248320 x 5120), GB/s and fraction of
+                8 TB/s per launch;
   cpu_baseline  the CPU oracle (a C restatement of the reference's CPU path) on the box's host cores, on a bounded
                 sample of the same workload (a short prompt, then --spec 3 rounds for ~20 s);
 and the per-round byte model (weights read once + DeltaNet state + KV + MTP) as round_roofline.
@@ -67,6 +70,37 @@ def kernel_roofline(ctx, k):
         w.free()
     return {"kernel": f"kq_wave_kernel Q4_K {rows}x{cols} N={n}", "us_per_launch": round(us, 3),
             "bytes_per_launch": traffic_alg, "achieved_GBs": achieved}
+
+
+def kernel_sweep(ctx):
+    """The matvec (N = 1) and the blocked verify op (N = k+1 in {2, 4, 6, 8}) on the single-op shapes: Q4_K
+    17408 x 5120 and Q6_K 5120 x 17408 over 8 distinct weights each (beyond the MALL), and the Q6_K lm_head
+    248320 x 5120 at N = 1 (the draft chain's matvec). HIP-event time per launch on the context stream; GB/s from
+    the algorithmic bytes W + N*x + N*y. Flat GB/s against N means each weight super-block is read once per launch."""
+    out = []
+    for t, rows, cols, nw, ns in [(aq.Q4_K, 17408, 5120, 8, (1, 2, 4, 6, 8)), (aq.Q6_K, 5120, 17408, 8, (1, 2, 4, 6, 8)),
+                                  (aq.Q6_K, 248320, 5120, 1, (1,))]:
+        ws = [aq.SynthWeight(ctx, aq.synth_spec(t, rows, cols, seed=SEED + 200 + i)) for i in range(nw)]
+        wbytes = rows * aq.row_bytes(t, cols)
+        for n in ns:
+            x = np.random.default_rng(n).standard_normal((n, cols)).astype(np.float32)
+            act = aq.Act(ctx, cols, n)
+            act.set(x)
+            act.quantize(t, n)
+            y = aq.DeviceBuffer(ctx, n * rows * 4)
+            reps = 200 if nw > 1 else 20
+            aq.matmul_time(ctx, ws, act, n, y, reps // 8)
+            us = aq.matmul_time(ctx, ws, act, n, y, reps)
+            nbytes = wbytes + n * (cols // 256) * 292 + n * rows * 4
+            gbs = nbytes / (us * 1e-6) / 1e9
+            name = {aq.Q4_K: "Q4_K", aq.Q6_K: "Q6_K"}[t]
+            out.append({"kernel": f"{name} {rows}x{cols}", "n": n, "us_per_launch": round(us, 2),
+                        "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            y.free()
+            act.free()
+        for w in ws:
+            w.free()
+    return out
 
 
 def measured_traffic():
@@ -145,6 +179,7 @@ def main():
     ctx = aq.Context(0)
     k = a.spec
     kr = kernel_roofline(ctx, k)
+    ks = kernel_sweep(ctx) if not a.kernel_only else None
     if a.kernel_only:  # the counter runs: the dominant kernel plus a plain device copy of known size
         nbytes = 512 << 20
         src, dst = aq.DeviceBuffer(ctx, nbytes), aq.DeviceBuffer(ctx, nbytes)
@@ -223,6 +258,7 @@ def main():
                      "frac": round(kr["achieved_GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": kr["kernel"], "us_per_launch": kr["us_per_launch"],
                      "bytes_per_launch": kr["bytes_per_launch"]},
+        "kernels": ks,
         "round_roofline": {"bytes_per_round": rb, "ms_per_round": round(ms_round, 3),
                            "achieved_GBs": round(rb / (ms_round * 1e-3) / 1e9, 1),
                            "frac": round(rb / (ms_round * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
