@@ -834,7 +834,7 @@ inline int kq_pick_chunk(int nb, int nc, bool has45, bool has6, int ksw, int pf)
 }
 
 // Grid. One tile per wave, work-groups past the resident ones starting as others end, when there are at most
-// KQ_PERSIST2 / 2 tiles per resident wave, when the staging is chunked, when F32 segments are present (their
+// KQ_PERSIST_MIN tiles per resident wave, when the staging is chunked, when F32 segments are present (their
 // work-groups end early and free their slots) or when there are more than KQ_DYN tiles per resident wave (the
 // dispatcher then balances the long stream over CUs that run at unequal speed). Otherwise a persistent grid: the
 // resident work-groups shared between the segments by weight bytes, then trimmed so that every wave of a segment
@@ -843,7 +843,7 @@ inline int kq_pick_chunk(int nb, int nc, bool has45, bool has6, int ksw, int pf)
 // against 20.3 us persistent (two tiles each on half the slots); gate + up in one launch (2.1 per resident wave)
 // faster persistent.
 constexpr int KQ_DYN = 8;
-constexpr int KQ_PERSIST2 = 3;
+constexpr double KQ_PERSIST_MIN = 1.5;
 // The launch shape of kq_wave_kernel<T0, T1, NC, KSW, PF> for group G: staging chunk and LDS bytes, tiles and F32
 // work-groups, and the work-groups resident at once (less the F32 ones).
 struct KqPlan {
@@ -893,7 +893,7 @@ int launch_wave_pf(KqGroup G, const KqPlan &P, hipStream_t stream) {
     G.chk = P.chk;
     const long cap = P.cap;
     const bool persistent = G.chk >= G.nb && P.f32_wgs == 0 && cap >= G.nseg &&
-                            2 * P.tiles > KQ_PERSIST2 * 4 * cap && P.tiles <= KQ_DYN * 4 * cap;
+                            (double)P.tiles > KQ_PERSIST_MIN * 4 * cap && P.tiles <= KQ_DYN * 4 * cap;
     // the F32 segments' work-groups take the lowest indices: dispatched first, they are done early and free their
     // slots for the K-quant work-groups past the resident ones
     std::stable_partition(G.seg, G.seg + G.nseg, [](const KqSeg &sg) { return sg.type == AQ_TYPE_F32; });
