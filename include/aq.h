@@ -93,6 +93,9 @@ typedef struct aq_state aq_state;
 typedef struct aq_weight aq_weight;
 
 const char *aq_last_error(void);
+/* The hash of the sources and flags this library was built from (the build's stamp; bindings refuse a library whose
+ * stamp differs from the sources beside it). No counterpart in the reference. */
+const char *aq_build_hash(void);
 int aq_device_count(int *out);
 int aq_init(int device, aq_ctx **out);
 int aq_ctx_free(aq_ctx *ctx);
@@ -133,10 +136,16 @@ int aq_act_get_q8_0(const aq_act *a, void *ggml_out, size_t ncols);
  * (matvec.rs:336), `matmul_fn` (matvec.rs:377) and the blocked kernel `dot_q8k_t` (kdot.rs:314). `y_dev` is a
  * device buffer of ncols * rows f32. The activation must have been quantised for w's type. */
 int aq_matmul(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, float *y_dev);
-/* Debug form of the K-quant dot for column 0: per (row, super-block) the 8 exact i32 lane sums and (Q4_K/Q5_K)
- * the 4 exact i32 min products the reference keeps in `sumi` / `prod` (kdot.rs:37-140). lanes_dev: rows*nb*8,
- * mins_dev: rows*nb*4 (zero for Q6_K). */
-int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, int32_t *lanes_dev, int32_t *mins_dev);
+/* The exact integers of the K-quant dot, from the same kernel and grid aq_matmul runs (instantiated with its
+ * integer outputs on): per column c < ncols (1, 4 or 8), row and super-block the 8 i32 lane sums and (Q4_K/Q5_K) the
+ * 4 i32 min products the reference keeps in `sumi` / `prod` (kdot.rs:37-140; Q6_K lanes after the -32 fold).
+ * lanes_dev: ncols*rows*nb*8 ([c][row][sb][lane]); mins_dev: ncols*rows*nb*4 (zero for Q6_K). */
+int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, int32_t *lanes_dev,
+                int32_t *mins_dev);
+
+/* ids_dev[r] = argmax of row r of the t rows of n f32 at x_dev (device): `argmax` (model.rs:505-513), the first
+ * maximum on ties; a NaN never becomes the maximum, and a NaN at index 0 is never replaced (the answer is 0). */
+int aq_argmax(aq_ctx *ctx, const float *x_dev, size_t n, size_t t, uint32_t *ids_dev);
 
 /* ------------------------------------------------------------------------------------ synthetic tensors */
 

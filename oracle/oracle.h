@@ -37,6 +37,8 @@ size_t or_row_bytes(int type, size_t cols);
 float or_dot_q8k(int type, const uint8_t *w, const uint8_t *x_q8k, size_t n);
 void or_dot_q8k_t(int type, const uint8_t *w, const uint8_t *const *xs, size_t t, size_t n, float *out);
 void or_kq_isums(int type, const uint8_t *w, const uint8_t *x_q8k, size_t n, int32_t *lanes, int32_t *mins);
+void or_kq_isums_mat(int type, const uint8_t *w, size_t rows, const uint8_t *x_q8k, size_t n, int32_t *lanes,
+                     int32_t *mins);
 float or_dot_q8(int type, const uint8_t *w, const uint8_t *x_q8_0, size_t n);
 float or_dot_f32(const float *w, const float *x, size_t n);
 
@@ -51,7 +53,8 @@ void or_rmsnorm_gated(const float *x, const float *gate, const float *w, float e
 void or_softmax(const float *x, float *y, size_t n);
 float or_expf(float x);
 float or_log1pf(float x);
-void or_eval_math(int fn, const float *x, float *y, size_t n);
+void or_eval_math(int fn, const float *x, float *y, size_t n, int restated);
+uint64_t or_math_sweep(int fn, uint32_t first, uint64_t count, uint32_t stride, uint32_t *first_bad);
 float or_silu(float x);
 float or_sigmoid(float x);
 float or_softplus(float x);

@@ -522,6 +522,15 @@ void or_kq_isums(int type, const uint8_t *w, const uint8_t *x_q8k, size_t n, int
     or_q8k_release(&x);
 }
 
+/* or_kq_isums over `rows` weight rows (row r at w + r * row_bytes): lanes [rows][nb][8], mins [rows][nb][4]. */
+void or_kq_isums_mat(int type, const uint8_t *w, size_t rows, const uint8_t *x_q8k, size_t n, int32_t *lanes,
+                     int32_t *mins) {
+    const size_t nb = n / 256, rb = nb * kq_block_bytes(type);
+#pragma omp parallel for schedule(static)
+    for (long r = 0; r < (long)rows; r++)
+        or_kq_isums(type, w + (size_t)r * rb, x_q8k, n, lanes + (size_t)r * nb * 8, mins + (size_t)r * nb * 4);
+}
+
 /* ================================================================== Q8_0 / Q4_0 / F32 weight dots */
 
 /* dot.rs:29-45 `dot_q8_0_q8` and dot.rs:48-66 `dot_q4_0_q8`: one f32 accumulator, blocks left to right. */
@@ -604,17 +613,11 @@ void or_rmsnorm(const float *x, const float *w, float eps, float *y, size_t n) {
     for (size_t i = 0; i < n; i++) y[i] = (x[i] * inv) * w[i];
 }
 
-/* The reference's f32 exp / log1p are the platform libm's expf / log1pf. The oracle evaluates them with aq_math.h,
- * the routine the device uses too (pinned against libm by tests/test_math.py), so device and oracle agree bit for
- * bit at any depth; building with -DOR_LIBM=1 restores the platform libm calls (liboracle_libm.so) to measure how
- * far a libm's last-ulp choices move the outputs. */
-#if OR_LIBM
+/* The reference's f32 exp / log1p are the platform libm's expf / log1pf (Rust's f32::exp / f32::ln_1p lower to
+ * them); the oracle calls exactly those. The device evaluates aq_math.h's restatement of the same two GNU libc
+ * algorithms; or_math_sweep below compares that restatement with these calls over any range of f32 bit patterns. */
 #define OR_EXPF expf
 #define OR_LOG1PF log1pf
-#else
-#define OR_EXPF aq_expf
-#define OR_LOG1PF aq_log1pf
-#endif
 
 /* act.rs:7-9 `silu`, 12-14 `sigmoid`, 33-40 `softplus` */
 float or_silu(float x) { return x / (1.0f + OR_EXPF(-x)); }
@@ -622,17 +625,46 @@ float or_sigmoid(float x) { return 1.0f / (1.0f + OR_EXPF(-x)); }
 float or_softplus(float x) { return x > 20.0f ? x : OR_LOG1PF(OR_EXPF(x)); }
 float or_expf(float x) { return OR_EXPF(x); }
 float or_log1pf(float x) { return OR_LOG1PF(x); }
-/* fn: 0 exp, 1 log1p, 2 silu, 3 sigmoid, 4 softplus, elementwise */
-void or_eval_math(int fn, const float *x, float *y, size_t n) {
-    for (size_t i = 0; i < n; i++) {
-        switch (fn) {
-        case 0: y[i] = OR_EXPF(x[i]); break;
-        case 1: y[i] = OR_LOG1PF(x[i]); break;
-        case 2: y[i] = or_silu(x[i]); break;
-        case 3: y[i] = or_sigmoid(x[i]); break;
-        default: y[i] = or_softplus(x[i]); break;
+/* fn: 0 exp, 1 log1p, 2 silu, 3 sigmoid, 4 softplus, elementwise; restated != 0 evaluates aq_math.h's restatement
+ * (the device's arithmetic) instead of the platform libm (the reference's) */
+static float eval_one(int fn, float x, int restated) {
+    const float e = restated ? aq_expf(-x) : OR_EXPF(-x);
+    switch (fn) {
+    case 0: return restated ? aq_expf(x) : OR_EXPF(x);
+    case 1: return restated ? aq_log1pf(x) : OR_LOG1PF(x);
+    case 2: return x / (1.0f + e);
+    case 3: return 1.0f / (1.0f + e);
+    default: return x > 20.0f ? x : (restated ? aq_log1pf(aq_expf(x)) : OR_LOG1PF(OR_EXPF(x)));
+    }
+}
+
+void or_eval_math(int fn, const float *x, float *y, size_t n, int restated) {
+    for (size_t i = 0; i < n; i++) y[i] = eval_one(fn, x[i], restated);
+}
+
+/* Compare the restatement with the platform libm on the f32 bit patterns first, first + stride, ... (count of
+ * them, wrapping at 2^32), on all cores. Returns the number of arguments whose results differ in any bit (two NaNs
+ * count as equal) and the first such pattern in *first_bad (0xffffffff if none). */
+uint64_t or_math_sweep(int fn, uint32_t first, uint64_t count, uint32_t stride, uint32_t *first_bad) {
+    uint64_t bad = 0;
+    uint32_t fb = 0xffffffffu;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (int64_t i = 0; i < (int64_t)count; i++) {
+        const uint32_t u = first + (uint32_t)((uint64_t)i * stride);
+        float x;
+        memcpy(&x, &u, 4);
+        const float a = eval_one(fn, x, 0), b = eval_one(fn, x, 1);
+        uint32_t ua, ub;
+        memcpy(&ua, &a, 4);
+        memcpy(&ub, &b, 4);
+        if (ua != ub && !(a != a && b != b)) {
+            bad++;
+#pragma omp critical
+            if (u < fb) fb = u;
         }
     }
+    *first_bad = fb;
+    return bad;
 }
 
 /* rmsnorm.rs:37-46 `rmsnorm_gated` */

@@ -46,6 +46,15 @@ class AqSpecStats(C.Structure):
 _lib = None
 
 
+def source_hash():
+    """The stamp a library built from the sources beside this package carries (build_lib.source_hash)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("aq_build_lib", os.path.join(os.path.dirname(HERE), "build_lib.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.source_hash()
+
+
 def lib():
     global _lib
     if _lib is not None:
@@ -53,6 +62,12 @@ def lib():
     if not os.path.exists(LIB_PATH):
         raise AqError(f"{LIB_PATH} is not built: run __graft_entry__.build() (hipcc, gfx950)")
     L = C.CDLL(LIB_PATH)
+    L.aq_build_hash.restype = C.c_char_p
+    L.aq_build_hash.argtypes = []
+    built, want = L.aq_build_hash().decode(), source_hash()
+    if built != want:
+        raise AqError(f"{LIB_PATH} was built from other sources (stamp {built}, sources {want}): rebuild it with "
+                      "__graft_entry__.build()")
     P, sz, i = C.c_void_p, C.c_size_t, C.c_int
     sigs = {
         "aq_last_error": (C.c_char_p, []),
@@ -75,7 +90,8 @@ def lib():
         "aq_act_get_q8k": (i, [P, P, sz]),
         "aq_act_get_q8_0": (i, [P, P, sz]),
         "aq_matmul": (i, [P, P, P, sz, P]),
-        "aq_kq_isums": (i, [P, P, P, P, P]),
+        "aq_kq_isums": (i, [P, P, P, sz, P, P]),
+        "aq_argmax": (i, [P, P, sz, sz, P]),
         "aq_matmul_time": (i, [P, P, sz, P, sz, P, i, C.POINTER(C.c_double)]),
         "aq_synth_host": (i, [P, P, i]),
         "aq_weight_synth": (i, [P, P, C.POINTER(P)]),
@@ -242,13 +258,25 @@ def matmul(ctx: Context, w: Weight, x: Act, ncols, y: DeviceBuffer = None):
     return out
 
 
-def kq_isums(ctx: Context, w: Weight, x: Act):
+def kq_isums(ctx: Context, w: Weight, x: Act, ncols=1):
+    """The kernel's exact integers (aq_kq_isums): lanes [ncols, rows, nb, 8], mins [ncols, rows, nb, 4]."""
     nb = w.cols // 256
-    lanes = DeviceBuffer(ctx, w.rows * nb * 8 * 4)
-    mins = DeviceBuffer(ctx, w.rows * nb * 4 * 4)
-    check(lib().aq_kq_isums(ctx.h, w.h, x.h, lanes.p, mins.p))
-    return (lanes.download(np.int32, w.rows * nb * 8).reshape(w.rows, nb, 8),
-            mins.download(np.int32, w.rows * nb * 4).reshape(w.rows, nb, 4))
+    lanes = DeviceBuffer(ctx, ncols * w.rows * nb * 8 * 4)
+    mins = DeviceBuffer(ctx, ncols * w.rows * nb * 4 * 4)
+    check(lib().aq_kq_isums(ctx.h, w.h, x.h, ncols, lanes.p, mins.p))
+    return (lanes.download(np.int32, ncols * w.rows * nb * 8).reshape(ncols, w.rows, nb, 8),
+            mins.download(np.int32, ncols * w.rows * nb * 4).reshape(ncols, w.rows, nb, 4))
+
+
+def argmax(ctx: Context, x):
+    """Per-row argmax on the device (aq_argmax, model.rs:505-513): x [t, n] f32 -> t ids."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    t, n = x.shape
+    xb = DeviceBuffer(ctx, x.nbytes)
+    ib = DeviceBuffer(ctx, t * 4)
+    xb.upload(x)
+    check(lib().aq_argmax(ctx.h, xb.p, n, t, ib.p))
+    return ib.download(np.uint32, t).tolist()
 
 
 def matmul_time(ctx: Context, ws, x: Act, ncols, y: DeviceBuffer, iters):

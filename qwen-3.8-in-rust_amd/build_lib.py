@@ -3,6 +3,7 @@
 Flags: -ffp-contract=off keeps the reference's no-FMA arithmetic where the kernels reproduce its order;
 `-Xclang -target-feature -Xclang -packed-fp32-ops` keeps the compiler from emitting packed FP32 ops.
 """
+import hashlib
 import os
 import subprocess
 import sys
@@ -23,17 +24,34 @@ COMMON = ["-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract
           "-Wno-unused-variable", "-Wno-unused-but-set-variable"]
 
 
+INCLUDE = os.path.join(os.path.dirname(HERE), "include", "aq.h")
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def source_hash() -> str:
+    """sha256 of every csrc/ source and header, include/aq.h and the compiler flags: the stamp libaq.so carries
+    (aq_build_hash) and aqueduct.lib() checks, so a library built from other sources is never loaded."""
+    h = hashlib.sha256()
+    files = sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".h")))
+    for f in files:
+        h.update(f.encode() + b"\0")
+        h.update(open(os.path.join(CSRC, f), "rb").read())
+    h.update(open(INCLUDE, "rb").read())
+    h.update(" ".join(COMMON + [ARCH]).encode())
+    return h.hexdigest()[:32]
 
 
 def build(verbose: bool = False, jobs: int = 8) -> str:
     os.makedirs(OBJ_DIR, exist_ok=True)
     srcs = sources()
+    stamp = [f'-DAQ_BUILD_HASH="{source_hash()}"']
 
     def compile_one(src):
         obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-        cmd = [HIPCC] + COMMON + ["-c", src, "-o", obj]
+        cmd = [HIPCC] + COMMON + stamp + ["-c", src, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)

@@ -122,7 +122,10 @@ struct Act {
 int launch_q8k_quantize(const Act &a, size_t ncols, const float *src, size_t src_stride, hipStream_t stream);
 int launch_q8_0_quantize(const Act &a, size_t ncols, const float *src, size_t src_stride, hipStream_t stream);
 int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
-int launch_kq_isums(const Weight &w, const Act &x, int32_t *lanes, int32_t *mins, hipStream_t stream);
+// The K-quant kernel with its exact integers written out: per column c, row r, super-block sb, lanes[((c * rows + r)
+// * nb + sb) * 8 + l] (Q6_K after the -32 fold) and mins[... * 4 + i] (zero for Q6_K); y as launch_matmul.
+int kq_isums_run(const Weight &w, const Act &x, size_t ncols, float *y, int32_t *lanes, int32_t *mins,
+                 hipStream_t stream);
 // The matrix-core K-quant kernel (kq_mfma.hip); launch_matmul routes K-quant weights here.
 int launch_kq_mfma(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
 // n matrices that read the same activations (y_i = W_i x [+ resid_i]): K-quants of one K, as few launches as
@@ -130,8 +133,6 @@ int launch_kq_mfma(const Weight &w, const Act &x, size_t ncols, float *y, const 
 // last launch. resids may be null.
 int launch_kq_group(const Weight *const *ws, float *const *ys, const float *const *resids, int n, const Act &x,
                     size_t ncols, hipStream_t stream);
-// The v_dot4 K-quant kernel (matmul.hip), kept as the second implementation the tests compare against.
-int launch_kq_dot4(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
 int launch_repack(Weight &w, const uint8_t *ggml_dev, bool to_planes, hipStream_t stream);
 
 } // namespace aq

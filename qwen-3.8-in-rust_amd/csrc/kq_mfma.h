@@ -97,10 +97,13 @@ __device__ __forceinline__ void load_w(WRegs<TYPE> &w, const MfArgs &a, uint32_t
 // Q4_K/Q5_K min product of min lane j, for every column. xq: the super-block's codes, 256 bytes per column (lane-slot
 // order, XS bytes per column); xd: its f32 scales per column; xm: its activation-sum pairs [pair][ncp].
 // kdot.rs:37-140 per lane.
-template <int TYPE, int NC, int XS = 256>
+// With IS, the exact integers behind the products are also returned: is0/is1 the lane sums of lanes j and j+4
+// (Q6_K: after the -32 fold), ism the min product of min lane j (Q4_K/Q5_K), per column.
+template <int TYPE, int NC, int XS = 256, bool IS = false>
 __device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t *xq, const float *xd,
                                             const uint32_t *xm, int ncp, int j, int r, float *pr0, float *pr1,
-                                            float *pm) {
+                                            float *pm, int *is0 = nullptr, int *is1 = nullptr,
+                                            int *ism = nullptr) {
     constexpr int NCG = (NC + 3) / 4;
     constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
     uint32_t code0[8], code1[8]; // 4 unsigned codes per sub-block, lanes j and j+4
@@ -203,12 +206,24 @@ __device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t 
                 const int lo0 = (int)(int16_t)(mw0[c] & 0xFFFF), hi0 = (int)(int16_t)(mw0[c] >> 16);
                 if constexpr (Q6) {
                     const int lo1 = (int)(int16_t)(mw1[c] & 0xFFFF), hi1 = (int)(int16_t)(mw1[c] >> 16);
-                    pr0[col] = dd * (float)(s0[c] - 32 * (lo0 * os00 + hi0 * os01));
-                    pr1[col] = dd * (float)(s1[c] - 32 * (lo1 * os10 + hi1 * os11));
+                    const int i0 = s0[c] - 32 * (lo0 * os00 + hi0 * os01), i1 = s1[c] - 32 * (lo1 * os10 + hi1 * os11);
+                    pr0[col] = dd * (float)i0;
+                    pr1[col] = dd * (float)i1;
+                    if constexpr (IS) {
+                        is0[col] = i0;
+                        is1[col] = i1;
+                        ism[col] = 0;
+                    }
                 } else {
+                    const int im = mn0 * lo0 + mn1 * hi0;
                     pr0[col] = dd * (float)s0[c];
                     pr1[col] = dd * (float)s1[c];
-                    pm[col] = (-dxs[c] * dminw) * (float)(mn0 * lo0 + mn1 * hi0);
+                    pm[col] = (-dxs[c] * dminw) * (float)im;
+                    if constexpr (IS) {
+                        is0[col] = s0[c];
+                        is1[col] = s1[c];
+                        ism[col] = im;
+                    }
                 }
             }
         }
@@ -221,10 +236,11 @@ __device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t 
 // without carries, and the MFMA accumulator sums sc_i-weighted dots over the 8 sub-blocks. The lane sum is then
 // sum_i D_i << (DB*i) = sum_s sc[s] * dot_s exactly — the same integer as kdot.rs:37-95 — with no per-output
 // scale multiply.
-template <int TYPE, int NC, int XS = 256>
+template <int TYPE, int NC, int XS = 256, bool IS = false>
 __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const int8_t *xq, const float *xd,
                                                   const uint32_t *xm, int ncp, int j, int r, float *pr0,
-                                                  float *pr1, float *pm) {
+                                                  float *pr1, float *pm, int *is0 = nullptr, int *is1 = nullptr,
+                                                  int *ism = nullptr) {
     constexpr int NCG = (NC + 3) / 4;
     constexpr int DB = TYPE == AQ_TYPE_Q4_K ? 3 : 2;   // digit bits
     constexpr int ND = TYPE == AQ_TYPE_Q4_K ? 2 : 3;   // digits of a 6-bit scale
@@ -312,9 +328,15 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
                 }
                 const float dd = dxs[c] * dw;
                 const int lo0 = (int)(int16_t)(mw0[c] & 0xFFFF), hi0 = (int)(int16_t)(mw0[c] >> 16);
+                const int im = mn0 * lo0 + mn1 * hi0;
                 pr0[col] = dd * (float)s0;
                 pr1[col] = dd * (float)s1;
-                pm[col] = (-dxs[c] * dminw) * (float)(mn0 * lo0 + mn1 * hi0);
+                pm[col] = (-dxs[c] * dminw) * (float)im;
+                if constexpr (IS) {
+                    is0[col] = s0;
+                    is1[col] = s1;
+                    ism[col] = im;
+                }
             }
         }
     }
@@ -355,6 +377,7 @@ struct KqGroup {
     const float *xd;
     const int16_t *xbs, *xq8s;
     size_t xcol;
+    int32_t *isl, *ism; // integer check (IS instances only): lane sums [col][row][sb][8], min products [..][4]
 };
 
 // Activations of every super-block to LDS: codes [sb][column][KQ_XS], scales [sb][NCP], activation-sum pairs
@@ -485,7 +508,7 @@ constexpr int kq_nch_max() { return 3 * NC; }
 // through the wave's LDS slot; per tile: the lane reduction ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)) [+ (m0+m2)+(m1+m3)]
 // (kdot.rs:1-18) and the store. With chunked staging (G.chk < nb) every wave runs exactly one tile (idle ones on
 // clamped rows), because all waves of the work-group meet at the chunk barriers.
-template <int TYPE, int NC, int KSW, int PF, bool HAS45, bool HAS6>
+template <int TYPE, int NC, int KSW, int PF, bool HAS45, bool HAS6, bool IS = false>
 __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, int wg, int8_t *sxq, float *sxd,
                                             uint32_t *sxm, float *xw) {
     static_assert(KSW == 2 || KSW == 4, "K slices per wave");
@@ -607,10 +630,24 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
         const int8_t *xq = sxq + (size_t)ls * NC * KQ_XS;
         const float *xd = sxd + ls * NCP;
         const uint32_t *xm = sxm + (ls * NP + POFF) * NCP;
+        int ip[3][IS ? NC : 1];
         if constexpr (Q6)
-            sb_products<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr[0], pr[1], pr[2]);
+            sb_products<TYPE, NC, KQ_XS, IS>(wv, xq, xd, xm, NCP, j, r, pr[0], pr[1], pr[2], ip[0], ip[1], ip[2]);
         else
-            sb_products_split<TYPE, NC, KQ_XS>(wv, xq, xd, xm, NCP, j, r, pr[0], pr[1], pr[2]);
+            sb_products_split<TYPE, NC, KQ_XS, IS>(wv, xq, xd, xm, NCP, j, r, pr[0], pr[1], pr[2], ip[0], ip[1],
+                                                   ip[2]);
+        if constexpr (IS) { // the exact integers of this (row, super-block), lanes j and j+4, min lane j
+            const int orow = (gw + ck * nw) * RW + rg * 4 + r;
+            if (sb < nb && orow < a.rows) {
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const size_t o = ((size_t)c * a.rows + orow) * nb + sb;
+                    G.isl[o * 8 + j] = ip[0][c];
+                    G.isl[o * 8 + j + 4] = ip[1][c];
+                    G.ism[o * 4 + j] = ip[2][c];
+                }
+            }
+        }
         // every product is final here (the empty asm pins its computation above the refill), so no use of the
         // consumed weight registers sinks below it
 #pragma unroll
@@ -750,7 +787,7 @@ __device__ __forceinline__ void kq_f32_run(const KqGroup &G, const KqSeg &sg, in
     }
 }
 
-template <int T0, int T1, int NC, int KSW, int PF>
+template <int T0, int T1, int NC, int KSW, int PF, bool IS = false>
 __global__ void __launch_bounds__(256) kq_wave_kernel(KqGroup G) {
     constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
     constexpr bool HAS45 = T0 != AQ_TYPE_Q6_K || T1 != AQ_TYPE_Q6_K;
@@ -772,9 +809,9 @@ __global__ void __launch_bounds__(256) kq_wave_kernel(KqGroup G) {
     uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)ns * NCP);
     float *xw = xch + (threadIdx.x >> 6) * X::FLOATS;
     if (T0 == T1 || sg.type == T0)
-        kq_wave_run<T0, NC, KSW, PF, HAS45, HAS6>(G, sg, wg, sxq, sxd, sxm, xw);
+        kq_wave_run<T0, NC, KSW, PF, HAS45, HAS6, IS>(G, sg, wg, sxq, sxd, sxm, xw);
     else
-        kq_wave_run<T1, NC, KSW, PF, HAS45, HAS6>(G, sg, wg, sxq, sxd, sxm, xw);
+        kq_wave_run<T1, NC, KSW, PF, HAS45, HAS6, IS>(G, sg, wg, sxq, sxd, sxm, xw);
 }
 
 constexpr int KQ_LDS_MAX = 160 * 1024 - 512; // a CU's LDS, less a margin
@@ -852,7 +889,7 @@ struct KqPlan {
     long tiles, f32_wgs, cap;
     double bytes;
 };
-template <int T0, int T1, int NC, int KSW, int PF>
+template <int T0, int T1, int NC, int KSW, int PF, bool IS = false>
 int kq_plan(const KqGroup &G, KqPlan &P) {
     constexpr int RW = 16 / KSW; // rows per tile
     constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
@@ -861,7 +898,7 @@ int kq_plan(const KqGroup &G, KqPlan &P) {
     P.lds = kq_sb_lds_bytes(NC, HAS45, HAS6) * (size_t)(P.chk < G.nb ? P.chk : G.nb);
     constexpr size_t xch = kq_xch_bytes<NC, KSW>();
     AQ_REQUIRE(P.lds + xch <= (size_t)KQ_LDS_MAX, "kq_mfma: activation staging exceeds LDS");
-    const void *fn = reinterpret_cast<const void *>(&kq_wave_kernel<T0, T1, NC, KSW, PF>);
+    const void *fn = reinterpret_cast<const void *>(&kq_wave_kernel<T0, T1, NC, KSW, PF, IS>);
     if (P.lds > 64 * 1024) {
         static bool raised = false; // once per instantiation: allow dynamic LDS up to the CU's size
         if (!raised) {
@@ -887,7 +924,7 @@ int kq_plan(const KqGroup &G, KqPlan &P) {
     return 0;
 }
 
-template <int T0, int T1, int NC, int KSW, int PF>
+template <int T0, int T1, int NC, int KSW, int PF, bool IS = false>
 int launch_wave_pf(KqGroup G, const KqPlan &P, hipStream_t stream) {
     constexpr int RW = 16 / KSW; // rows per tile
     G.chk = P.chk;
@@ -917,7 +954,7 @@ int launch_wave_pf(KqGroup G, const KqPlan &P, hipStream_t stream) {
         wgs += (int)n;
         sg.wg_end = wgs;
     }
-    hipLaunchKernelGGL((kq_wave_kernel<T0, T1, NC, KSW, PF>), dim3((unsigned)wgs), dim3(256), P.lds, stream, G);
+    hipLaunchKernelGGL((kq_wave_kernel<T0, T1, NC, KSW, PF, IS>), dim3((unsigned)wgs), dim3(256), P.lds, stream, G);
     return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_wave launch");
 }
 
@@ -980,6 +1017,53 @@ int launch_run_t(const Weight *const *ws, float *const *ys, const float *const *
     return launch_wave_t<T0, T1>(G, rows, ncols, stream);
 }
 
+// The integer check: the production grid and kernel of one K-quant matrix of type T (the K slices the production
+// launch would pick), with the integer outputs on; y receives the usual f32 outputs.
+template <int T, int NC, int KSW>
+int launch_isums_ks(KqGroup G, hipStream_t stream) {
+    KqPlan P;
+    const int rc = kq_plan<T, T, NC, KSW, KQ_PF, true>(G, P);
+    if (rc) return rc;
+    return launch_wave_pf<T, T, NC, KSW, KQ_PF, true>(G, P, stream);
+}
+
+template <int T, int NC>
+int launch_isums_nc(const Weight &w, const Act &x, float *y, int32_t *lanes, int32_t *mins, hipStream_t stream) {
+    KqGroup G{};
+    G.nseg = 1;
+    G.nb = (int)w.nb;
+    G.xqs = x.qs;
+    G.xd = x.d;
+    G.xbs = x.bs;
+    G.xq8s = x.q8s;
+    G.xcol = x.n;
+    G.xf = x.f32;
+    G.isl = lanes;
+    G.ism = mins;
+    KqSeg &sg = G.seg[0];
+    sg.qa = w.qa;
+    sg.qb = w.qb;
+    sg.sc = w.sc;
+    sg.dm = w.dm;
+    sg.y = y;
+    sg.resid = nullptr;
+    sg.rows = (int)w.rows;
+    sg.type = w.type;
+    if (kq_pick_ksw(G.nb, sg.rows) == 2) return launch_isums_ks<T, NC, 2>(G, stream);
+    return launch_isums_ks<T, NC, 4>(G, stream);
+}
+
+template <int T>
+int launch_isums_t(const Weight &w, const Act &x, size_t ncols, float *y, int32_t *lanes, int32_t *mins,
+                   hipStream_t stream) {
+    switch (ncols) {
+    case 1: return launch_isums_nc<T, 1>(w, x, y, lanes, mins, stream);
+    case 4: return launch_isums_nc<T, 4>(w, x, y, lanes, mins, stream);
+    case 8: return launch_isums_nc<T, 8>(w, x, y, lanes, mins, stream);
+    default: return fail(AQ_EINVAL, "kq isums: ncols must be 1, 4 or 8");
+    }
+}
+
 } // namespace
 
 // One launch per type pair; each is instantiated in its own source file (kq_pair_*.hip) so they build in parallel.
@@ -993,5 +1077,8 @@ AQ_KQ_RUN_DECL(kq_run_q4q5)
 AQ_KQ_RUN_DECL(kq_run_q4q6)
 AQ_KQ_RUN_DECL(kq_run_q5q6)
 #undef AQ_KQ_RUN_DECL
+// The matmul of one K-quant matrix with its exact integers written out (kq_isums.hip).
+int kq_isums_run(const Weight &w, const Act &x, size_t ncols, float *y, int32_t *lanes, int32_t *mins,
+                 hipStream_t stream);
 
 } // namespace aq

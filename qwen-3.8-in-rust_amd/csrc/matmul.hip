@@ -1,17 +1,7 @@
 // matmul.hip — weight x activation products on gfx950: y[c*rows + r] = W[r] . x[c] for c < ncols.
 //
-// K-quant weights (Q4_K, Q5_K, Q6_K) x Q8_K activations. The arithmetic is the reference's
-// (kdot.rs:37-140, avx2.rs:565-1063): per super-block 8 exact i32 lane sums (lane l = elements 4l..4l+3 of every
-// 32-element sub-block, the 6-bit or int8 sub-block scale multiplied in as an integer), the Q4_K/Q5_K mins in 4
-// exact i32 lanes through the activation sub-block sums, the Q6_K -32 offset folded through the group sums;
-// then per lane `acc += (dx*dw) * float(sum)` super-block by super-block, no FMA, and the row reduced as
-// ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) [+ (m0+m2)+(m1+m3)]. Every column runs the same per-column code, so a
-// column of an N-column (verify) call equals the 1-column call bit for bit, and both equal the CPU reference.
-//
-// Mapping: 8 threads per weight row (thread = lane l), 8 rows per wave, 4 waves per block; each thread walks
-// the row's super-blocks in order, so its f32 lane accumulator is the reference's sequential chain for free.
-// Weight bytes come in as aligned 16-byte loads from the plane layout (aq_common.h); the integer products run
-// on v_dot4_i32_i8; the activation tile is re-read from L2 by every row of the wave (it is tiny and hot).
+// K-quant weights (Q4_K, Q5_K, Q6_K) go to the matrix-core kernel (kq_mfma.h); this file holds the Q8_0 / Q4_0
+// and F32 products, the weight repacking into planes, and the dispatch by weight type.
 #include "aq_common.h"
 
 #include <map>
@@ -21,19 +11,6 @@
 namespace aq {
 namespace {
 
-struct KqArgs {
-    const uint8_t *qa, *qb, *sc, *dm;
-    int rows, nb;
-    const int8_t *xqs;   // ncols x n, lane-permuted
-    const float *xd;     // ncols x nb
-    const int16_t *xbs;  // ncols x nb x 16
-    const int16_t *xq8s; // ncols x nb x 8
-    size_t xcol;         // n (bytes of codes per column)
-    float *y;
-    const float *resid;
-    int32_t *isum_lanes, *isum_mins; // isums debug (column 0)
-};
-
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
@@ -42,134 +19,6 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     _Float16 f;
     __builtin_memcpy(&f, &h, 2);
     return (float)f;
-}
-
-template <int TYPE, int NC, bool ISUMS>
-__global__ void __launch_bounds__(256) kq_matmul_kernel(KqArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int l = lane & 7;
-    int row = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * 8 + (lane >> 3);
-    const bool valid = row < a.rows;
-    if (!valid) row = a.rows - 1; // keep every lane in the shuffles below; the store is skipped
-    const int nb = a.nb;
-    float acc[NC], accm[NC];
-#pragma unroll
-    for (int c = 0; c < NC; c++) acc[c] = accm[c] = 0.0f;
-
-    for (int sb = 0; sb < nb; sb++) {
-        const size_t wsb = (size_t)row * nb + sb; // row-major block index (the debug lane-sum output)
-        // ---------------------------------------------------------------- weights of this super-block
-        const uint4 qa = *reinterpret_cast<const uint4 *>(a.qa + kq_qa_off(row, sb, nb, l));
-        uint32_t code[8]; // 4 unsigned codes per sub-block s, lane l's positions
-        int scl[8];       // the integer scale of each of lane l's 8 sub-blocks
-        int mn0 = 0, mn1 = 0;
-        int off_sc0 = 0, off_sc1 = 0; // Q6_K: scales of groups 2l, 2l+1 (the -32 fold)
-        float dw, dminw = 0.0f;
-        if constexpr (TYPE == AQ_TYPE_Q4_K || TYPE == AQ_TYPE_Q5_K) {
-            const uint32_t *s12 = reinterpret_cast<const uint32_t *>(a.sc + kq_sc_off(row, sb, nb) + 4);
-            const uint32_t q0 = s12[0], q1 = s12[1], q2 = s12[2];
-            const uint32_t sc_lo = q0 & 0x3F3F3F3Fu;                                  // sc[0..3]
-            const uint32_t mn_lo = q1 & 0x3F3F3F3Fu;                                  // mn[0..3]
-            const uint32_t sc_hi = (q2 & 0x0F0F0F0Fu) | ((q0 >> 2) & 0x30303030u);    // sc[4..7]
-            const uint32_t mn_hi = ((q2 >> 4) & 0x0F0F0F0Fu) | ((q1 >> 2) & 0x30303030u); // mn[4..7]
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                scl[s] = (sc_lo >> (8 * s)) & 0xFF;
-                scl[s + 4] = (sc_hi >> (8 * s)) & 0xFF;
-            }
-            // lane l < 4 folds the mins of sub-blocks 2l, 2l+1
-            const uint32_t mnw = l < 2 ? mn_lo : mn_hi;
-            mn0 = (mnw >> (16 * (l & 1))) & 0xFF;
-            mn1 = (mnw >> (16 * (l & 1) + 8)) & 0xFF;
-            const uint32_t w4[4] = {qa.x, qa.y, qa.z, qa.w};
-            uint32_t qh = 0;
-            if constexpr (TYPE == AQ_TYPE_Q5_K) qh = *reinterpret_cast<const uint32_t *>(a.qb + kq_qb5_off(row, sb, nb, l));
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                code[2 * j] = w4[j] & 0x0F0F0F0Fu;
-                code[2 * j + 1] = (w4[j] >> 4) & 0x0F0F0F0Fu;
-                if constexpr (TYPE == AQ_TYPE_Q5_K) {
-                    code[2 * j] |= ((qh >> (2 * j)) & 0x01010101u) << 4;
-                    code[2 * j + 1] |= ((qh >> (2 * j + 1)) & 0x01010101u) << 4;
-                }
-            }
-            const uint32_t dmw = *reinterpret_cast<const uint32_t *>(a.sc + kq_sc_off(row, sb, nb));
-            dw = half_bits_to_float((uint16_t)(dmw & 0xFFFF));
-            dminw = half_bits_to_float((uint16_t)(dmw >> 16));
-        } else { // Q6_K
-            const uint2 qh2 = *reinterpret_cast<const uint2 *>(a.qb + kq_qb6_off(row, sb, nb, l));
-            const uint4 s16 = *reinterpret_cast<const uint4 *>(a.sc + kq_sc_off(row, sb, nb));
-            const uint32_t sw[4] = {s16.x, s16.y, s16.z, s16.w};
-            const uint32_t ql[4] = {qa.x, qa.y, qa.z, qa.w}; // (h, jj) = 0:(0,0) 1:(0,1) 2:(1,0) 3:(1,1)
-            const uint32_t qhw[2] = {qh2.x, qh2.y};
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const uint32_t lo = k < 2 ? (ql[h * 2 + k] & 0x0F0F0F0Fu) : ((ql[h * 2 + k - 2] >> 4) & 0x0F0F0F0Fu);
-                    const uint32_t hi = ((qhw[h] >> (2 * k)) & 0x03030303u) << 4;
-                    code[h * 4 + k] = lo | hi;
-                    const int g = h * 8 + 2 * k + (l >> 2); // group of lane l's positions in sub-block (h, k)
-                    scl[h * 4 + k] = (int)(int8_t)((sw[g >> 2] >> (8 * (g & 3))) & 0xFF);
-                }
-            }
-            const int g0 = 2 * l, g1 = 2 * l + 1;
-            off_sc0 = (int)(int8_t)((sw[g0 >> 2] >> (8 * (g0 & 3))) & 0xFF);
-            off_sc1 = (int)(int8_t)((sw[g1 >> 2] >> (8 * (g1 & 3))) & 0xFF);
-            dw = half_bits_to_float(*reinterpret_cast<const uint16_t *>(a.dm + kq_dm_off(row, sb, nb)));
-        }
-        // ---------------------------------------------------------------- every activation column
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-            const size_t xb = (size_t)c * a.xcol + (size_t)sb * 256 + lane_slot(l) * 32;
-            const uint4 x0 = *reinterpret_cast<const uint4 *>(a.xqs + xb);
-            const uint4 x1 = *reinterpret_cast<const uint4 *>(a.xqs + xb + 16);
-            const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            int sumi = 0;
-#pragma unroll
-            for (int s = 0; s < 8; s++) sumi += scl[s] * dot4(code[s], xs[s], 0);
-            const size_t xm = (size_t)c * nb + sb;
-            const float dx = a.xd[xm];
-            int prod = 0;
-            if constexpr (TYPE == AQ_TYPE_Q6_K) {
-                const uint32_t bsw = *reinterpret_cast<const uint32_t *>(a.xbs + xm * 16 + 2 * l);
-                const int bs0 = (int)(int16_t)(bsw & 0xFFFF), bs1 = (int)(int16_t)(bsw >> 16);
-                sumi -= 32 * (bs0 * off_sc0 + bs1 * off_sc1);
-                acc[c] += (dx * dw) * (float)sumi;
-            } else {
-                acc[c] += (dx * dw) * (float)sumi;
-                if (l < 4) {
-                    const uint32_t qsw = *reinterpret_cast<const uint32_t *>(a.xq8s + xm * 8 + 2 * l);
-                    prod = mn0 * (int)(int16_t)(qsw & 0xFFFF) + mn1 * (int)(int16_t)(qsw >> 16);
-                    accm[c] += (-dx * dminw) * (float)prod;
-                }
-            }
-            if constexpr (ISUMS) {
-                if (c == 0 && valid) {
-                    a.isum_lanes[wsb * 8 + l] = sumi;
-                    if (l < 4) a.isum_mins[wsb * 4 + l] = TYPE == AQ_TYPE_Q6_K ? 0 : prod;
-                }
-            }
-        }
-    }
-    // ---------------------------------------------------------------- row reduction in the reference's order
-#pragma unroll
-    for (int c = 0; c < NC; c++) {
-        float v = acc[c];
-        v = v + __shfl_xor(v, 4); // l0+l4, l1+l5, l2+l6, l3+l7
-        v = v + __shfl_xor(v, 2); // (l0+l4)+(l2+l6), (l1+l5)+(l3+l7)
-        v = v + __shfl_xor(v, 1);
-        if constexpr (TYPE != AQ_TYPE_Q6_K) {
-            float m = accm[c];
-            m = m + __shfl_xor(m, 2); // m0+m2, m1+m3
-            m = m + __shfl_xor(m, 1);
-            v = v + m;
-        }
-        if (l == 0 && valid && !ISUMS) {
-            const size_t o = (size_t)c * a.rows + row;
-            a.y[o] = a.resid ? a.resid[o] + v : v;
-        }
-    }
 }
 
 // --------------------------------------------------------------------------------- Q8_0 / Q4_0 / F32 rows
@@ -491,46 +340,6 @@ __global__ void repack_kernel(int type, size_t nblocks, size_t nb, uint8_t *ggml
     }
 }
 
-template <int TYPE, bool ISUMS>
-int launch_kq_typed(const KqArgs &args, size_t ncols, hipStream_t stream) {
-    const dim3 grid((unsigned)((args.rows + 31) / 32)), block(256);
-    switch (ncols) {
-#define CASE(N)                                                                                               \
-    case N: hipLaunchKernelGGL((kq_matmul_kernel<TYPE, N, ISUMS>), grid, block, 0, stream, args); break;
-        CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
-#undef CASE
-    default: return fail(AQ_EINVAL, "matmul: ncols must be 1..8 for K-quant weights in this build");
-    }
-    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_matmul launch");
-}
-
-template <bool ISUMS>
-int launch_kq(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, int32_t *lanes,
-              int32_t *mins, hipStream_t stream) {
-    KqArgs args{};
-    args.qa = w.qa;
-    args.qb = w.qb;
-    args.sc = w.sc;
-    args.dm = w.dm;
-    args.rows = (int)w.rows;
-    args.nb = (int)w.nb;
-    args.xqs = x.qs;
-    args.xd = x.d;
-    args.xbs = x.bs;
-    args.xq8s = x.q8s;
-    args.xcol = x.n;
-    args.y = y;
-    args.resid = resid;
-    args.isum_lanes = lanes;
-    args.isum_mins = mins;
-    switch (w.type) {
-    case AQ_TYPE_Q4_K: return launch_kq_typed<AQ_TYPE_Q4_K, ISUMS>(args, ncols, stream);
-    case AQ_TYPE_Q5_K: return launch_kq_typed<AQ_TYPE_Q5_K, ISUMS>(args, ncols, stream);
-    case AQ_TYPE_Q6_K: return launch_kq_typed<AQ_TYPE_Q6_K, ISUMS>(args, ncols, stream);
-    default: return fail(AQ_EUNSUP, "kq: not a K-quant type");
-    }
-}
-
 // dot.rs:180-200 for F32 weights (ssm_alpha / ssm_beta: few rows, long columns): one work-group per row;
 // thread b computes block b's 32-element partial left to right for every column, then one thread per column
 // adds the partials in block order (acc += part), and `acc + 0.0f` when the row has no short tail.
@@ -712,14 +521,6 @@ int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const f
     case 8: return launch_q8_nc<8>(args, stream);
     default: return fail(AQ_EINVAL, "matmul: ncols must be 1..8 for Q8_0/Q4_0/F32 weights in this build");
     }
-}
-
-int launch_kq_dot4(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream) {
-    return launch_kq<false>(w, x, ncols, y, resid, nullptr, nullptr, stream);
-}
-
-int launch_kq_isums(const Weight &w, const Act &x, int32_t *lanes, int32_t *mins, hipStream_t stream) {
-    return launch_kq<true>(w, x, 1, nullptr, nullptr, lanes, mins, stream);
 }
 
 int launch_repack(Weight &w, const uint8_t *ggml_dev, bool to_planes, hipStream_t stream) {

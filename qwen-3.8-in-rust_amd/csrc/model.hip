@@ -411,6 +411,8 @@ struct aq_state {
     uint32_t *ids = nullptr, *amax = nullptr, *drafts = nullptr, *emitted = nullptr, *info = nullptr, *prompt = nullptr,
              *shifted = nullptr;
     void *amax_scratch = nullptr;
+    float *attn_sc = nullptr; // attention score rows [T][n_head][attn_sc_stride], when contexts outgrow the LDS
+    size_t attn_sc_stride = 0;
     uint32_t *pinned = nullptr; // host, 64 words
     aq::DnArgs *commit_args = nullptr; // device: the commit's DnArgs per DeltaNet slot, for par = 0 then par = 1
     int n_dn = 0;
@@ -596,6 +598,8 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
         a.nkv = (int)c.n_head_kv;
         a.hd = (int)c.head_dim;
         a.rd = (int)c.rope_dim;
+        a.gsc = s->attn_sc;
+        a.gsc_stride = s->attn_sc_stride;
         if ((rc = launch_attention(a, s->stream))) return rc;
         kv->len += t;
         if (!q8k) {
@@ -925,6 +929,12 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
             AQ_S(dalloc_t(s, T * nv, &s->sv_a[i]));
             AQ_S(dalloc_t(s, T * nv, &s->sv_b[i]));
         }
+    }
+    // score rows in device memory when a context can outgrow the attention kernel's LDS (the MTP's cache is the
+    // longest: cap + T rows)
+    if (cap + 2 * T > attn_lds_positions((int)c.head_dim)) {
+        s->attn_sc_stride = cap + 2 * T;
+        AQ_S(dalloc_t(s, T * c.n_head * s->attn_sc_stride, &s->attn_sc));
     }
     if (m->has_mtp) {
         s->mtp_kv.cap = cap + T;

@@ -80,7 +80,13 @@ struct AttnArgs {
     int out_q8k = 0; // also the Q8_K form of `out` into q8k (head_dim 256: one head row = one 256-block)
     Act q8k;
     int t = 0, nh = 0, nkv = 0, hd = 0, rd = 0;
+    // Score rows in device memory for contexts whose scores do not fit the work-group's LDS: row (i, h) at
+    // gsc + (i * nh + h) * gsc_stride, gsc_stride >= base + t. Null: only contexts that fit the LDS are accepted.
+    float *gsc = nullptr;
+    size_t gsc_stride = 0;
 };
+// The longest context (base + t) whose score row the attention kernel keeps in LDS for head_dim hd.
+size_t attn_lds_positions(int hd);
 // Norm + RoPE of q and k, K/V appended at cache rows base..base+t, then per (head, row) softmax attention over
 // base + row + 1 positions with the sigmoid output gate (gqa_attention.rs:327-418).
 int launch_attention(const AttnArgs &a, hipStream_t stream);

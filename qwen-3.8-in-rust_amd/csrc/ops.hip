@@ -682,12 +682,17 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnArgs a) {
 
 // Scores (sequential dot over head_dim, times scaling), softmax (softmax.rs:22-49: max, exp, 8-lane sum, divide),
 // weighted V sum (sequential over positions), times sigmoid(gate).
+// GSC: the score row lives in device memory (a.gsc) instead of LDS, for contexts past attn_lds_positions; the
+// arithmetic and its order are the same.
+template <bool GSC>
 __global__ void __launch_bounds__(256) attn_core_kernel(AttnArgs a) {
-    extern __shared__ float sm[]; // hd + (base + t) + 32
+    extern __shared__ float sm[]; // hd + (base + t, unless GSC) + 32
     const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x, hd = a.hd;
     const int kvh = h / (a.nh / a.nkv);
     const size_t len = a.base + i + 1;
-    float *qs = sm, *sc = sm + hd, *red = sc + a.base + a.t;
+    float *qs = sm;
+    float *sc = GSC ? a.gsc + ((size_t)i * a.nh + h) * a.gsc_stride : sm + hd;
+    float *red = GSC ? sm + hd : sc + a.base + a.t;
     for (int d = tid; d < hd; d += 256) qs[d] = a.q[(size_t)i * a.nh * hd + (size_t)h * hd + d];
     __syncthreads();
     float mx = -INFINITY;
@@ -842,8 +847,11 @@ __global__ void __launch_bounds__(256) argmax_partial_kernel(const float *x, siz
     }
 }
 
-__global__ void __launch_bounds__(64) argmax_final_kernel(const float *pv, const uint32_t *pi, int nchunk,
-                                                          uint32_t *ids) {
+// model.rs:505-513: best = 0, replaced by i only when v[i] > v[best]. So a NaN never replaces the best, a NaN at
+// index 0 is never replaced (the answer is 0), and among equal maxima the first wins. The partial kernels skip NaN
+// (a comparison with NaN is false); here the row's first value decides the NaN case.
+__global__ void __launch_bounds__(64) argmax_final_kernel(const float *x, size_t stride, const float *pv,
+                                                          const uint32_t *pi, int nchunk, uint32_t *ids) {
     __shared__ float sv[1];
     __shared__ uint32_t si[1];
     const int r = blockIdx.x;
@@ -851,7 +859,10 @@ __global__ void __launch_bounds__(64) argmax_final_kernel(const float *pv, const
     uint32_t bi = 0xFFFFFFFFu;
     for (int c = threadIdx.x; c < nchunk; c += 64) amax_merge(bv, bi, pv[(size_t)r * nchunk + c], pi[(size_t)r * nchunk + c]);
     amax_block(bv, bi, sv, si);
-    if (threadIdx.x == 0) ids[r] = bi == 0xFFFFFFFFu ? 0u : bi;
+    if (threadIdx.x == 0) {
+        const float v0 = x[(size_t)r * stride];
+        ids[r] = (v0 != v0 || bi == 0xFFFFFFFFu) ? 0u : bi;
+    }
 }
 
 // -------------------------------------------------------------------------------------------- acceptance
@@ -1040,13 +1051,20 @@ int launch_attention(const AttnArgs &a, hipStream_t stream) {
     hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)(a.nh + a.nkv), (unsigned)a.t), dim3(a.hd), 0, stream, a);
     int rc = launched("attention prologue");
     if (rc) return rc;
-    const size_t shmem = (a.hd + a.base + a.t + 32) * sizeof(float);
-    AQ_REQUIRE(shmem <= 160 * 1024, "attention: context too long for one work-group's LDS");
     AQ_REQUIRE(!a.out_q8k || (a.hd == 256 && a.q8k.qs && a.q8k.n == (size_t)a.nh * 256 && a.q8k.ncols >= (size_t)a.t),
                "attention: Q8_K output needs head_dim 256 and a buffer of t rows of nh * 256");
-    hipLaunchKernelGGL(attn_core_kernel, dim3((unsigned)a.nh, (unsigned)a.t), dim3(256), shmem, stream, a);
+    if (a.base + a.t <= attn_lds_positions(a.hd)) {
+        const size_t shmem = (a.hd + a.base + a.t + 32) * sizeof(float);
+        hipLaunchKernelGGL(attn_core_kernel<false>, dim3((unsigned)a.nh, (unsigned)a.t), dim3(256), shmem, stream, a);
+    } else {
+        AQ_REQUIRE(a.gsc && a.base + a.t <= a.gsc_stride, "attention: context longer than the state's score rows");
+        const size_t shmem = (a.hd + 32) * sizeof(float);
+        hipLaunchKernelGGL(attn_core_kernel<true>, dim3((unsigned)a.nh, (unsigned)a.t), dim3(256), shmem, stream, a);
+    }
     return launched("attention");
 }
+
+size_t attn_lds_positions(int hd) { return 65536 / sizeof(float) - (size_t)hd - 32; }
 
 size_t argmax_scratch_bytes(size_t n, size_t t) {
     const size_t nchunk = (n + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
@@ -1062,7 +1080,7 @@ int launch_argmax(const float *x, size_t n, size_t stride, size_t t, uint32_t *i
                        pv, pi, nchunk);
     int rc = launched("argmax");
     if (rc) return rc;
-    hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)t), dim3(64), 0, stream, pv, pi, nchunk, ids);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)t), dim3(64), 0, stream, x, stride, pv, pi, nchunk, ids);
     return launched("argmax final");
 }
 

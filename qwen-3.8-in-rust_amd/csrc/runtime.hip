@@ -4,6 +4,7 @@
 #include <vector>
 
 #include "aq_common.h"
+#include "ops.h"
 
 namespace aq {
 
@@ -128,6 +129,11 @@ using namespace aq;
 extern "C" {
 
 const char *aq_last_error(void) { return g_last_error.c_str(); }
+
+#ifndef AQ_BUILD_HASH
+#define AQ_BUILD_HASH "unstamped"
+#endif
+const char *aq_build_hash(void) { return AQ_BUILD_HASH; }
 
 int aq_device_count(int *out) {
     AQ_REQUIRE(out, "aq_device_count: null out");
@@ -364,15 +370,31 @@ int aq_matmul(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, fl
     return 0;
 }
 
-int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, int32_t *lanes_dev, int32_t *mins_dev) {
+int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, int32_t *lanes_dev,
+                int32_t *mins_dev) {
     AQ_REQUIRE(ctx && w && x && lanes_dev && mins_dev, "aq_kq_isums: null argument");
     AQ_REQUIRE(is_kquant(w->w.type), "aq_kq_isums: K-quant weights only");
     AQ_REQUIRE(x->a.n == w->w.cols, "aq_kq_isums: activation length");
+    AQ_REQUIRE(ncols >= 1 && ncols <= x->a.ncols, "aq_kq_isums: ncols");
     AQ_HIP(hipSetDevice(ctx->device));
-    int rc = launch_kq_isums(w->w, x->a, lanes_dev, mins_dev, ctx->stream);
-    if (rc) return rc;
-    AQ_HIP(hipStreamSynchronize(ctx->stream));
-    return 0;
+    void *y = nullptr;
+    if (hipMalloc(&y, ncols * w->w.rows * 4) != hipSuccess) return fail(AQ_ENOMEM, "aq_kq_isums: outputs");
+    int rc = kq_isums_run(w->w, x->a, ncols, (float *)y, lanes_dev, mins_dev, ctx->stream);
+    if (!rc && hipStreamSynchronize(ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_kq_isums: sync");
+    (void)hipFree(y);
+    return rc;
+}
+
+int aq_argmax(aq_ctx *ctx, const float *x_dev, size_t n, size_t t, uint32_t *ids_dev) {
+    AQ_REQUIRE(ctx && x_dev && ids_dev, "aq_argmax: null argument");
+    AQ_REQUIRE(n >= 1 && t >= 1 && n <= 0xFFFFFFFEull, "aq_argmax: empty or over-long rows");
+    AQ_HIP(hipSetDevice(ctx->device));
+    void *scratch = nullptr;
+    if (hipMalloc(&scratch, argmax_scratch_bytes(n, t)) != hipSuccess) return fail(AQ_ENOMEM, "aq_argmax: scratch");
+    int rc = launch_argmax(x_dev, n, n, t, ids_dev, scratch, ctx->stream);
+    if (!rc && hipStreamSynchronize(ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_argmax: sync");
+    (void)hipFree(scratch);
+    return rc;
 }
 
 int aq_matmul_time(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_act *x, size_t ncols, float *y_dev,

@@ -43,33 +43,29 @@ def tensor_table(tensors):
 
 
 _lib = None
-_lib_libm = None
 
 
-def lib_libm():
-    """The oracle built with the platform libm's expf / log1pf (or_eval_math and the model entry points)."""
-    global _lib_libm
-    if _lib_libm is None:
-        lib()
-        L = C.CDLL(os.path.join(ROOT, "oracle", "liboracle_libm.so"))
-        L.or_eval_math.restype = None
-        L.or_eval_math.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_size_t]
-        _lib_libm = L
-    return _lib_libm
-
-
-def eval_math(fn, x, libm=False):
+def eval_math(fn, x, restated=False):
+    """fn 0 exp, 1 log1p, 2 silu, 3 sigmoid, 4 softplus: the platform libm's (the reference's arithmetic), or
+    with restated=True aq_math.h's restatement (the device's arithmetic) compiled for the host."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.zeros_like(x)
-    (lib_libm() if libm else lib()).or_eval_math(fn, x.ctypes.data, y.ctypes.data, x.size)
+    lib().or_eval_math(fn, x.ctypes.data, y.ctypes.data, x.size, int(restated))
     return y
+
+
+def math_sweep(fn, first=0, count=1 << 32, stride=1):
+    """Restatement vs platform libm over f32 bit patterns first, first+stride, ...: (mismatches, first bad)."""
+    fb = C.c_uint32()
+    bad = lib().or_math_sweep(fn, first, count, stride, C.byref(fb))
+    return int(bad), fb.value
 
 
 def lib():
     global _lib
     if _lib is not None:
         return _lib
-    if not (os.path.exists(LIB_PATH) and os.path.exists(os.path.join(ROOT, "oracle", "liboracle_libm.so"))):
+    if not os.path.exists(LIB_PATH):
         import importlib.util
         spec = importlib.util.spec_from_file_location("build_oracle", os.path.join(ROOT, "oracle", "build_oracle.py"))
         mod = importlib.util.module_from_spec(spec)
@@ -88,6 +84,7 @@ def lib():
         "or_dot_q8k": (C.c_float, [C.c_int, P, P, sz]),
         "or_dot_q8k_t": (None, [C.c_int, P, P, sz, sz, P]),
         "or_kq_isums": (None, [C.c_int, P, P, sz, P, P]),
+        "or_kq_isums_mat": (None, [C.c_int, P, sz, P, sz, P, P]),
         "or_dot_q8": (C.c_float, [C.c_int, P, P, sz]),
         "or_dot_f32": (C.c_float, [P, P, sz]),
         "or_matmul": (None, [C.c_int, P, sz, sz, P, sz, P, C.c_int]),
@@ -95,7 +92,8 @@ def lib():
         "or_rmsnorm_gated": (None, [P, P, P, C.c_float, P, sz]),
         "or_softmax": (None, [P, P, sz]),
         "or_silu": (C.c_float, [C.c_float]),
-        "or_eval_math": (None, [C.c_int, P, P, sz]),
+        "or_eval_math": (None, [C.c_int, P, P, sz, C.c_int]),
+        "or_math_sweep": (C.c_uint64, [C.c_int, C.c_uint32, C.c_uint64, C.c_uint32, C.POINTER(C.c_uint32)]),
         "or_sigmoid": (C.c_float, [C.c_float]),
         "or_softplus": (C.c_float, [C.c_float]),
         "or_swiglu": (None, [P, P, P, sz]),
@@ -165,6 +163,16 @@ def kq_isums(t, wrow, xq, n):
     lanes = np.zeros(nb * 8, np.int32)
     mins = np.zeros(nb * 4, np.int32)
     lib().or_kq_isums(t, ptr(np.ascontiguousarray(wrow)), ptr(np.ascontiguousarray(xq)), n, ptr(lanes), ptr(mins))
+    return lanes, mins
+
+
+def kq_isums_mat(t, w, rows, xq, n):
+    """or_kq_isums of every row: lanes [rows, nb, 8], mins [rows, nb, 4]."""
+    nb = n // 256
+    lanes = np.zeros((rows, nb, 8), np.int32)
+    mins = np.zeros((rows, nb, 4), np.int32)
+    lib().or_kq_isums_mat(t, ptr(np.ascontiguousarray(w)), rows, ptr(np.ascontiguousarray(xq)), n, ptr(lanes),
+                          ptr(mins))
     return lanes, mins
 
 

@@ -130,8 +130,8 @@ def test_kquant_isums_bit_exact_on_fixture_rows(ctx):
             a.quantize(t, 1)
             lanes, mins = aq.kq_isums(ctx, w, a)
             want_l, want_m = O.kq_isums(t, w_raw[r], O.q8k_quantize(x_deq[r]), width)
-            assert np.array_equal(lanes[r].ravel(), want_l), f"{c['case']} row {r} lanes"
-            assert np.array_equal(mins[r].ravel(), want_m), f"{c['case']} row {r} mins"
+            assert np.array_equal(lanes[0, r].ravel(), want_l), f"{c['case']} row {r} lanes"
+            assert np.array_equal(mins[0, r].ravel(), want_m), f"{c['case']} row {r} mins"
             y = aq.matmul(ctx, w, a, 1)
             want = O.dot_q8k(t, w_raw[r], O.q8k_quantize(x_deq[r]), width)
             assert bits_equal(y[0, r], want), f"{c['case']} row {r}: {y[0, r]} vs {want}"
@@ -166,6 +166,28 @@ def test_q8_weight_dots_bit_exact_on_fixture_rows(ctx):
             y = aq.matmul(ctx, w, a, 1)
             want = O.dot_q8(t, w_raw[r], O.q8_0_quantize(x_deq[r]), width)
             assert bits_equal(y[0, r], want), f"{c['case']} row {r}: {y[0, r]} vs {want}"
+
+
+@pytest.mark.parametrize("t,rows,cols", [(aq.Q4_K, 17408, 5120), (aq.Q6_K, 5120, 17408), (aq.Q5_K, 1024, 5120)])
+def test_kquant_isums_full_shapes_on_the_matmul_kernel(ctx, t, rows, cols):
+    """Config 2's integer contract on the kernel the product runs: the exact i32 lane sums and min products of every
+    (row, super-block) from kq_wave_kernel (its integer-output instance, same grid), N = 1 and each column of N = 4,
+    equal the reference's sumi / prod (kdot.rs:37-140) from the oracle."""
+    say(f"isums full shape type {t} {rows}x{cols}")
+    spec = aq.synth_spec(t, rows, cols, seed=4048 + t, b=0.02)
+    host = aq.synth_host(spec).view(np.uint8)
+    w = aq.SynthWeight(ctx, spec)
+    x = np.random.default_rng(31 + t).standard_normal((4, cols)).astype(np.float32)
+    a = aq.Act(ctx, cols, 4)
+    a.set(x)
+    a.quantize(t, 4)
+    for n in (1, 4):
+        lanes, mins = aq.kq_isums(ctx, w, a, n)
+        for c in range(n):
+            want_l, want_m = O.kq_isums_mat(t, host, rows, O.q8k_quantize(x[c]), cols)
+            bad = int(np.sum(lanes[c] != want_l))
+            assert bad == 0, f"N={n} column {c}: {bad} lane sums differ"
+            assert np.array_equal(mins[c], want_m), f"N={n} column {c}: min products differ"
 
 
 @pytest.mark.parametrize("t,rows,cols", [(aq.Q4_K, 17408, 5120), (aq.Q6_K, 5120, 17408), (aq.Q5_K, 1024, 5120),
