@@ -146,6 +146,12 @@ int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, 
 /* ids_dev[r] = argmax of row r of the t rows of n f32 at x_dev (device): `argmax` (model.rs:505-513), the first
  * maximum on ties; a NaN never becomes the maximum, and a NaN at index 0 is never replaced (the answer is 0). */
 int aq_argmax(aq_ctx *ctx, const float *x_dev, size_t n, size_t t, uint32_t *ids_dev);
+/* aq_argmax without any device allocation: no counterpart in the reference; for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops). Its partial results live in a fixed device array of 128 KiB
+ * per GPU, held until the process ends, so t <= 16 rows of n <= 2^20 values (larger calls return AQ_EINVAL). Every
+ * call on one GPU shares that array: calls that overlap on one GPU (several contexts or threads) race. Nothing in
+ * it carries from one call to the next. Same results as aq_argmax. */
+int aq_argmax_noalloc(aq_ctx *ctx, const float *x_dev, size_t n, size_t t, uint32_t *ids_dev);
 
 /* ------------------------------------------------------------------------------------ synthetic tensors */
 

@@ -92,6 +92,7 @@ def lib():
         "aq_matmul": (i, [P, P, P, sz, P]),
         "aq_kq_isums": (i, [P, P, P, sz, P, P]),
         "aq_argmax": (i, [P, P, sz, sz, P]),
+        "aq_argmax_noalloc": (i, [P, P, sz, sz, P]),
         "aq_matmul_time": (i, [P, P, sz, P, sz, P, i, C.POINTER(C.c_double)]),
         "aq_synth_host": (i, [P, P, i]),
         "aq_weight_synth": (i, [P, P, C.POINTER(P)]),

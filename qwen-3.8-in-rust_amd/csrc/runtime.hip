@@ -1,6 +1,7 @@
 // runtime.hip — lifecycle, device memory, weights, activation buffers and the operator-level C-ABI
 // (include/aq.h). Every entry point validates its arguments and returns an AQ_E* code instead of aborting.
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "aq_common.h"
@@ -18,6 +19,33 @@ int fail(int code, const std::string &msg) {
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// The allocation-free argmax's partial results: a file-scope device array, one copy per GPU, held until the
+// process ends. Rows of at most AQ_NOALLOC_MAX_N values, at most AQ_NOALLOC_MAX_ROWS rows per call.
+constexpr size_t AQ_NOALLOC_MAX_N = (size_t)1 << 20, AQ_NOALLOC_MAX_ROWS = 16;
+constexpr size_t AQ_NOALLOC_SCRATCH = 128 * 1024;
+static __device__ __align__(256) uint8_t scratch[AQ_NOALLOC_SCRATCH];
+// Its address on each device (hipGetSymbolAddress with that device current, at aq_init); host code uses these,
+// never the array's name, which in host code is only a stand-in.
+static std::mutex g_scratch_mu;
+static std::vector<void *> g_scratch_ptr;
+
+static int scratch_setup(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if ((size_t)device < g_scratch_ptr.size() && g_scratch_ptr[device]) return 0;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        return fail(AQ_EHIP, std::string("aq_init: hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    if (g_scratch_ptr.size() <= (size_t)device) g_scratch_ptr.resize(device + 1, nullptr);
+    g_scratch_ptr[device] = ptr;
+    return 0;
+}
+
+static void *scratch_ptr(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return (size_t)device < g_scratch_ptr.size() ? g_scratch_ptr[device] : nullptr;
+}
 
 // Allocate the planes of a weight (layouts in aq_common.h).
 static int alloc_weight(Weight &w, int type, size_t rows, size_t cols, int device) {
@@ -153,6 +181,8 @@ int aq_init(int device, aq_ctx **out) {
     AQ_HIP(hipGetDeviceProperties(&prop, device));
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(AQ_EUNSUP, std::string("aq_init: this build targets gfx950, device is ") + prop.gcnArchName);
+    const int rc = scratch_setup(device); // the device is current
+    if (rc) return rc;
     aq_ctx *c = new aq_ctx();
     c->device = device;
     AQ_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
@@ -394,6 +424,26 @@ int aq_argmax(aq_ctx *ctx, const float *x_dev, size_t n, size_t t, uint32_t *ids
     int rc = launch_argmax(x_dev, n, n, t, ids_dev, scratch, ctx->stream);
     if (!rc && hipStreamSynchronize(ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_argmax: sync");
     (void)hipFree(scratch);
+    return rc;
+}
+
+int aq_argmax_noalloc(aq_ctx *ctx, const float *x_dev, size_t n, size_t t, uint32_t *ids_dev) {
+    AQ_REQUIRE(ctx && x_dev && ids_dev, "aq_argmax_noalloc: null argument");
+    AQ_REQUIRE(n >= 1 && t >= 1, "aq_argmax_noalloc: empty rows");
+    AQ_REQUIRE(n <= AQ_NOALLOC_MAX_N && t <= AQ_NOALLOC_MAX_ROWS,
+               "aq_argmax_noalloc: at most " + std::to_string(AQ_NOALLOC_MAX_ROWS) + " rows of at most " +
+                   std::to_string(AQ_NOALLOC_MAX_N) + " values (got " + std::to_string(t) + " x " +
+                   std::to_string(n) + ")");
+    static_assert((AQ_NOALLOC_MAX_ROWS * ((AQ_NOALLOC_MAX_N + 2047) / 2048) * 4 + 255) / 256 * 256 +
+                          AQ_NOALLOC_MAX_ROWS * ((AQ_NOALLOC_MAX_N + 2047) / 2048) * 4 <=
+                      AQ_NOALLOC_SCRATCH,
+                  "the argmax partials of the largest call fit the scratch array");
+    AQ_REQUIRE(argmax_scratch_bytes(n, t) <= AQ_NOALLOC_SCRATCH, "aq_argmax_noalloc: scratch too small");
+    void *sp = scratch_ptr(ctx->device);
+    AQ_REQUIRE(sp, "aq_argmax_noalloc: the device's scratch address is not set up (aq_init)");
+    AQ_HIP(hipSetDevice(ctx->device));
+    int rc = launch_argmax(x_dev, n, n, t, ids_dev, sp, ctx->stream);
+    if (!rc && hipStreamSynchronize(ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_argmax_noalloc: sync");
     return rc;
 }
 
