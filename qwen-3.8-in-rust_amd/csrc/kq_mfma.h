@@ -62,6 +62,12 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u16x2 as_u16x2(uint32_t w) { return __builtin_bit_cast(u16x2, w); }
 __device__ __forceinline__ uint32_t as_u32(u16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
+// a.lo * b.lo + a.hi * b.hi of two signed 16-bit pairs (v_dot2_i32_i16), exact in i32
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ int sdot2(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b), 0, false);
+}
+
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
 __device__ __forceinline__ int ubyte(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xFF); }
 
@@ -110,6 +116,7 @@ __device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t 
     int scl0[8], scl1[8];        // integer scale per sub-block, lanes j and j+4
     int mn0 = 0, mn1 = 0;        // Q4_K/Q5_K mins of sub-blocks 2j, 2j+1 (min lane j)
     int os00 = 0, os01 = 0, os10 = 0, os11 = 0; // Q6_K -32 fold scales: groups 2l, 2l+1 of l = j, j+4
+    uint32_t osp0 = 0, osp1 = 0;                 // the same as signed 16-bit pairs
     float dw, dminw = 0.0f;
     if constexpr (Q6) {
         const uint32_t ql0[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w};
@@ -134,6 +141,8 @@ __device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t 
         os10 = sbyte(sw[2 + (j >> 1)], 2 * (j & 1));
         os11 = sbyte(sw[2 + (j >> 1)], 2 * (j & 1) + 1);
         dw = h2f(wv.d6);
+        osp0 = ((uint32_t)os00 & 0xFFFFu) | ((uint32_t)os01 << 16);
+        osp1 = ((uint32_t)os10 & 0xFFFFu) | ((uint32_t)os11 << 16);
     } else {
         const uint32_t q0 = wv.sc.y, q1 = wv.sc.z, q2 = wv.sc.w;
         const uint32_t sc_lo = q0 & 0x3F3F3F3Fu, mn_lo = q1 & 0x3F3F3F3Fu;
@@ -205,8 +214,8 @@ __device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t 
                 const float dd = dxs[c] * dw;
                 const int lo0 = (int)(int16_t)(mw0[c] & 0xFFFF), hi0 = (int)(int16_t)(mw0[c] >> 16);
                 if constexpr (Q6) {
-                    const int lo1 = (int)(int16_t)(mw1[c] & 0xFFFF), hi1 = (int)(int16_t)(mw1[c] >> 16);
-                    const int i0 = s0[c] - 32 * (lo0 * os00 + hi0 * os01), i1 = s1[c] - 32 * (lo1 * os10 + hi1 * os11);
+                    // the -32 fold: lo * os_a + hi * os_b as one dot2 of the 16-bit pairs, exact
+                    const int i0 = s0[c] - 32 * sdot2(osp0, mw0[c]), i1 = s1[c] - 32 * sdot2(osp1, mw1[c]);
                     pr0[col] = dd * (float)i0;
                     pr1[col] = dd * (float)i1;
                     if constexpr (IS) {
@@ -263,13 +272,18 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
     const uint32_t sc_hi = (q2 & 0x0F0F0F0Fu) | ((q0 >> 2) & 0x30303030u);
     const uint32_t mn_hi = ((q2 >> 4) & 0x0F0F0F0Fu) | ((q1 >> 2) & 0x30303030u);
     const uint32_t mnw = j < 2 ? mn_lo : mn_hi;
-    const int mn0 = ubyte(mnw, 2 * (j & 1)), mn1 = ubyte(mnw, 2 * (j & 1) + 1);
-    // digit words: byte s of dig[i][0] (s < 4) / dig[i][1] (s >= 4) = digit i of sc[s]
-    uint32_t dig[ND][2];
+    // the min lane's two mins as a 16-bit pair, for one dot2 per column against the activation-sum pair
+    const uint32_t mnp = __builtin_amdgcn_perm(0u, mnw, (uint32_t)(2 * (j & 1)) | 0x0C00u |
+                                                          ((uint32_t)(2 * (j & 1) + 1) << 16) | 0x0C000000u);
+    // digit pair words: the 16-bit halves of dig[i][p] are digit i of sc[2p] and sc[2p + 1]; a packed multiply
+    // broadcasts one half to both halves of the code word (op_sel), so no per-sub-block byte shuffle is needed
+    uint32_t dig[ND][4];
 #pragma unroll
-    for (int i = 0; i < ND; i++) {
-        dig[i][0] = (sc_lo >> (DB * i)) & (DM * 0x01010101u);
-        dig[i][1] = (sc_hi >> (DB * i)) & (DM * 0x01010101u);
+    for (int p = 0; p < 4; p++) {
+        const uint32_t src = p < 2 ? sc_lo : sc_hi, b0 = (uint32_t)(2 * (p & 1));
+        const uint32_t pw = __builtin_amdgcn_perm(0u, src, b0 | 0x0C00u | ((b0 + 1u) << 16) | 0x0C000000u);
+#pragma unroll
+        for (int i = 0; i < ND; i++) dig[i][p] = (pw >> (DB * i)) & (DM * 0x00010001u);
     }
     uint32_t code0[8], code1[8];
     const uint32_t w0[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w};
@@ -306,8 +320,8 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
             for (int i = 0; i < ND; i++) {
                 // digit i of sc[s] in both 16-bit halves, then one packed 16-bit multiply per code word (the four
                 // byte products stay below 256, so no carry crosses a byte)
-                const uint32_t sel = (uint32_t)(s & 3) | 0x0C00u | ((uint32_t)(s & 3) << 16) | 0x0C000000u;
-                const u16x2 d2 = as_u16x2(__builtin_amdgcn_perm(0u, dig[i][s >> 2], sel));
+                const u16x2 dp = as_u16x2(dig[i][s >> 1]);
+                const u16x2 d2 = (s & 1) ? (u16x2){dp.y, dp.y} : (u16x2){dp.x, dp.x};
                 a0[i] = mfma_acc(x0[s], as_u32(as_u16x2(code0[s]) * d2), a0[i]);
                 a1[i] = mfma_acc(x1[s], as_u32(as_u16x2(code1[s]) * d2), a1[i]);
             }
@@ -327,8 +341,7 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
                     s1 = (s1 << DB) + a1[i][c];
                 }
                 const float dd = dxs[c] * dw;
-                const int lo0 = (int)(int16_t)(mw0[c] & 0xFFFF), hi0 = (int)(int16_t)(mw0[c] >> 16);
-                const int im = mn0 * lo0 + mn1 * hi0;
+                const int im = sdot2(mnp, mw0[c]); // mn0 * lo0 + mn1 * hi0, exact
                 pr0[col] = dd * (float)s0;
                 pr1[col] = dd * (float)s1;
                 pm[col] = (-dxs[c] * dminw) * (float)im;
@@ -395,7 +408,8 @@ __device__ __forceinline__ void kq_stage(const KqGroup &G, int8_t *sxq, float *s
     const int o = threadIdx.x & 15, nrec = ns * NC;
     for (int r0 = (int)threadIdx.x >> 4; r0 < nrec; r0 += 32) {
         const int ra = r0, rb = r0 + 16 < nrec ? r0 + 16 : r0; // the second record, or the first again
-        const int ca = ra / ns, sa = ra - ca * ns, cb = rb / ns, sbb = rb - cb * ns;
+        // record r = (super-block r / NC, column r % NC): NC is a constant, so no division by a runtime value
+        const int sa = ra / NC, ca = ra - sa * NC, sbb = rb / NC, cb = rb - sbb * NC;
         const uint4 va =
             *reinterpret_cast<const uint4 *>(G.xqs + (size_t)ca * G.xcol + (size_t)(s0 + sa) * 256 + o * 16);
         const uint4 vb =
@@ -404,7 +418,7 @@ __device__ __forceinline__ void kq_stage(const KqGroup &G, int8_t *sxq, float *s
         *reinterpret_cast<uint4 *>(sxq + ((size_t)sbb * NC + cb) * KQ_XS + o * 16) = vb;
     }
     for (int e = (int)threadIdx.x; e < nrec; e += 256) {
-        const int c = e / ns, sb = e % ns;
+        const int sb = e / NC, c = e - sb * NC;
         const size_t m = (size_t)c * nb + s0 + sb;
         sxd[sb * NCP + c] = G.xd[m];
         if constexpr (HAS45) {
@@ -436,28 +450,30 @@ struct KqStageRegs {
 };
 constexpr int KQ_STAGE_REGS = 5 * 16; // records the register staging holds
 
-__device__ __forceinline__ uint4 kq_rec_load(const KqGroup &G, int i, int ns, int nrec) {
-    const int rc = min((int)(threadIdx.x >> 4) + 16 * i, nrec - 1);
-    const int c = rc / ns, sb = rc - c * ns;
-    return *reinterpret_cast<const uint4 *>(G.xqs + (size_t)c * G.xcol + (size_t)sb * 256 + (threadIdx.x & 15) * 16);
+template <int NC>
+__device__ __forceinline__ uint4 kq_rec_load(const KqGroup &G, int i, int nrec) {
+    // unsigned 32-bit index math (the activations are far below 4 GiB): a constant divisor and one offset register
+    const uint32_t rc = min((threadIdx.x >> 4) + 16u * (uint32_t)i, (uint32_t)nrec - 1u);
+    const uint32_t sb = rc / NC, c = rc - sb * NC;
+    return *reinterpret_cast<const uint4 *>(G.xqs + (c * (uint32_t)G.xcol + sb * 256u + (threadIdx.x & 15u) * 16u));
 }
 template <int NC>
-__device__ __forceinline__ void kq_rec_store(int8_t *sxq, const uint4 v, int i, int ns, int nrec) {
+__device__ __forceinline__ void kq_rec_store(int8_t *sxq, const uint4 v, int i, int nrec) {
     // past the end a thread rewrites the last record with the bytes it loaded from there: no branches
-    const int rc = min((int)(threadIdx.x >> 4) + 16 * i, nrec - 1);
-    const int c = rc / ns, sb = rc - c * ns;
-    *reinterpret_cast<uint4 *>(sxq + ((size_t)sb * NC + c) * KQ_XS + (threadIdx.x & 15) * 16) = v;
+    const uint32_t rc = min((threadIdx.x >> 4) + 16u * (uint32_t)i, (uint32_t)nrec - 1u);
+    const uint32_t sb = rc / NC, c = rc - sb * NC;
+    *reinterpret_cast<uint4 *>(sxq + ((sb * NC + c) * KQ_XS + (threadIdx.x & 15u) * 16u)) = v;
 }
 template <int NC, bool HAS45, bool HAS6>
 __device__ __forceinline__ void kq_stage_load(const KqGroup &G, KqStageRegs<HAS45, HAS6> &R, int ns) {
     const int nb = G.nb, nrec = ns * NC;
-    R.r0 = kq_rec_load(G, 0, ns, nrec);
-    R.r1 = kq_rec_load(G, 1, ns, nrec);
-    R.r2 = kq_rec_load(G, 2, ns, nrec);
-    R.r3 = kq_rec_load(G, 3, ns, nrec);
-    R.r4 = kq_rec_load(G, 4, ns, nrec);
-    const int e = min((int)threadIdx.x, nrec - 1), c = e / ns, sb = e % ns;
-    const size_t m = (size_t)c * nb + sb;
+    R.r0 = kq_rec_load<NC>(G, 0, nrec);
+    R.r1 = kq_rec_load<NC>(G, 1, nrec);
+    R.r2 = kq_rec_load<NC>(G, 2, nrec);
+    R.r3 = kq_rec_load<NC>(G, 3, nrec);
+    R.r4 = kq_rec_load<NC>(G, 4, nrec);
+    const uint32_t e = min(threadIdx.x, (uint32_t)nrec - 1u), sb = e / NC, c = e - sb * NC;
+    const uint32_t m = c * (uint32_t)nb + sb;
     R.d = G.xd[m];
     if constexpr (HAS45) R.q8 = *reinterpret_cast<const uint4 *>(G.xq8s + m * 8);
     if constexpr (HAS6) {
@@ -471,12 +487,12 @@ __device__ __forceinline__ void kq_stage_store(const KqStageRegs<HAS45, HAS6> &R
     constexpr int NCP = (NC + 3) / 4 * 4;
     constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), P6 = HAS45 ? 4 : 0;
     const int nrec = ns * NC;
-    kq_rec_store<NC>(sxq, R.r0, 0, ns, nrec);
-    kq_rec_store<NC>(sxq, R.r1, 1, ns, nrec);
-    kq_rec_store<NC>(sxq, R.r2, 2, ns, nrec);
-    kq_rec_store<NC>(sxq, R.r3, 3, ns, nrec);
-    kq_rec_store<NC>(sxq, R.r4, 4, ns, nrec);
-    const int e = min((int)threadIdx.x, nrec - 1), c = e / ns, sb = e % ns;
+    kq_rec_store<NC>(sxq, R.r0, 0, nrec);
+    kq_rec_store<NC>(sxq, R.r1, 1, nrec);
+    kq_rec_store<NC>(sxq, R.r2, 2, nrec);
+    kq_rec_store<NC>(sxq, R.r3, 3, nrec);
+    kq_rec_store<NC>(sxq, R.r4, 4, nrec);
+    const uint32_t e = min(threadIdx.x, (uint32_t)nrec - 1u), sb = e / NC, c = e - sb * NC;
     sxd[sb * NCP + c] = R.d;
     if constexpr (HAS45) {
         const uint32_t pv[4] = {R.q8.x, R.q8.y, R.q8.z, R.q8.w};
@@ -787,8 +803,16 @@ __device__ __forceinline__ void kq_f32_run(const KqGroup &G, const KqSeg &sg, in
     }
 }
 
+// Up to four columns (four K slices, no Q5_K) the kernel fits 128 VGPRs without spilling, i.e. four waves per SIMD
+// (16 per CU, every wave slot of a CU with four work-groups); the bound keeps the compiler there (Q4_K at N = 4: 134
+// VGPRs otherwise, three waves per SIMD, and a quarter of a 4352-wave launch waiting for slots).
+template <int T0, int T1, int NC, int KSW, int PF>
+constexpr int kq_waves_per_eu() {
+    return NC <= 4 && KSW == 4 && T0 != AQ_TYPE_Q5_K && T1 != AQ_TYPE_Q5_K ? 4 : 1;
+}
 template <int T0, int T1, int NC, int KSW, int PF, bool IS = false>
-__global__ void __launch_bounds__(256) kq_wave_kernel(KqGroup G) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves_per_eu<T0, T1, NC, KSW, PF>())))
+kq_wave_kernel(KqGroup G) {
     constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
     constexpr bool HAS45 = T0 != AQ_TYPE_Q6_K || T1 != AQ_TYPE_Q6_K;
     constexpr int NCP = (NC + 3) / 4 * 4;

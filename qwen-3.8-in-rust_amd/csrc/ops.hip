@@ -311,6 +311,13 @@ constexpr int DN_TMAX = 8;      // rows per DeltaNet launch
 constexpr int DN_BLK_MAX = 256; // 32-blocks of the alpha/beta rows (hidden <= 8192)
 constexpr int DN_THREADS = 512; // waves 0-3 hold state columns (dv <= 256); 4-6 run the per-row sums
 
+// Parts per state column in the recurrence: as many as the work-group holds (H * DV <= DN_THREADS), at most four,
+// with whole float4s of keys per part.
+template <int DK, int DV>
+constexpr int dn_parts() {
+    return (4 * DV <= DN_THREADS && DK % 16 == 0) ? 4 : (2 * DV <= DN_THREADS && DK % 8 == 0) ? 2 : 1;
+}
+
 template <int DK, int DV>
 __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const int t) {
     static_assert(DK <= 256 && DV <= 256 && DN_THREADS >= 448 && DN_TMAX * 2 <= 16, "DeltaNet work-group shape");
@@ -508,85 +515,96 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
             rbeta[i] = a.raw ? v : sigmoid_f(v);
         }
     }
-    // ---- the state column (waves 0-3, which skip the sums above: the loads fly while waves 4 and 5 work; placed
-    // after the sums so the column's registers are not live inside them)
-    float s[DK];
+    // ---- the state column, split by key: thread j holds keys [h KH, h KH + KH) of column c = j % DV, part
+    // h = j / DV (the loads fly while waves 4-7 finish the sums above)
+    constexpr int H = dn_parts<DK, DV>(), KH = DK / H;
+    const int c = j % DV, h = j / DV;
+    const bool has_col = h < H;
+    float s[KH];
     float *srec = a.rec + (size_t)p * DK * DV;
-    if (has_v) {
+    if (has_col) {
 #pragma unroll
-        for (int k = 0; k < DK; k++) s[k] = srec[(size_t)k * DV + j];
+        for (int k = 0; k < KH; k++) s[k] = srec[(size_t)(h * KH + k) * DV + c];
     }
     __syncthreads();
     if (!a.raw) {
         for (int e = j; e < t * DK; e += DN_THREADS) {
-            const int i = e / DK, c = e % DK;
-            sq[i][c] = (sq[i][c] * rq[i]) * a.qscale;
-            sk[i][c] = sk[i][c] * rk[i];
+            const int i = e / DK, cc = e % DK;
+            sq[i][cc] = (sq[i][cc] * rq[i]) * a.qscale;
+            sk[i][cc] = sk[i][cc] * rk[i];
         }
         __syncthreads();
     }
 
-    // ---- C: the recurrence of column j (deltanet.rs:43-86). S *= decay and the kv sum share one pass over k,
-    // the update and the o sum another; each pass reads k (and q) from LDS a chunk of 32 at a time, all reads of a
-    // chunk issued before its first use.
-    if (has_v) {
-        constexpr int CH = DK < 32 ? DK : 32, NCH = DK / CH;    // pass 1 chunk (k)
-        constexpr int CH2 = DK < 16 ? DK : 16, NCH2 = DK / CH2; // pass 2 chunk (k and q)
-        static_assert(DK % CH == 0 && CH % 4 == 0 && DK % CH2 == 0 && CH2 % 4 == 0, "DeltaNet key width");
-        for (int i = 0; i < t; i++) {
-            const float decay = rdec[i], beta = rbeta[i], vval = sv[i][j];
-            const float4 *k4 = reinterpret_cast<const float4 *>(sk[i]), *q4 = reinterpret_cast<const float4 *>(sq[i]);
-            float kv = 0.0f;
+    // ---- C: the recurrence of column c (deltanet.rs:43-86), row after row. Each part updates its keys' state and
+    // forms their products in parallel (S *= decay, S k; then S += k delta, S q); the two sums over k stay one
+    // left-to-right chain from 0, handed from part to part in key order through LDS, so kv and o are the
+    // reference's sequential sums. Every thread meets the barriers. The two sums hand over through separate
+    // slots, so the next row's kv hand-off never overwrites an o hand-off still being read.
+    __shared__ float xfer[DV], xfer2[DV], xdelta[DV];
+    for (int i = 0; i < t; i++) {
+        float pk[KH];
+        float kv = 0.0f;
+        const float4 *k4 = reinterpret_cast<const float4 *>(sk[i] + h * KH);
+        const float4 *q4 = reinterpret_cast<const float4 *>(sq[i] + h * KH);
+        if (has_col) {
+            const float decay = rdec[i];
 #pragma unroll
-            for (int c = 0; c < NCH; c++) {
-                float4 kb[CH / 4];
+            for (int u = 0; u < KH / 4; u++) {
+                const float4 kb = k4[u];
+                const float kk[4] = {kb.x, kb.y, kb.z, kb.w};
 #pragma unroll
-                for (int u = 0; u < CH / 4; u++) kb[u] = k4[c * (CH / 4) + u];
-#pragma unroll
-                for (int u = 0; u < CH / 4; u++) {
-                    const float kk[4] = {kb[u].x, kb[u].y, kb[u].z, kb[u].w};
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int k = c * CH + 4 * u + e;
-                        s[k] *= decay;
-                        kv += s[k] * kk[e];
-                    }
+                for (int e = 0; e < 4; e++) {
+                    s[4 * u + e] *= decay;
+                    pk[4 * u + e] = s[4 * u + e] * kk[e];
                 }
-            }
-            const float delta = (vval - kv) * beta;
-            float ov = 0.0f;
-            // k is read again rather than kept: holding it next to S leaves no registers for reading ahead
-            __asm__ volatile("" ::: "memory");
-#pragma unroll
-            for (int c = 0; c < NCH2; c++) {
-                float4 kb[CH2 / 4], qb[CH2 / 4];
-#pragma unroll
-                for (int u = 0; u < CH2 / 4; u++) {
-                    kb[u] = k4[c * (CH2 / 4) + u];
-                    qb[u] = q4[c * (CH2 / 4) + u];
-                }
-#pragma unroll
-                for (int u = 0; u < CH2 / 4; u++) {
-                    const float kk[4] = {kb[u].x, kb[u].y, kb[u].z, kb[u].w};
-                    const float qq[4] = {qb[u].x, qb[u].y, qb[u].z, qb[u].w};
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int k = c * CH2 + 4 * u + e;
-                        s[k] += kk[e] * delta;
-                        ov += s[k] * qq[e];
-                    }
-                }
-            }
-            if (a.raw) {
-                if (a.out) a.out[(size_t)i * vd + p * DV + j] = ov;
-            } else {
-                so[i][j] = ov;
             }
         }
-        if (a.write_state) {
 #pragma unroll
-            for (int k = 0; k < DK; k++) srec[(size_t)k * DV + j] = s[k];
+        for (int hh = 0; hh < H; hh++) {
+            if (has_col && h == hh) {
+                if (hh > 0) kv = xfer[c];
+#pragma unroll
+                for (int k = 0; k < KH; k++) kv += pk[k];
+                if (hh + 1 < H) xfer[c] = kv;
+                else xdelta[c] = (sv[i][c] - kv) * rbeta[i];
+            }
+            __syncthreads();
         }
+        float ov = 0.0f;
+        if (has_col) {
+            const float delta = xdelta[c];
+#pragma unroll
+            for (int u = 0; u < KH / 4; u++) {
+                const float4 kb = k4[u], qb = q4[u];
+                const float kk[4] = {kb.x, kb.y, kb.z, kb.w}, qq[4] = {qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    s[4 * u + e] += kk[e] * delta;
+                    pk[4 * u + e] = s[4 * u + e] * qq[e];
+                }
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < H; hh++) {
+            if (has_col && h == hh) {
+                if (hh > 0) ov = xfer2[c];
+#pragma unroll
+                for (int k = 0; k < KH; k++) ov += pk[k];
+                if (hh + 1 < H) {
+                    xfer2[c] = ov;
+                } else if (a.raw) {
+                    if (a.out) a.out[(size_t)i * vd + p * DV + c] = ov;
+                } else {
+                    so[i][c] = ov;
+                }
+            }
+            if (hh + 1 < H) __syncthreads();
+        }
+    }
+    if (has_col && a.write_state) {
+#pragma unroll
+        for (int k = 0; k < KH; k++) srec[(size_t)(h * KH + k) * DV + c] = s[k];
     }
 
     // ---- D: gated RMSNorm of each output row
