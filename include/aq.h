@@ -211,6 +211,36 @@ typedef struct aq_model_bytes {
 } aq_model_bytes;
 int aq_model_get_bytes(const aq_model *m, aq_model_bytes *out);
 
+/* ------------------------------------------------------------------------------------------- GGUF files */
+
+/* A GGUF v3 file: header, metadata and tensor index parsed (`Gguf::open`, gguf.rs:483-608); the tensor data is
+ * mapped read-only, not read. */
+typedef struct aq_gguf aq_gguf;
+int aq_gguf_open(const char *path, aq_gguf **out);
+int aq_gguf_close(aq_gguf *g);
+int aq_gguf_info(const aq_gguf *g, uint32_t *alignment, uint64_t *data_offset, uint64_t *n_tensors, uint64_t *n_kv);
+/* Tensor i in file order (`Gguf::tensor`, gguf.rs:722): name, ggml type, rows (the outer dims; 1 for a vector) x
+ * cols (ne[0]), offset relative to the data section, bytes, and a pointer to the mapped bytes. Pointers live
+ * until aq_gguf_close. */
+int aq_gguf_tensor(const aq_gguf *g, uint64_t i, const char **name, int32_t *ggml_type, int64_t *rows, int64_t *cols,
+                   uint64_t *rel_offset, uint64_t *nbytes, const void **data);
+/* Typed metadata reads (`Gguf::get_u32` / `get_f32` / `get_str`); a missing key or another type is AQ_EINVAL. */
+int aq_gguf_get_u32(const aq_gguf *g, const char *key, uint32_t *out);
+int aq_gguf_get_f32(const aq_gguf *g, const char *key, float *out);
+int aq_gguf_get_str(const aq_gguf *g, const char *key, const char **out);
+/* `ModelConfig::from_gguf` (config.rs:146-379): the model contract from the metadata, checked against the tensor
+ * index (layer schedule, shapes); the vocabulary is len(tokenizer.ggml.tokens), or token_embd's rows without it. */
+int aq_gguf_model_config(const aq_gguf *g, aq_model_config *out);
+/* `Model::load` (model.rs:140-356) from a GGUF file: the config derived as above, every tensor copied to HBM.
+ * cfg_out (nullable) receives the config. */
+int aq_model_load_gguf(aq_ctx *ctx, const char *path, aq_model **out, aq_model_config *cfg_out);
+/* Offsets relative to the data section of the plan's tensors written in this order at `alignment`. */
+int aq_gguf_layout(const aq_tensor_plan *plan, size_t n, uint32_t alignment, uint64_t *rel_offsets);
+/* A GGUF v3 file of the synthetic model: aq_model_plan's tensors (bytes as aq_synth_host, `threads` workers) under
+ * the metadata keys the config derivation reads, with a placeholder tokenizer. No counterpart in the reference (its
+ * tiny checkpoint comes from tools/make_tiny_checkpoint.py and llama.cpp's converter). */
+int aq_gguf_write_synth(const char *path, const aq_model_config *cfg, int mix, uint64_t seed, int threads);
+
 /* Per-sequence state: DeltaNet conv/recurrent state, KV caches, the speculative buffers (spec_k drafts,
  * 0 = plain decode only) for positions < max_pos. `Model::new_state_spec` spec.rs:184 + `State::reserve`
  * model.rs:123. spec_k <= 7. */

@@ -93,6 +93,19 @@ def lib():
         "aq_kq_isums": (i, [P, P, P, sz, P, P]),
         "aq_argmax": (i, [P, P, sz, sz, P]),
         "aq_argmax_noalloc": (i, [P, P, sz, sz, P]),
+        "aq_gguf_open": (i, [C.c_char_p, C.POINTER(P)]),
+        "aq_gguf_close": (i, [P]),
+        "aq_gguf_info": (i, [P, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                             C.POINTER(C.c_uint64)]),
+        "aq_gguf_tensor": (i, [P, C.c_uint64, C.POINTER(C.c_char_p), C.POINTER(C.c_int32), C.POINTER(C.c_int64),
+                               C.POINTER(C.c_int64), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(P)]),
+        "aq_gguf_get_u32": (i, [P, C.c_char_p, C.POINTER(C.c_uint32)]),
+        "aq_gguf_get_f32": (i, [P, C.c_char_p, C.POINTER(C.c_float)]),
+        "aq_gguf_get_str": (i, [P, C.c_char_p, C.POINTER(C.c_char_p)]),
+        "aq_gguf_model_config": (i, [P, P]),
+        "aq_model_load_gguf": (i, [P, C.c_char_p, C.POINTER(P), P]),
+        "aq_gguf_layout": (i, [P, sz, C.c_uint32, P]),
+        "aq_gguf_write_synth": (i, [C.c_char_p, P, i, C.c_uint64, i]),
         "aq_matmul_time": (i, [P, P, sz, P, sz, P, i, C.POINTER(C.c_double)]),
         "aq_synth_host": (i, [P, P, i]),
         "aq_weight_synth": (i, [P, P, C.POINTER(P)]),
@@ -515,3 +528,86 @@ def eval_math(ctx: Context, fn, x):
     y = np.zeros_like(x)
     check(lib().aq_eval_math(ctx.h, fn, ptr(x), ptr(y), x.size))
     return y
+
+
+# ------------------------------------------------------------------------------------------------ GGUF files
+class Gguf:
+    """A GGUF v3 file (aq_gguf_open): metadata reads, the tensor index, the derived model config."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        check(lib().aq_gguf_open(os.fsencode(path), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().aq_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def info(self):
+        a, d, nt, nk = C.c_uint32(), C.c_uint64(), C.c_uint64(), C.c_uint64()
+        check(lib().aq_gguf_info(self.h, C.byref(a), C.byref(d), C.byref(nt), C.byref(nk)))
+        return {"alignment": a.value, "data_offset": d.value, "n_tensors": nt.value, "n_kv": nk.value}
+
+    def tensors(self, with_data=False):
+        """[(name, type, rows, cols, rel_offset, nbytes[, bytes])] in file order."""
+        out = []
+        for i in range(self.info()["n_tensors"]):
+            nm, t, r, c, off, nb, dp = (C.c_char_p(), C.c_int32(), C.c_int64(), C.c_int64(), C.c_uint64(),
+                                        C.c_uint64(), C.c_void_p())
+            check(lib().aq_gguf_tensor(self.h, i, C.byref(nm), C.byref(t), C.byref(r), C.byref(c), C.byref(off),
+                                       C.byref(nb), C.byref(dp)))
+            e = (nm.value.decode(), t.value, r.value, c.value, off.value, nb.value)
+            if with_data:
+                e += (np.ctypeslib.as_array((C.c_uint8 * nb.value).from_address(dp.value)).copy(),)
+            out.append(e)
+        return out
+
+    def get_u32(self, key):
+        v = C.c_uint32()
+        check(lib().aq_gguf_get_u32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def get_f32(self, key):
+        v = C.c_float()
+        check(lib().aq_gguf_get_f32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def get_str(self, key):
+        v = C.c_char_p()
+        check(lib().aq_gguf_get_str(self.h, key.encode(), C.byref(v)))
+        return v.value.decode()
+
+    def model_config(self):
+        c = AqModelConfig()
+        check(lib().aq_gguf_model_config(self.h, C.byref(c)))
+        return c
+
+
+def gguf_write_synth(path, cfg, mix, seed, threads=0):
+    check(lib().aq_gguf_write_synth(os.fsencode(path), C.byref(cfg), mix, seed, threads))
+
+
+def gguf_layout(plan_entries, alignment=32):
+    """Data-section offsets of [(name, AqSynthSpec)] written in this order."""
+    arr = (AqTensorPlan * len(plan_entries))()
+    for i, (name, sp) in enumerate(plan_entries):
+        arr[i].name = name.encode()
+        arr[i].spec = sp
+    out = np.zeros(len(plan_entries), np.uint64)
+    check(lib().aq_gguf_layout(arr, len(plan_entries), alignment, ptr(out)))
+    return out
+
+
+def model_load_gguf(ctx: Context, path):
+    """(Model, config) of a GGUF file (aq_model_load_gguf)."""
+    m = Model.__new__(Model)
+    m.ctx = ctx
+    cfg = AqModelConfig()
+    h = C.c_void_p()
+    check(lib().aq_model_load_gguf(ctx.h, os.fsencode(path), C.byref(h), C.byref(cfg)))
+    m.h, m.cfg = h, cfg
+    return m, cfg

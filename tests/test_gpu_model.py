@@ -224,6 +224,24 @@ def test_tiny_synth_on_device_equals_host_upload(ctx, tiny):
     assert tiny["gm"].bytes() == gs.bytes()
 
 
+def test_tiny_model_loaded_from_gguf_equals_tensor_table(ctx, tiny, tmp_path):
+    """aq_model_load_gguf (config derived from the file's metadata, tensors from the mapped file) against the same
+    model loaded from host tensors: the same config and bit-identical logits and state."""
+    print("case tiny model from a GGUF file", flush=True)
+    p = tmp_path / "tiny.gguf"
+    aq.gguf_write_synth(p, tiny["cfg"], aq.MIX_TINY, SEED, threads=4)
+    gm, cfg = aq.model_load_gguf(ctx, p)
+    assert all(getattr(cfg, n) == getattr(tiny["cfg"], n) for n, _ in aq.AqModelConfig._fields_)
+    a, b = aq.State(tiny["gm"], 0, 64), aq.State(gm, 0, 64)
+    ta, la = a.prefill(tiny["prompt"], want_logits=True)
+    tb, lb = b.prefill(tiny["prompt"], want_logits=True)
+    assert ta == tb and np.array_equal(la, lb)
+    for _ in range(4):
+        ta, tb = a.forward_token(ta), b.forward_token(tb)
+        assert ta == tb
+    assert np.array_equal(a.export(), b.export())
+
+
 def test_tiny_plain_greedy_matches_oracle(ctx, tiny):
     print("case tiny plain greedy", flush=True)
     gs = aq.State(tiny["gm"], 0, 128)
