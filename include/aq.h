@@ -98,6 +98,8 @@ const char *aq_last_error(void);
 const char *aq_build_hash(void);
 int aq_device_count(int *out);
 int aq_init(int device, aq_ctx **out);
+/* Frees the context's stream and events only. Objects made from it (weights, activations, models, states) are freed
+ * by their own calls, before or after this one; every other call on them needs the context alive. */
 int aq_ctx_free(aq_ctx *ctx);
 int aq_synchronize(aq_ctx *ctx);
 
@@ -125,16 +127,18 @@ int aq_act_new(aq_ctx *ctx, size_t n, size_t ncols, aq_act **out);
 int aq_act_free(aq_act *a);
 /* Upload `ncols` x `n` host f32 rows. */
 int aq_act_set_f32(aq_act *a, const float *host, size_t ncols);
-/* Quantise the f32 rows on the device: Q8_K (`Q8KRow::quantize_into`, q8k.rs:54-114) when `kind` is
- * AQ_TYPE_Q4_K/Q5_K/Q6_K, Q8_0 (`Q8Row::quantize_into`, q8.rs:68-106) when AQ_TYPE_Q8_0/Q4_0. */
+/* Quantise the f32 rows on the device for weights of `weight_type` (matvec.rs:147-160 `act_kind`): Q8_K
+ * (`Q8KRow::quantize_into`, q8k.rs:54-114) for AQ_TYPE_Q4_K/Q5_K/Q6_K, Q8_0 (`Q8Row::quantize_into`, q8.rs:68-106)
+ * for AQ_TYPE_Q8_0/Q4_0, and for the K-quants too while the q8-fine switch is on. */
 int aq_act_quantize(aq_act *a, int weight_type, size_t ncols);
 /* The quantised rows in ggml wire layout: Q8_K 292 B per 256 (q8k.rs:139-150), Q8_0 34 B per 32 (q8.rs:155-162). */
 int aq_act_get_q8k(const aq_act *a, void *ggml_out, size_t ncols);
 int aq_act_get_q8_0(const aq_act *a, void *ggml_out, size_t ncols);
 
-/* y[c * rows + r] = W[r] . x[c] for c < ncols (ncols 1..16; 1 is the matvec). Replaces `matvec`
- * (matvec.rs:336), `matmul_fn` (matvec.rs:377) and the blocked kernel `dot_q8k_t` (kdot.rs:314). `y_dev` is a
- * device buffer of ncols * rows f32. The activation must have been quantised for w's type. */
+/* y[c * rows + r] = W[r] . x[c] for c < ncols (ncols 1..8, at most the activation's columns; 1 is the matvec). Replaces `matvec`
+ * (matvec.rs:336), `matmul_fn` (matvec.rs:377) and the blocked kernel `dot_q8k_t` (kdot.rs:314); under the q8-fine
+ * switch, K-quant weights take `dot_q4_k_q8` / `dot_q5_k_q8` / `dot_q6_k_q8` (dot.rs:69-160). `y_dev` is a device
+ * buffer of ncols * rows f32. The activation must have been quantised for w's type under the same switch. */
 int aq_matmul(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, float *y_dev);
 /* The exact integers of the K-quant dot, from the same kernel and grid aq_matmul runs (instantiated with its
  * integer outputs on): per column c < ncols (1, 4 or 8), row and super-block the 8 i32 lane sums and (Q4_K/Q5_K) the
@@ -142,6 +146,14 @@ int aq_matmul(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, fl
  * lanes_dev: ncols*rows*nb*8 ([c][row][sb][lane]); mins_dev: ncols*rows*nb*4 (zero for Q6_K). */
 int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, int32_t *lanes_dev,
                 int32_t *mins_dev);
+
+/* The q8-fine switch: `set_q8_fine` / `q8_fine` (matvec.rs:127-145, `aqueduct run --q8-fine`, run.rs:203). Process-
+ * wide, off by default. On, K-quant weights take Q8_0 activations (per-32 scales, the dots of dot.rs:69-160) instead
+ * of Q8_K ones, in aq_act_quantize / aq_matmul and in every model call (forward, prefill, speculative rounds). Every
+ * later call reads it: change it only while no call is running, and between a quantise and its matmul keep it
+ * unchanged. aq_kq_isums is the Q8_K kernel's and returns AQ_EUNSUP while it is on. */
+int aq_set_q8_fine(int on);
+int aq_q8_fine(void);
 
 /* ids_dev[r] = argmax of row r of the t rows of n f32 at x_dev (device): `argmax` (model.rs:505-513), the first
  * maximum on ties; a NaN never becomes the maximum, and a NaN at index 0 is never replaced (the answer is 0). */

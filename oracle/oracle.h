@@ -39,11 +39,15 @@ void or_dot_q8k_t(int type, const uint8_t *w, const uint8_t *const *xs, size_t t
 void or_kq_isums(int type, const uint8_t *w, const uint8_t *x_q8k, size_t n, int32_t *lanes, int32_t *mins);
 void or_kq_isums_mat(int type, const uint8_t *w, size_t rows, const uint8_t *x_q8k, size_t n, int32_t *lanes,
                      int32_t *mins);
-float or_dot_q8(int type, const uint8_t *w, const uint8_t *x_q8_0, size_t n);
+float or_dot_q8(int type, const uint8_t *w, const uint8_t *x_q8_0, size_t n); /* any quantised type */
 float or_dot_f32(const float *w, const float *x, size_t n);
 
 /* ---- matmul: y[c*rows + r] = W[r] . x[c] from f32 activations, quantised as the weight type requires
- * (matvec.rs:147-160 act_kind, 282-292 one_row, 511-539 matmul_impl). threads <= 0: all. */
+ * (matvec.rs:147-160 act_kind, 282-292 one_row, 511-539 matmul_impl). threads <= 0: all. With the q8-fine switch
+ * on (matvec.rs:133 set_q8_fine; process-wide, read by every later matmul and model call), K-quant weights take
+ * Q8_0 activations (dot.rs:69-160). */
+void or_set_q8_fine(int on);
+int or_q8_fine(void);
 void or_matmul(int type, const uint8_t *w, size_t rows, size_t cols, const float *x, size_t ncols, float *y,
                int threads);
 

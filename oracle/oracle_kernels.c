@@ -162,8 +162,9 @@ void or_q8k_quantize(const float *x, size_t n, uint8_t *out) {
     or_q8k_release(&r);
 }
 
-/* q8.rs:81-121 `Q8Row::quantize_scalar_into` (ggml quantize_row_q8_0_ref); only d (f16 bits), d32 and the
- * codes are kept: the derived `dxs`/`off6` serve the `--q8-fine` K-quant kernels, which are out of scope. */
+/* q8.rs:81-121 `Q8Row::quantize_scalar_into` (ggml quantize_row_q8_0_ref); d (f16 bits), d32 and the codes are
+ * kept. The derived `dxs`/`off6` of q8.rs:107-120 are recomputed from the codes where the K-quant x Q8_0 dots
+ * need them (q8_fine_sums below), with the same integer sums and the same single f32 product. */
 void or_q8_from_f32(const float *x, size_t n, or_q8 *r) {
     size_t nb = n / 32;
     r->n = n;
@@ -533,8 +534,90 @@ void or_kq_isums_mat(int type, const uint8_t *w, size_t rows, const uint8_t *x_q
 
 /* ================================================================== Q8_0 / Q4_0 / F32 weight dots */
 
-/* dot.rs:29-45 `dot_q8_0_q8` and dot.rs:48-66 `dot_q4_0_q8`: one f32 accumulator, blocks left to right. */
+/* q8.rs:107-120 `Q8Row::derive` for one 32-block: lo = sum(q[0..16]), hi = sum(q[16..32]); dxs = d32 * f32(lo + hi)
+ * (exact: an 11-bit scale times a sum of at most 12 bits); off6 = [32 lo, 0, 0, 0, 32 hi, 0, 0, 0]. */
+static void q8_fine_sums(const or_q8 *x, size_t b, int32_t *lo, int32_t *hi, float *dxs) {
+    int32_t l = 0, h = 0;
+    for (int j = 0; j < 16; j++) l += x->qs[b * 32 + j];
+    for (int j = 16; j < 32; j++) h += x->qs[b * 32 + j];
+    *lo = l;
+    *hi = h;
+    *dxs = x->d32[b] * (float)(l + h);
+}
+
+/* dot.rs:69-99 `dot_q45_k_q8` (with the code closures of dot.rs:101-117), the `--q8-fine` form of Q4_K / Q5_K
+ * (matvec.rs:129-160): per sub-block s of super-block sb, against the Q8_0 block xb = 8 sb + s, 8 exact i32 lanes
+ * p32[j/4] += q*x; acc[i] += f32(p32[i]) * (d32[xb] * (d * sc)); accm[s] += (m * -dmin) * dxs[xb]; the result is
+ * reduce8(acc) + reduce8(accm). No FMA. */
+static float dot_q45_k_q8(int q5, const uint8_t *w, const or_q8 *x) {
+    const size_t bb = q5 ? 176 : 144;
+    float acc[8] = {0}, accm[8] = {0};
+    for (size_t sb = 0; sb < x->nb / 8; sb++) {
+        const uint8_t *wb = w + sb * bb;
+        const float d = f16_at(wb, 0), dmin = f16_at(wb, 2);
+        for (int s = 0; s < 8; s++) {
+            int sc, m;
+            scale_min_k4(s, wb + 4, &sc, &m);
+            const size_t xb = sb * 8 + s;
+            const int8_t *xq = x->qs + xb * 32;
+            int32_t p32[8] = {0};
+            for (int j = 0; j < 32; j++) p32[j / 4] += code_q45(wb, q5, s, j) * xq[j];
+            const float f = x->d32[xb] * (d * (float)sc);
+            for (int i = 0; i < 8; i++) acc[i] += (float)p32[i] * f;
+            int32_t lo, hi;
+            float dxs;
+            q8_fine_sums(x, xb, &lo, &hi, &dxs);
+            accm[s] += ((float)m * -dmin) * dxs;
+        }
+    }
+    return reduce8(acc) + reduce8(accm);
+}
+
+/* dot.rs:119-160 `dot_q6_k_q8`: unsigned 6-bit codes against Q8_0 block xb = 8 sb + 4 half + k; the -32 offset is
+ * taken in integer from lane 0 (32 lo) and lane 4 (32 hi); lanes 0..3 are scaled by the group scale sc[2k], lanes
+ * 4..7 by sc[2k + 1]: acc[i] += f32(p32[i]) * (d32[xb] * (d * sc)); the result is reduce8(acc). */
+static float dot_q6_k_q8(const uint8_t *w, const or_q8 *x) {
+    float acc[8] = {0};
+    for (size_t sb = 0; sb < x->nb / 8; sb++) {
+        const uint8_t *wb = w + sb * 210;
+        const float d = f16_at(wb, 208);
+        for (int half = 0; half < 2; half++) {
+            const uint8_t *ql = wb + half * 64, *qh = wb + 128 + half * 32;
+            const int8_t *sc = (const int8_t *)(wb + 192 + half * 8);
+            for (int k = 0; k < 4; k++) {
+                const size_t xb = sb * 8 + half * 4 + k;
+                const int8_t *xq = x->qs + xb * 32;
+                int32_t p32[8] = {0};
+                for (int l = 0; l < 32; l++) {
+                    int lo;
+                    switch (k) {
+                    case 0: lo = ql[l] & 0xF; break;
+                    case 1: lo = ql[l + 32] & 0xF; break;
+                    case 2: lo = ql[l] >> 4; break;
+                    default: lo = ql[l + 32] >> 4; break;
+                    }
+                    const int hi = (qh[l] >> (2 * k)) & 3;
+                    p32[l / 4] += (lo | (hi << 4)) * xq[l];
+                }
+                int32_t slo, shi;
+                float dxs;
+                q8_fine_sums(x, xb, &slo, &shi, &dxs);
+                p32[0] -= 32 * slo;
+                p32[4] -= 32 * shi;
+                const float f_lo = x->d32[xb] * (d * (float)sc[2 * k]);
+                const float f_hi = x->d32[xb] * (d * (float)sc[2 * k + 1]);
+                for (int i = 0; i < 8; i++) acc[i] += (float)p32[i] * (i < 4 ? f_lo : f_hi);
+            }
+        }
+    }
+    return reduce8(acc);
+}
+
+/* dot.rs:29-45 `dot_q8_0_q8` and dot.rs:48-66 `dot_q4_0_q8`: one f32 accumulator, blocks left to right; K-quant
+ * weights take the Q8_0-grain kernels above (dot.rs:202-226 `dot_q8` routes every type). */
 float or_dot_q8_row(int type, const uint8_t *w, const or_q8 *x) {
+    if (type == AQ_TYPE_Q4_K || type == AQ_TYPE_Q5_K) return dot_q45_k_q8(type == AQ_TYPE_Q5_K, w, x);
+    if (type == AQ_TYPE_Q6_K) return dot_q6_k_q8(w, x);
     float acc = 0.0f;
     if (type == AQ_TYPE_Q8_0) {
         for (size_t b = 0; b < x->nb; b++) {

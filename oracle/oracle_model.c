@@ -107,13 +107,19 @@ static float *get_vec(const aq_tensor *ts, size_t n, const char *name, size_t le
     return v;
 }
 
+/* matvec.rs:127-145 `Q8_FINE` / `set_q8_fine` / `q8k_activations`: process-wide, off by default. */
+static int g_q8_fine = 0;
+void or_set_q8_fine(int on) { g_q8_fine = on != 0; }
+int or_q8_fine(void) { return g_q8_fine; }
+
 /* matvec.rs:147-160 `act_kind` + 282-292 `one_row` + 483-539 `matmul_impl`: y[c*rows + r] = W[r] . x[c].
- * K-quant weights take Q8_K rows through the blocked kernel (bit-identical to the single-row one); Q8_0/Q4_0
- * take Q8_0 rows; F32 takes f32. Row-parallel; every row is computed by one thread, so thread count never
- * changes a bit (matvec.rs:1-4). */
+ * K-quant weights take Q8_K rows through the blocked kernel (bit-identical to the single-row one), or with the
+ * q8-fine switch on, Q8_0 rows one row at a time (`one_row` -> `dot_q8`); Q8_0/Q4_0 take Q8_0 rows; F32 takes f32.
+ * Row-parallel; every row is computed by one thread, so thread count never changes a bit (matvec.rs:1-4). */
 static void matmul(const or_mat *w, const float *x, size_t ncols, float *y, int threads) {
     size_t rows = w->rows, cols = w->cols;
-    if (w->type == AQ_TYPE_Q4_K || w->type == AQ_TYPE_Q5_K || w->type == AQ_TYPE_Q6_K) {
+    const int kq = w->type == AQ_TYPE_Q4_K || w->type == AQ_TYPE_Q5_K || w->type == AQ_TYPE_Q6_K;
+    if (kq && !g_q8_fine) {
         or_q8k *acts = (or_q8k *)calloc(ncols, sizeof(or_q8k));
         const or_q8k *ptrs[16];
         for (size_t c = 0; c < ncols; c++) {
@@ -132,7 +138,7 @@ static void matmul(const or_mat *w, const float *x, size_t ncols, float *y, int 
         }
         for (size_t c = 0; c < ncols; c++) or_q8k_release(&acts[c]);
         free(acts);
-    } else if (w->type == AQ_TYPE_Q8_0 || w->type == AQ_TYPE_Q4_0) {
+    } else if (kq || w->type == AQ_TYPE_Q8_0 || w->type == AQ_TYPE_Q4_0) {
         or_q8 *acts = (or_q8 *)calloc(ncols, sizeof(or_q8));
         for (size_t c = 0; c < ncols; c++) {
             or_q8_alloc(&acts[c], cols);

@@ -91,6 +91,8 @@ def lib():
         "aq_act_get_q8_0": (i, [P, P, sz]),
         "aq_matmul": (i, [P, P, P, sz, P]),
         "aq_kq_isums": (i, [P, P, P, sz, P, P]),
+        "aq_set_q8_fine": (i, [i]),
+        "aq_q8_fine": (i, []),
         "aq_argmax": (i, [P, P, sz, sz, P]),
         "aq_argmax_noalloc": (i, [P, P, sz, sz, P]),
         "aq_gguf_open": (i, [C.c_char_p, C.POINTER(P)]),
@@ -270,6 +272,21 @@ def matmul(ctx: Context, w: Weight, x: Act, ncols, y: DeviceBuffer = None):
     if own:
         y.free()
     return out
+
+
+class q8_fine:
+    """The q8-fine switch (aq_set_q8_fine; matvec.rs:133 `set_q8_fine`) on inside the block, restored after."""
+
+    def __init__(self, on=True):
+        self.on = on
+
+    def __enter__(self):
+        self.prev = lib().aq_q8_fine()
+        check(lib().aq_set_q8_fine(1 if self.on else 0))
+        return self
+
+    def __exit__(self, *exc):
+        check(lib().aq_set_q8_fine(self.prev))
 
 
 def kq_isums(ctx: Context, w: Weight, x: Act, ncols=1):

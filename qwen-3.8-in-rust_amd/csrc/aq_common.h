@@ -49,6 +49,12 @@ inline int block_bytes(int t) {
 }
 inline bool is_kquant(int t) { return t == AQ_TYPE_Q4_K || t == AQ_TYPE_Q5_K || t == AQ_TYPE_Q6_K; }
 
+// The q8-fine switch (matvec.rs:127-145 `Q8_FINE`, `set_q8_fine`): process-wide, off by default. On, K-quant weights
+// take Q8_0 activations (per-32 scales) through launch_kq_q8f instead of Q8_K ones; every later quantiser choice and
+// K-quant launch reads it, so it is changed only while no call is running.
+bool q8_fine();
+void set_q8_fine(bool on);
+
 // Device weight planes. A ggml row of `nb` blocks is split into planes so that every kernel load is an aligned
 // vector load; the integer math is unchanged (the GGUF bytes are the source of truth and aq_weight_download
 // restores them exactly).
@@ -133,6 +139,9 @@ int launch_kq_mfma(const Weight &w, const Act &x, size_t ncols, float *y, const 
 // last launch. resids may be null.
 int launch_kq_group(const Weight *const *ws, float *const *ys, const float *const *resids, int n, const Act &x,
                     size_t ncols, hipStream_t stream);
+// K-quant weights x Q8_0 activations (kq_q8f.hip, dot.rs:69-160); launch_matmul routes K-quant weights here when
+// the q8-fine switch is on. y as launch_matmul; ncols 1..16.
+int launch_kq_q8f(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
 int launch_repack(Weight &w, const uint8_t *ggml_dev, bool to_planes, hipStream_t stream);
 
 } // namespace aq

@@ -29,6 +29,13 @@ int launch_run(const Weight *const *ws, float *const *ys, const float *const *re
 int launch_kq_group(const Weight *const *ws, float *const *ys, const float *const *resids, int n, const Act &x,
                     size_t ncols, hipStream_t stream) {
     AQ_REQUIRE(n >= 1 && ws && ys, "kq_mfma: no matrices");
+    if (q8_fine()) { // Q8_0 activations: one launch per matrix (matvec.rs:282-292 `one_row` for every type)
+        for (int i = 0; i < n; i++) {
+            const int rc = launch_matmul(*ws[i], x, ncols, ys[i], resids ? resids[i] : nullptr, stream);
+            if (rc) return rc;
+        }
+        return 0;
+    }
     AQ_REQUIRE(ncols >= 1 && ncols <= 8, "kq_mfma: ncols must be 1..8");
     int nq = 0; // the K-quant matrices come first; F32 ones (at most two) ride in the last launch
     while (nq < n && ws[nq]->type != AQ_TYPE_F32) nq++;

@@ -496,7 +496,8 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
 } // namespace
 
 int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream) {
-    if (is_kquant(w.type)) return launch_kq_mfma(w, x, ncols, y, resid, stream);
+    if (is_kquant(w.type))
+        return q8_fine() ? launch_kq_q8f(w, x, ncols, y, resid, stream) : launch_kq_mfma(w, x, ncols, y, resid, stream);
     Q8Args args{};
     args.type = w.type;
     args.qa = w.qa;

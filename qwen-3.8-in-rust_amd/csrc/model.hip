@@ -178,6 +178,7 @@ struct DevLayer {
 
 struct aq_model {
     aq_ctx *ctx = nullptr;
+    int device = 0; // the context's device, kept so that freeing never reads the context
     aq_model_config cfg{};
     size_t kd = 0, vd = 0, cd = 0;
     aq::Weight embed, lm_head;
@@ -336,6 +337,7 @@ uint64_t layer_bytes(const aq_model *m, const DevLayer &L) {
 int build_model(aq_ctx *ctx, const aq_model_config *cfg, Source &src, aq_model **out) {
     aq_model *m = new aq_model();
     m->ctx = ctx;
+    m->device = ctx->device;
     m->cfg = *cfg;
     m->kd = (size_t)cfg->dn_n_k_heads * cfg->dn_head_dim_k;
     m->vd = (size_t)cfg->dn_n_v_heads * cfg->dn_head_dim_v;
@@ -395,6 +397,7 @@ struct KvDev {
 
 struct aq_state {
     aq_model *m = nullptr;
+    int device = 0; // the model's device, kept so that freeing never reads the model
     hipStream_t stream = nullptr;
     hipEvent_t ev[5] = {};
     bool ev_pending = false;
@@ -865,7 +868,7 @@ int aq_model_synth(aq_ctx *ctx, const aq_model_config *cfg, int mix, uint64_t se
 }
 
 int aq_model_free(aq_model *m) {
-    if (m) (void)hipSetDevice(m->ctx->device);
+    if (m) (void)hipSetDevice(m->device);
     free_model(m);
     return 0;
 }
@@ -885,6 +888,7 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
     const aq_model_config &c = m->cfg;
     aq_state *s = new aq_state();
     s->m = m;
+    s->device = m->device;
     s->k = spec_k;
     s->max_pos = max_pos + MAX_ROWS; // room for a verify batch past the last committed position
     const size_t T = MAX_ROWS, h = c.hidden, nv = c.dn_n_v_heads;
@@ -1044,7 +1048,7 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
 }
 
 int aq_state_free(aq_state *s) {
-    if (s) (void)hipSetDevice(s->m->ctx->device);
+    if (s) (void)hipSetDevice(s->device);
     free_state(s);
     return 0;
 }
@@ -1267,6 +1271,7 @@ int aq_layer_run(aq_ctx *ctx, const aq_model_config *cfg, const aq_tensor *tenso
     AQ_HIP(hipSetDevice(ctx->device));
     aq_model *m = new aq_model();
     m->ctx = ctx;
+    m->device = ctx->device;
     m->cfg = *cfg;
     m->cfg.n_layer = 0;
     m->cfg.has_mtp = 0;

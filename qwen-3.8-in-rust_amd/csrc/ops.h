@@ -9,10 +9,11 @@
 namespace aq {
 
 // What a row kernel writes besides (optionally) f32: nothing, Q8_K (for K-quant weights) or Q8_0 (for Q8_0 /
-// Q4_0 weights). F32 weights read the f32 rows.
+// Q4_0 weights, and for K-quant weights under the q8-fine switch). F32 weights read the f32 rows
+// (matvec.rs:147-160 `act_kind`).
 enum QuantKind { QK_NONE = 0, QK_Q8K = 1, QK_Q80 = 2 };
 inline QuantKind quant_kind_for(int weight_type) {
-    if (is_kquant(weight_type)) return QK_Q8K;
+    if (is_kquant(weight_type)) return q8_fine() ? QK_Q80 : QK_Q8K;
     if (weight_type == AQ_TYPE_Q8_0 || weight_type == AQ_TYPE_Q4_0) return QK_Q80;
     return QK_NONE;
 }

@@ -1,5 +1,6 @@
 // runtime.hip — lifecycle, device memory, weights, activation buffers and the operator-level C-ABI
 // (include/aq.h). Every entry point validates its arguments and returns an AQ_E* code instead of aborting.
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -13,8 +14,18 @@ static thread_local std::string g_last_error;
 
 void set_error(const std::string &msg) { g_last_error = msg; }
 
+namespace {
+std::atomic<bool> g_q8_fine{false};
+}
+bool q8_fine() { return g_q8_fine.load(std::memory_order_relaxed); }
+void set_q8_fine(bool on) { g_q8_fine.store(on, std::memory_order_relaxed); }
+
+// Every error return passes here: it also clears HIP's per-thread last error, so that a failed runtime call whose
+// code this library already reported (an allocation that ran out of memory, say) is not reported again by the
+// launch check of a later, unrelated call.
 int fail(int code, const std::string &msg) {
     set_error(msg);
+    (void)hipGetLastError();
     return code;
 }
 
@@ -265,7 +276,7 @@ int aq_weight_upload(aq_ctx *ctx, int ggml_type, size_t rows, size_t cols, const
 
 int aq_weight_free(aq_weight *w) {
     if (!w) return 0;
-    (void)hipSetDevice(w->ctx->device);
+    (void)hipSetDevice(w->w.device);
     free_weight(w->w);
     delete w;
     return 0;
@@ -305,7 +316,7 @@ int aq_act_new(aq_ctx *ctx, size_t n, size_t ncols, aq_act **out) {
 
 int aq_act_free(aq_act *a) {
     if (!a) return 0;
-    (void)hipSetDevice(a->ctx->device);
+    (void)hipSetDevice(a->a.device);
     free_act(a->a);
     delete a;
     return 0;
@@ -324,11 +335,11 @@ int aq_act_quantize(aq_act *a, int weight_type, size_t ncols) {
     AQ_REQUIRE(a, "aq_act_quantize: null act");
     AQ_REQUIRE(ncols >= 1 && ncols <= a->a.ncols, "aq_act_quantize: ncols out of range");
     AQ_HIP(hipSetDevice(a->ctx->device));
-    if (is_kquant(weight_type)) {
+    if (is_kquant(weight_type) && !q8_fine()) {
         AQ_REQUIRE(a->a.n % 256 == 0, "aq_act_quantize: Q8_K needs n % 256 == 0 (matvec.rs:73-77)");
         return launch_q8k_quantize(a->a, ncols, a->a.f32, a->a.n, a->ctx->stream);
     }
-    if (weight_type == AQ_TYPE_Q8_0 || weight_type == AQ_TYPE_Q4_0) {
+    if (is_kquant(weight_type) || weight_type == AQ_TYPE_Q8_0 || weight_type == AQ_TYPE_Q4_0) {
         AQ_REQUIRE(a->a.n % 32 == 0, "aq_act_quantize: Q8_0 needs n % 32 == 0");
         return launch_q8_0_quantize(a->a, ncols, a->a.f32, a->a.n, a->ctx->stream);
     }
@@ -400,8 +411,16 @@ int aq_matmul(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, fl
     return 0;
 }
 
+int aq_set_q8_fine(int on) {
+    set_q8_fine(on != 0);
+    return 0;
+}
+
+int aq_q8_fine(void) { return q8_fine() ? 1 : 0; }
+
 int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, int32_t *lanes_dev,
                 int32_t *mins_dev) {
+    if (q8_fine()) return fail(AQ_EUNSUP, "aq_kq_isums: the integer lanes are the Q8_K kernel's; q8-fine is on");
     AQ_REQUIRE(ctx && w && x && lanes_dev && mins_dev, "aq_kq_isums: null argument");
     AQ_REQUIRE(is_kquant(w->w.type), "aq_kq_isums: K-quant weights only");
     AQ_REQUIRE(x->a.n == w->w.cols, "aq_kq_isums: activation length");

@@ -88,6 +88,8 @@ def lib():
         "or_dot_q8": (C.c_float, [C.c_int, P, P, sz]),
         "or_dot_f32": (C.c_float, [P, P, sz]),
         "or_matmul": (None, [C.c_int, P, sz, sz, P, sz, P, C.c_int]),
+        "or_set_q8_fine": (None, [C.c_int]),
+        "or_q8_fine": (C.c_int, []),
         "or_rmsnorm": (None, [P, P, C.c_float, P, sz]),
         "or_rmsnorm_gated": (None, [P, P, P, C.c_float, P, sz]),
         "or_softmax": (None, [P, P, sz]),
@@ -186,6 +188,21 @@ def dot_q8k_t(t, wrow, xqs, n):
 
 def dot_q8(t, wrow, xq, n):
     return lib().or_dot_q8(t, ptr(np.ascontiguousarray(wrow)), ptr(np.ascontiguousarray(xq)), n)
+
+
+class q8_fine:
+    """Context manager: the oracle's process-wide q8-fine switch (matvec.rs:133 set_q8_fine) on inside the block."""
+
+    def __init__(self, on=True):
+        self.on = on
+
+    def __enter__(self):
+        self.prev = lib().or_q8_fine()
+        lib().or_set_q8_fine(1 if self.on else 0)
+        return self
+
+    def __exit__(self, *exc):
+        lib().or_set_q8_fine(self.prev)
 
 
 def matmul(t, w, rows, cols, x, threads=4):
