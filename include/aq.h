@@ -79,6 +79,16 @@ typedef struct aq_model_config {
     uint32_t has_mtp;      /* 1: blk.{n_layer} is an MTP (nextn) block */
 } aq_model_config;
 
+/* The sampler's settings (`SamplerConfig`, sample.rs:57-68): temperature <= 0 is greedy (argmax; the other fields
+ * unused), top_k 0 = off, top_p >= 1 = off, min_p 0 = off; seed seeds xoshiro256** through splitmix64. */
+typedef struct aq_sampler_config {
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    float min_p;
+    uint64_t seed;
+} aq_sampler_config;
+
 /* Per-round counters of the speculative loop (the reference's SpecStats, spec.rs:12-59). */
 typedef struct aq_spec_stats {
     uint64_t rounds, drafted, accepted, emitted;
@@ -164,6 +174,33 @@ int aq_argmax(aq_ctx *ctx, const float *x_dev, size_t n, size_t t, uint32_t *ids
  * call on one GPU shares that array: calls that overlap on one GPU (several contexts or threads) race. Nothing in
  * it carries from one call to the next. Same results as aq_argmax. */
 int aq_argmax_noalloc(aq_ctx *ctx, const float *x_dev, size_t n, size_t t, uint32_t *ids_dev);
+
+/* ---------------------------------------------------------------------------------------------- sampler */
+
+/* The sampler on the device: `Sampler` (sample.rs:148-303) with its xoshiro256** state in device memory. Replaces
+ * `Sampler::new` (sample.rs:159), `reseed` (164). Buffers are sized for `vocab` at creation; every call below runs on
+ * the context's stream and returns after it (the model's sampled calls run it on the state's stream instead: one
+ * sampler is used by one call at a time). */
+typedef struct aq_sampler aq_sampler;
+int aq_sampler_new(aq_ctx *ctx, const aq_sampler_config *cfg, uint32_t vocab, aq_sampler **out);
+int aq_sampler_free(aq_sampler *sp);
+int aq_sampler_reseed(aq_sampler *sp, uint64_t seed);
+/* The generator's four state words (for reproducibility checks). */
+int aq_sampler_get_rng(aq_sampler *sp, uint64_t *out4);
+/* `process` (sample.rs:181-236) of the vocab logits at logits_dev: the kept set (ids by probability descending,
+ * probabilities summing to 1) stays on the device; n_kept (nullable) receives its size. Greedy: the argmax alone. */
+int aq_sampler_process(aq_sampler *sp, const float *logits_dev, uint32_t *n_kept);
+/* `kept` (sample.rs:176-179): host copies of the last kept set (cap entries at most); *n its size. */
+int aq_sampler_kept(aq_sampler *sp, uint32_t *ids, float *probs, size_t cap, size_t *n);
+/* `draw` (sample.rs:239-251) from the last kept set; `sample` (254-257) = process then draw. */
+int aq_sampler_draw(aq_sampler *sp, uint32_t *tok);
+int aq_sampler_sample(aq_sampler *sp, const float *logits_dev, uint32_t *tok);
+/* `write_dense` (sample.rs:259-265): the last kept set as vocab f32 at dense_dev, zeros elsewhere. */
+int aq_sampler_write_dense(aq_sampler *sp, float *dense_dev);
+/* `accept_or_resample` (sample.rs:272-303): accept draft d with probability min(1, p(d)/q(d)), else a draw from
+ * norm(max(0, p - q)); q_dev is the dense draft distribution (vocab f32). Greedy: accepted iff d is the argmax. */
+int aq_sampler_accept_or_resample(aq_sampler *sp, const float *target_dev, const float *q_dev, uint32_t d,
+                                  int *accepted, uint32_t *tok);
 
 /* ------------------------------------------------------------------------------------ synthetic tensors */
 
@@ -271,6 +308,17 @@ int aq_spec_prefill(aq_state *s, const uint32_t *ids, size_t n, uint32_t *x_t);
  * commit the DeltaNet state of the accepted rows, truncate the KV caches, re-feed the MTP and draft the next k.
  * emitted: capacity k+1; *m = accepted drafts; *n_emitted = m+1. */
 int aq_spec_round(aq_state *s, uint32_t x_p, uint32_t *emitted, uint32_t *n_emitted, uint32_t *m);
+/* The same calls under a sampler (sample.rs; sampler and state on one device, sampler vocabulary = the model's): the
+ * token after the prompt or a forward is `Sampler::sample` of its logits (run.rs's sampled loop; spec.rs:241);
+ * drafts are drawn from the MTP's processed distribution (spec.rs:192-203); a round accepts by the rejection-sampling
+ * rule `accept_or_resample`, the bonus after k acceptances is a draw (spec.rs:367-380). The sampler's random state
+ * advances on the state's stream in the reference's order. A greedy sampler gives the greedy calls. */
+int aq_prefill_sampled(aq_state *s, aq_sampler *sp, const uint32_t *ids, size_t n, float *logits_last_host,
+                       uint32_t *next);
+int aq_forward_token_sampled(aq_state *s, aq_sampler *sp, uint32_t id, float *logits_host, uint32_t *next);
+int aq_spec_prefill_sampled(aq_state *s, aq_sampler *sp, const uint32_t *ids, size_t n, uint32_t *x_t);
+int aq_spec_round_sampled(aq_state *s, aq_sampler *sp, uint32_t x_p, uint32_t *emitted, uint32_t *n_emitted,
+                          uint32_t *m);
 /* `Model::spec_set_drafts` (spec.rs:436) test hook, and the current drafts. */
 int aq_spec_set_drafts(aq_state *s, const uint32_t *d, size_t k);
 int aq_spec_get_drafts(aq_state *s, uint32_t *d, size_t k);

@@ -98,6 +98,31 @@ void or_spec_logits_row(const or_state *s, size_t i, float *out);
 uint32_t or_state_pos(const or_state *s);
 size_t or_state_export(const or_state *s, float *out);
 
+/* ---- the sampler (sample.rs; oracle_sample.c) */
+void or_rng_seed(uint64_t seed, uint64_t s[4]);
+uint64_t or_rng_next(uint64_t s[4]);
+float or_rng_f32(uint64_t s[4]);
+typedef struct or_sampler or_sampler;
+or_sampler *or_sampler_new(const aq_sampler_config *cfg, size_t vocab);
+void or_sampler_free(or_sampler *sp);
+void or_sampler_reseed(or_sampler *sp, uint64_t seed);
+void or_sampler_rng(const or_sampler *sp, uint64_t out[4]);
+int or_sampler_is_greedy(const or_sampler *sp); /* NULL counts as greedy */
+size_t or_sampler_process(or_sampler *sp, const float *logits);
+size_t or_sampler_kept(const or_sampler *sp, uint32_t *ids, float *probs);
+uint32_t or_sampler_draw(or_sampler *sp);
+uint32_t or_sampler_sample(or_sampler *sp, const float *logits);
+void or_sampler_write_dense(const or_sampler *sp, float *out);
+int or_sampler_accept_or_resample(or_sampler *sp, const float *target, const float *q, uint32_t d, uint32_t *tok);
+/* The model calls with a sampler (NULL or temperature <= 0: greedy, as the functions above): run.rs's sampled loop
+ * (prefill / forward_token then Sampler::sample) and spec.rs:229-433 with the rejection-sampling acceptance. */
+uint32_t or_forward_token_s(const or_model *m, or_state *s, or_sampler *sp, uint32_t id, float *logits);
+uint32_t or_prefill_s(const or_model *m, or_state *s, or_sampler *sp, const uint32_t *ids, size_t n,
+                      float *logits_last);
+uint32_t or_spec_prefill_s(const or_model *m, or_state *s, or_sampler *sp, const uint32_t *ids, size_t n);
+uint32_t or_spec_round_s(const or_model *m, or_state *s, or_sampler *sp, uint32_t x_p, uint32_t *emitted,
+                         uint32_t *n_emitted);
+
 /* One mixer / MLP / decoder layer alone (tests/layers.rs:109-271); see oracle_model.c. */
 int or_layer_run(const aq_model_config *cfg, const aq_tensor *ts, size_t n, int kind, const float *x, size_t t,
                  uint32_t start_pos, float *conv, float *rec, float *k_cache, float *v_cache, uint32_t *kv_len,

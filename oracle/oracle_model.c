@@ -65,6 +65,7 @@ struct or_state {
     float *hprev;       /* hidden */
     float *snapshot;
     float *saved_mixed, *saved_a, *saved_b;
+    float *q_dense; /* k x vocab: the dense draft distributions of a sampled round (spec.rs:192-203) */
 };
 
 /* =============================================================================== tensors and matmul */
@@ -307,6 +308,7 @@ or_state *or_state_new(const or_model *m, uint32_t spec_k, uint32_t max_pos) {
         s->saved_mixed = (float *)calloc(n_dn * t * m->cd + 1, sizeof(float));
         s->saved_a = (float *)calloc(n_dn * t * c->dn_n_v_heads + 1, sizeof(float));
         s->saved_b = (float *)calloc(n_dn * t * c->dn_n_v_heads + 1, sizeof(float));
+        s->q_dense = (float *)calloc((size_t)spec_k * c->vocab, sizeof(float));
     }
     return s;
 }
@@ -328,6 +330,7 @@ void or_state_free(or_state *s) {
     free(s->logits);
     free(s->normed);
     free(s->mtp_hout);
+    free(s->q_dense);
     free(s->hprev);
     free(s->snapshot);
     free(s->saved_mixed);
@@ -574,26 +577,32 @@ static void head_rows(const or_model *m, const float *hs, size_t t, float *norme
     matmul(&m->lm_head, normed, t, logits, m->threads);
 }
 
-uint32_t or_forward_token(const or_model *m, or_state *s, uint32_t id, float *logits) {
+/* The next token from a logits row: argmax (greedy), or Sampler::sample (sample.rs:254-257). */
+static uint32_t next_token(const float *lg, size_t vocab, or_sampler *sp) {
+    return or_sampler_is_greedy(sp) ? argmax(lg, vocab) : or_sampler_sample(sp, lg);
+}
+
+uint32_t or_forward_token_s(const or_model *m, or_state *s, or_sampler *sp, uint32_t id, float *logits) {
     size_t h = m->cfg.hidden, vocab = m->cfg.vocab;
     float *hs = forward_rows(m, s, &id, 1, 0);
     float *normed = (float *)malloc(h * sizeof(float));
     float *lg = logits ? logits : (float *)malloc(vocab * sizeof(float));
     head_rows(m, hs, 1, normed, lg);
-    uint32_t a = argmax(lg, vocab);
+    uint32_t a = next_token(lg, vocab, sp);
     if (!logits) free(lg);
     free(normed);
     free(hs);
     return a;
 }
 
-uint32_t or_prefill(const or_model *m, or_state *s, const uint32_t *ids, size_t n, float *logits_last) {
+uint32_t or_prefill_s(const or_model *m, or_state *s, or_sampler *sp, const uint32_t *ids, size_t n,
+                      float *logits_last) {
     size_t h = m->cfg.hidden, vocab = m->cfg.vocab;
     float *hs = forward_rows(m, s, ids, n, 0);
     float *normed = (float *)malloc(h * sizeof(float));
     float *lg = logits_last ? logits_last : (float *)malloc(vocab * sizeof(float));
     head_rows(m, hs + (n - 1) * h, 1, normed, lg);
-    uint32_t a = argmax(lg, vocab);
+    uint32_t a = next_token(lg, vocab, sp);
     if (!logits_last) free(lg);
     free(normed);
     free(hs);
@@ -623,31 +632,39 @@ static void mtp_rows(const or_model *m, or_state *s, const float *cat, size_t t,
     free(y);
 }
 
-/* mtp.rs:130-137 `head_in` + spec.rs:192-203 greedy `draft_token` */
-static uint32_t mtp_draft(const or_model *m, const float *hrow) {
+/* mtp.rs:130-137 `head_in` + spec.rs:192-203 `draft_token`: argmax, or process + draw with the processed
+ * distribution written densely to q_dense[i] for the acceptance rule. */
+static uint32_t mtp_draft(const or_model *m, or_state *s, or_sampler *sp, const float *hrow, size_t i) {
     size_t vocab = m->cfg.vocab;
     float *lg = (float *)malloc(vocab * sizeof(float));
     matmul(&m->lm_head, hrow, 1, lg, m->threads);
-    uint32_t d = argmax(lg, vocab);
+    uint32_t d;
+    if (or_sampler_is_greedy(sp)) {
+        d = argmax(lg, vocab);
+    } else {
+        or_sampler_process(sp, lg);
+        d = or_sampler_draw(sp);
+        or_sampler_write_dense(sp, s->q_dense + i * vocab);
+    }
     free(lg);
     return d;
 }
 
 /* spec.rs:205-222 `chain_drafts`: drafts from..k from the MTP hidden of row `prev` of the last rows. */
-static void chain_drafts(const or_model *m, or_state *s, size_t prev, size_t from) {
+static void chain_drafts(const or_model *m, or_state *s, or_sampler *sp, size_t prev, size_t from) {
     size_t h = m->cfg.hidden;
     float *cat = (float *)malloc(2 * h * sizeof(float));
     for (size_t i = from; i < s->k; i++) {
         memcpy(s->hprev, s->mtp_hout + prev * h, h * sizeof(float));
         mtp_set_row(m, cat, s->drafts[i - 1], s->hprev);
         mtp_rows(m, s, cat, 1, s->mtp_hout);
-        s->drafts[i] = mtp_draft(m, s->mtp_hout);
+        s->drafts[i] = mtp_draft(m, s, sp, s->mtp_hout, i);
         prev = 0;
     }
     free(cat);
 }
 
-uint32_t or_spec_prefill(const or_model *m, or_state *s, const uint32_t *ids, size_t t) {
+uint32_t or_spec_prefill_s(const or_model *m, or_state *s, or_sampler *sp, const uint32_t *ids, size_t t) {
     size_t h = m->cfg.hidden, vocab = m->cfg.vocab;
     uint32_t p = s->pos;
     float *hs = forward_rows(m, s, ids, t, 0);
@@ -656,7 +673,7 @@ uint32_t or_spec_prefill(const or_model *m, or_state *s, const uint32_t *ids, si
     float *lg = (float *)malloc(vocab * sizeof(float));
     float *nl = (float *)malloc(h * sizeof(float));
     head_rows(m, hs + (t - 1) * h, 1, nl, lg); /* logits_of(last row) */
-    uint32_t x_t = argmax(lg, vocab);
+    uint32_t x_t = next_token(lg, vocab, sp);
     /* the MTP over the prompt: row j = (x_{j+1}, h_j), the last row's token is x_T (spec.rs:243-265) */
     if (s->mtp_kv.len > p) s->mtp_kv.len = p;
     float *cats = (float *)malloc(t * 2 * h * sizeof(float));
@@ -664,8 +681,8 @@ uint32_t or_spec_prefill(const or_model *m, or_state *s, const uint32_t *ids, si
     float *hout = (float *)malloc(t * h * sizeof(float));
     mtp_rows(m, s, cats, t, hout);
     memcpy(s->mtp_hout, hout + (t - 1) * h, h * sizeof(float));
-    s->drafts[0] = mtp_draft(m, s->mtp_hout);
-    chain_drafts(m, s, 0, 1);
+    s->drafts[0] = mtp_draft(m, s, sp, s->mtp_hout, 0);
+    chain_drafts(m, s, sp, 0, 1);
     free(hout);
     free(cats);
     free(nl);
@@ -697,7 +714,8 @@ static void restore(const or_model *m, or_state *s) {
     }
 }
 
-uint32_t or_spec_round(const or_model *m, or_state *s, uint32_t x_p, uint32_t *emitted, uint32_t *n_emitted) {
+uint32_t or_spec_round_s(const or_model *m, or_state *s, or_sampler *sp, uint32_t x_p, uint32_t *emitted,
+                         uint32_t *n_emitted) {
     size_t h = m->cfg.hidden, vocab = m->cfg.vocab, k = s->k, t = k + 1;
     size_t nv = m->cfg.dn_n_v_heads, cd = m->cd;
     uint32_t p = s->pos;
@@ -708,15 +726,27 @@ uint32_t or_spec_round(const or_model *m, or_state *s, uint32_t x_p, uint32_t *e
     /* verify (spec.rs:277-314) */
     float *hs = forward_rows(m, s, batch, t, 1);
     head_rows(m, hs, t, s->normed, s->logits);
-    /* accept, greedy (spec.rs:355-366) */
+    /* accept: greedy (spec.rs:355-366) or the rejection-sampling rule (spec.rs:367-380) */
     size_t mm = 0, ne = 0;
-    while (mm < k) {
-        uint32_t a = argmax(s->logits + mm * vocab, vocab);
-        emitted[ne++] = a;
-        if (a != s->drafts[mm]) break;
-        mm++;
+    if (or_sampler_is_greedy(sp)) {
+        while (mm < k) {
+            uint32_t a = argmax(s->logits + mm * vocab, vocab);
+            emitted[ne++] = a;
+            if (a != s->drafts[mm]) break;
+            mm++;
+        }
+        if (mm == k) emitted[ne++] = argmax(s->logits + k * vocab, vocab);
+    } else {
+        while (mm < k) {
+            uint32_t tok;
+            const int ok = or_sampler_accept_or_resample(sp, s->logits + mm * vocab, s->q_dense + mm * vocab,
+                                                         s->drafts[mm], &tok);
+            emitted[ne++] = tok;
+            if (!ok) break;
+            mm++;
+        }
+        if (mm == k) emitted[ne++] = or_sampler_sample(sp, s->logits + k * vocab);
     }
-    if (mm == k) emitted[ne++] = argmax(s->logits + k * vocab, vocab);
     size_t keep = mm + 1;
     *n_emitted = (uint32_t)ne;
     /* roll back (spec.rs:396-415) */
@@ -741,12 +771,25 @@ uint32_t or_spec_round(const or_model *m, or_state *s, uint32_t x_p, uint32_t *e
     float *cats = (float *)malloc(keep * 2 * h * sizeof(float));
     for (size_t i = 0; i < keep; i++) mtp_set_row(m, cats + i * 2 * h, emitted[i], s->normed + i * h);
     mtp_rows(m, s, cats, keep, s->mtp_hout);
-    s->drafts[0] = mtp_draft(m, s->mtp_hout + (keep - 1) * h);
-    chain_drafts(m, s, keep - 1, 1);
+    s->drafts[0] = mtp_draft(m, s, sp, s->mtp_hout + (keep - 1) * h, 0);
+    chain_drafts(m, s, sp, keep - 1, 1);
     free(cats);
     free(hs);
     free(batch);
     return (uint32_t)mm;
+}
+
+uint32_t or_forward_token(const or_model *m, or_state *s, uint32_t id, float *logits) {
+    return or_forward_token_s(m, s, NULL, id, logits);
+}
+uint32_t or_prefill(const or_model *m, or_state *s, const uint32_t *ids, size_t n, float *logits_last) {
+    return or_prefill_s(m, s, NULL, ids, n, logits_last);
+}
+uint32_t or_spec_prefill(const or_model *m, or_state *s, const uint32_t *ids, size_t t) {
+    return or_spec_prefill_s(m, s, NULL, ids, t);
+}
+uint32_t or_spec_round(const or_model *m, or_state *s, uint32_t x_p, uint32_t *emitted, uint32_t *n_emitted) {
+    return or_spec_round_s(m, s, NULL, x_p, emitted, n_emitted);
 }
 
 void or_spec_set_drafts(or_state *s, const uint32_t *d, size_t k) {

@@ -91,6 +91,20 @@ def lib():
         "aq_act_get_q8_0": (i, [P, P, sz]),
         "aq_matmul": (i, [P, P, P, sz, P]),
         "aq_kq_isums": (i, [P, P, P, sz, P, P]),
+        "aq_sampler_new": (i, [P, P, C.c_uint32, C.POINTER(P)]),
+        "aq_sampler_free": (i, [P]),
+        "aq_sampler_reseed": (i, [P, C.c_uint64]),
+        "aq_sampler_get_rng": (i, [P, P]),
+        "aq_sampler_process": (i, [P, P, C.POINTER(C.c_uint32)]),
+        "aq_sampler_kept": (i, [P, P, P, sz, C.POINTER(sz)]),
+        "aq_sampler_draw": (i, [P, C.POINTER(C.c_uint32)]),
+        "aq_sampler_sample": (i, [P, P, C.POINTER(C.c_uint32)]),
+        "aq_sampler_write_dense": (i, [P, P]),
+        "aq_sampler_accept_or_resample": (i, [P, P, P, C.c_uint32, C.POINTER(C.c_int), C.POINTER(C.c_uint32)]),
+        "aq_prefill_sampled": (i, [P, P, P, sz, P, P]),
+        "aq_forward_token_sampled": (i, [P, P, C.c_uint32, P, P]),
+        "aq_spec_prefill_sampled": (i, [P, P, P, sz, P]),
+        "aq_spec_round_sampled": (i, [P, P, C.c_uint32, P, P, P]),
         "aq_set_q8_fine": (i, [i]),
         "aq_q8_fine": (i, []),
         "aq_argmax": (i, [P, P, sz, sz, P]),
@@ -272,6 +286,71 @@ def matmul(ctx: Context, w: Weight, x: Act, ncols, y: DeviceBuffer = None):
     if own:
         y.free()
     return out
+
+
+class AqSamplerConfig(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("seed", C.c_uint64)]
+
+
+def sampler_config(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, seed=0):
+    return AqSamplerConfig(temperature, top_k, top_p, min_p, seed)
+
+
+class Sampler:
+    """aq_sampler: the reference's Sampler (sample.rs:148-303) on the device."""
+
+    def __init__(self, ctx: Context, cfg, vocab):
+        self.ctx, self.cfg, self.vocab = ctx, cfg, vocab
+        h = C.c_void_p()
+        check(lib().aq_sampler_new(ctx.h, C.byref(cfg), vocab, C.byref(h)))
+        self.h = h
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().aq_sampler_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()
+
+    def reseed(self, seed):
+        check(lib().aq_sampler_reseed(self.h, seed))
+
+    def rng(self):
+        out = np.zeros(4, np.uint64)
+        check(lib().aq_sampler_get_rng(self.h, ptr(out)))
+        return out
+
+    def process(self, logits: DeviceBuffer):
+        n = C.c_uint32()
+        check(lib().aq_sampler_process(self.h, logits.p, C.byref(n)))
+        return self.kept()
+
+    def kept(self):
+        n = C.c_size_t()
+        check(lib().aq_sampler_kept(self.h, None, None, 0, C.byref(n)))
+        ids, probs = np.zeros(n.value, np.uint32), np.zeros(n.value, np.float32)
+        check(lib().aq_sampler_kept(self.h, ptr(ids), ptr(probs), n.value, C.byref(n)))
+        return ids, probs
+
+    def draw(self):
+        t = C.c_uint32()
+        check(lib().aq_sampler_draw(self.h, C.byref(t)))
+        return t.value
+
+    def sample(self, logits: DeviceBuffer):
+        t = C.c_uint32()
+        check(lib().aq_sampler_sample(self.h, logits.p, C.byref(t)))
+        return t.value
+
+    def write_dense(self, out: DeviceBuffer):
+        check(lib().aq_sampler_write_dense(self.h, out.p))
+
+    def accept_or_resample(self, target: DeviceBuffer, q: DeviceBuffer, d):
+        ok, t = C.c_int(), C.c_uint32()
+        check(lib().aq_sampler_accept_or_resample(self.h, target.p, q.p, d, C.byref(ok), C.byref(t)))
+        return bool(ok.value), t.value
 
 
 class q8_fine:
@@ -462,29 +541,41 @@ class State:
         check(lib().aq_state_pos(self.h, C.byref(p)))
         return p.value
 
-    def forward_token(self, tok, want_logits=False):
+    def forward_token(self, tok, want_logits=False, sampler=None):
         lg = np.zeros(self.model.cfg.vocab, np.float32) if want_logits else None
         a = C.c_uint32()
-        check(lib().aq_forward_token(self.h, tok, ptr(lg), C.byref(a)))
+        if sampler is None:
+            check(lib().aq_forward_token(self.h, tok, ptr(lg), C.byref(a)))
+        else:
+            check(lib().aq_forward_token_sampled(self.h, sampler.h, tok, ptr(lg), C.byref(a)))
         return (a.value, lg) if want_logits else a.value
 
-    def prefill(self, ids, want_logits=False):
+    def prefill(self, ids, want_logits=False, sampler=None):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         lg = np.zeros(self.model.cfg.vocab, np.float32) if want_logits else None
         a = C.c_uint32()
-        check(lib().aq_prefill(self.h, ptr(ids), ids.size, ptr(lg), C.byref(a)))
+        if sampler is None:
+            check(lib().aq_prefill(self.h, ptr(ids), ids.size, ptr(lg), C.byref(a)))
+        else:
+            check(lib().aq_prefill_sampled(self.h, sampler.h, ptr(ids), ids.size, ptr(lg), C.byref(a)))
         return (a.value, lg) if want_logits else a.value
 
-    def spec_prefill(self, ids):
+    def spec_prefill(self, ids, sampler=None):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         x = C.c_uint32()
-        check(lib().aq_spec_prefill(self.h, ptr(ids), ids.size, C.byref(x)))
+        if sampler is None:
+            check(lib().aq_spec_prefill(self.h, ptr(ids), ids.size, C.byref(x)))
+        else:
+            check(lib().aq_spec_prefill_sampled(self.h, sampler.h, ptr(ids), ids.size, C.byref(x)))
         return x.value
 
-    def spec_round(self, x_p):
+    def spec_round(self, x_p, sampler=None):
         em = np.zeros(self.k + 1, np.uint32)
         n, m = C.c_uint32(), C.c_uint32()
-        check(lib().aq_spec_round(self.h, x_p, ptr(em), C.byref(n), C.byref(m)))
+        if sampler is None:
+            check(lib().aq_spec_round(self.h, x_p, ptr(em), C.byref(n), C.byref(m)))
+        else:
+            check(lib().aq_spec_round_sampled(self.h, sampler.h, x_p, ptr(em), C.byref(n), C.byref(m)))
         return m.value, em[: n.value].tolist()
 
     def set_drafts(self, d):

@@ -417,6 +417,9 @@ struct aq_state {
     float *attn_sc = nullptr; // attention score rows [T][n_head][attn_sc_stride], when contexts outgrow the LDS
     size_t attn_sc_stride = 0;
     uint32_t *pinned = nullptr; // host, 64 words
+    aq_sampler *sp = nullptr;   // the sampler of the running sampled call (null: greedy)
+    float *q_dense = nullptr;   // k x vocab: each draft's dense distribution (sampled rounds)
+    uint32_t *q_idx = nullptr, *q_n = nullptr; // the ids last written into each q_dense row, and their count
     aq::DnArgs *commit_args = nullptr; // device: the commit's DnArgs per DeltaNet slot, for par = 0 then par = 1
     int n_dn = 0;
     bool spec_ready = false;
@@ -741,10 +744,20 @@ int mtp_rows(aq_state *s, size_t t) {
 // mtp.rs:130-137 `head_in` + spec.rs:192-203: draft = argmax(lm_head(hout row `row`)) into drafts[i].
 int mtp_draft(aq_state *s, size_t row, size_t i) {
     aq_model *m = s->m;
+    const size_t vocab = m->cfg.vocab;
     Act v = col_view(s->act_h, row);
     int rc = mm(s, m->lm_head, v, 1, s->logits);
-    if (!rc) rc = launch_argmax(s->logits, m->cfg.vocab, m->cfg.vocab, 1, s->drafts + i, s->amax_scratch, s->stream);
-    return rc;
+    if (rc) return rc;
+    if (sampler_greedy(s->sp)) return launch_argmax(s->logits, vocab, vocab, 1, s->drafts + i, s->amax_scratch, s->stream);
+    return sampler_draft(s->sp, s->logits, s->drafts + i, s->q_dense + i * vocab, s->q_idx + i * vocab, s->q_n + i,
+                         s->stream);
+}
+
+// The next token from one logits row: argmax (model.rs:505-513), or Sampler::sample under a sampler.
+int next_token(aq_state *s, const float *logits, uint32_t *tok_dev) {
+    const size_t vocab = s->m->cfg.vocab;
+    if (sampler_greedy(s->sp)) return launch_argmax(logits, vocab, vocab, 1, tok_dev, s->amax_scratch, s->stream);
+    return sampler_sample(s->sp, logits, tok_dev, s->stream);
 }
 
 // spec.rs:205-222 `chain_drafts`: drafts from..k-1, each from the previous draft and the MTP hidden row `prev`.
@@ -790,8 +803,7 @@ int run_prompt(aq_state *s, const uint32_t *ids, size_t n) {
         if (c0 + tc == n) {
             Act v = col_view(s->act_h, tc - 1);
             if ((rc = mm(s, m->lm_head, v, 1, s->logits))) return rc;
-            if ((rc = launch_argmax(s->logits, m->cfg.vocab, m->cfg.vocab, 1, s->amax, s->amax_scratch, s->stream)))
-                return rc;
+            if ((rc = next_token(s, s->logits, s->amax))) return rc;
         }
     }
     return 0;
@@ -974,6 +986,11 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
     AQ_S(dalloc_t(s, T, &s->drafts));
     AQ_S(dalloc_t(s, T, &s->emitted));
     AQ_S(dalloc_t(s, 8, &s->info));
+    if (spec_k > 0) {
+        AQ_S(dalloc_t(s, (size_t)spec_k * c.vocab, &s->q_dense));
+        AQ_S(dalloc_t(s, (size_t)spec_k * c.vocab, &s->q_idx));
+        AQ_S(dalloc_t(s, (size_t)spec_k, &s->q_n));
+    }
     AQ_S(dalloc_t(s, s->max_pos, &s->prompt));
     AQ_S(dalloc_t(s, s->max_pos, &s->shifted));
     AQ_S(dalloc(s, argmax_scratch_bytes(c.vocab, T), &s->amax_scratch));
@@ -1075,7 +1092,7 @@ int aq_forward_token(aq_state *s, uint32_t id, float *logits_host, uint32_t *arg
     int rc = copy_ids_in(s, s->ids, s->pinned + 8, 1);
     if (!rc) rc = forward_rows(s, s->ids, 1, PLAIN);
     if (!rc) rc = head_rows(s, s->xa, 1, s->normed);
-    if (!rc) rc = launch_argmax(s->logits, vocab, vocab, 1, s->amax, s->amax_scratch, s->stream);
+    if (!rc) rc = next_token(s, s->logits, s->amax);
     if (rc) return rc;
     if (logits_host) AQ_HIP(hipMemcpyAsync(logits_host, s->logits, vocab * 4, hipMemcpyDeviceToHost, s->stream));
     rc = sync_in(s, s->pinned, s->amax, 4);
@@ -1129,9 +1146,13 @@ int aq_spec_round(aq_state *s, uint32_t x_p, uint32_t *emitted, uint32_t *n_emit
     if ((rc = launch_make_batch(x_p, s->drafts, (int)k, s->ids, s->stream))) return rc;
     if ((rc = forward_rows(s, s->ids, t, VERIFY))) return rc;
     if ((rc = head_rows(s, s->xa, t, s->normed))) return rc;
-    if ((rc = launch_argmax(s->logits, vocab, vocab, t, s->amax, s->amax_scratch, s->stream))) return rc;
-    // accept on the device (spec.rs:355-366)
-    if ((rc = launch_accept(s->amax, s->drafts, (int)k, s->emitted, s->info, s->stream))) return rc;
+    if (sampler_greedy(s->sp)) { // accept on the device (spec.rs:355-366)
+        if ((rc = launch_argmax(s->logits, vocab, vocab, t, s->amax, s->amax_scratch, s->stream))) return rc;
+        if ((rc = launch_accept(s->amax, s->drafts, (int)k, s->emitted, s->info, s->stream))) return rc;
+    } else { // the rejection-sampling rule (spec.rs:367-380)
+        if ((rc = sampler_round(s->sp, s->logits, (int)k, s->drafts, s->q_dense, s->emitted, s->info, s->stream)))
+            return rc;
+    }
     AQ_HIP(hipMemcpyAsync(s->pinned, s->info, 3 * 4, hipMemcpyDeviceToHost, s->stream));
     AQ_HIP(hipMemcpyAsync(s->pinned + 16, s->emitted, t * 4, hipMemcpyDeviceToHost, s->stream));
     AQ_HIP(hipEventRecord(s->ev[1], s->stream));
@@ -1177,6 +1198,55 @@ int aq_spec_round(aq_state *s, uint32_t x_p, uint32_t *emitted, uint32_t *n_emit
     s->stats.verify_ms += vms;
     (void)h;
     return 0;
+}
+
+// ---------------------------------------------------------------------------------------- sampled calls
+// The calls above with a sampler in place of argmax: the token after the prompt / after a forward is
+// Sampler::sample of its logits (run.rs's sampled loop), drafts are drawn from the MTP's processed distribution, and
+// a round accepts by the rejection-sampling rule (spec.rs:192-203, 241, 367-380). A greedy sampler (temperature <= 0)
+// gives the greedy calls exactly, drawing nothing.
+namespace {
+struct SamplerScope {
+    aq_state *s;
+    SamplerScope(aq_state *st, aq_sampler *sp) : s(st) { s->sp = sp; }
+    ~SamplerScope() { s->sp = nullptr; }
+};
+int check_sampler(aq_state *s, aq_sampler *sp, const char *fn) {
+    AQ_REQUIRE(s && sp, std::string(fn) + ": null argument");
+    AQ_REQUIRE(sampler_vocab(sp) == s->m->cfg.vocab, std::string(fn) + ": sampler vocabulary != model vocabulary");
+    AQ_REQUIRE(sampler_device(sp) == s->device, std::string(fn) + ": sampler and state on different devices");
+    return 0;
+}
+} // namespace
+
+int aq_prefill_sampled(aq_state *s, aq_sampler *sp, const uint32_t *ids, size_t n, float *logits_last_host,
+                       uint32_t *next) {
+    int rc = check_sampler(s, sp, "aq_prefill_sampled");
+    if (rc) return rc;
+    SamplerScope g(s, sp);
+    return aq_prefill(s, ids, n, logits_last_host, next);
+}
+
+int aq_forward_token_sampled(aq_state *s, aq_sampler *sp, uint32_t id, float *logits_host, uint32_t *next) {
+    int rc = check_sampler(s, sp, "aq_forward_token_sampled");
+    if (rc) return rc;
+    SamplerScope g(s, sp);
+    return aq_forward_token(s, id, logits_host, next);
+}
+
+int aq_spec_prefill_sampled(aq_state *s, aq_sampler *sp, const uint32_t *ids, size_t n, uint32_t *x_t) {
+    int rc = check_sampler(s, sp, "aq_spec_prefill_sampled");
+    if (rc) return rc;
+    SamplerScope g(s, sp);
+    return aq_spec_prefill(s, ids, n, x_t);
+}
+
+int aq_spec_round_sampled(aq_state *s, aq_sampler *sp, uint32_t x_p, uint32_t *emitted, uint32_t *n_emitted,
+                          uint32_t *m_out) {
+    int rc = check_sampler(s, sp, "aq_spec_round_sampled");
+    if (rc) return rc;
+    SamplerScope g(s, sp);
+    return aq_spec_round(s, x_p, emitted, n_emitted, m_out);
 }
 
 int aq_spec_set_drafts(aq_state *s, const uint32_t *d, size_t k) {

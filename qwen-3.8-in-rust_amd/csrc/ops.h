@@ -97,6 +97,21 @@ int launch_attention(const AttnArgs &a, hipStream_t stream);
 size_t argmax_scratch_bytes(size_t n, size_t t);
 int launch_argmax(const float *x, size_t n, size_t stride, size_t t, uint32_t *ids, void *scratch, hipStream_t stream);
 
+// The sampler (sample.hip) for the model's sampled calls; `sp` null or temperature <= 0 is greedy.
+bool sampler_greedy(const aq_sampler *sp);
+uint32_t sampler_vocab(const aq_sampler *sp);
+int sampler_device(const aq_sampler *sp);
+// Sampler::sample of one logits row into *tok_dev (sample.rs:254-257).
+int sampler_sample(aq_sampler *sp, const float *logits, uint32_t *tok_dev, hipStream_t st);
+// A draft (spec.rs:192-203): process + draw into *tok_dev, the kept set written densely into q_dense (vocab f32),
+// whose previously written ids (q_idx, *q_n of them) are cleared first.
+int sampler_draft(aq_sampler *sp, const float *logits, uint32_t *tok_dev, float *q_dense, uint32_t *q_idx,
+                  uint32_t *q_n, hipStream_t st);
+// The sampled acceptance of a round (spec.rs:367-380) over k + 1 logits rows: info = {m, n_emitted, keep} and
+// emitted[0..n_emitted), as launch_accept.
+int sampler_round(aq_sampler *sp, const float *logits, int k, const uint32_t *drafts, const float *q_dense,
+                  uint32_t *emitted, uint32_t *info, hipStream_t st);
+
 // Greedy acceptance (spec.rs:355-366): info = {m, n_emitted, keep}, emitted[0..n_emitted).
 int launch_accept(const uint32_t *argmax_ids, const uint32_t *drafts, int k, uint32_t *emitted, uint32_t *info,
                   hipStream_t stream);

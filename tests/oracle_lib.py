@@ -115,6 +115,24 @@ def lib():
         "or_spec_prefill": (C.c_uint32, [P, P, P, sz]),
         "or_spec_round": (C.c_uint32, [P, P, C.c_uint32, P, P]),
         "or_spec_set_drafts": (None, [P, P, sz]),
+        "or_forward_token_s": (C.c_uint32, [P, P, P, C.c_uint32, P]),
+        "or_prefill_s": (C.c_uint32, [P, P, P, P, sz, P]),
+        "or_spec_prefill_s": (C.c_uint32, [P, P, P, P, sz]),
+        "or_spec_round_s": (C.c_uint32, [P, P, P, C.c_uint32, P, P]),
+        "or_rng_seed": (None, [C.c_uint64, P]),
+        "or_rng_next": (C.c_uint64, [P]),
+        "or_rng_f32": (C.c_float, [P]),
+        "or_sampler_new": (P, [P, sz]),
+        "or_sampler_free": (None, [P]),
+        "or_sampler_reseed": (None, [P, C.c_uint64]),
+        "or_sampler_rng": (None, [P, P]),
+        "or_sampler_is_greedy": (C.c_int, [P]),
+        "or_sampler_process": (sz, [P, P]),
+        "or_sampler_kept": (sz, [P, P, P]),
+        "or_sampler_draw": (C.c_uint32, [P]),
+        "or_sampler_sample": (C.c_uint32, [P, P]),
+        "or_sampler_write_dense": (None, [P, P]),
+        "or_sampler_accept_or_resample": (C.c_int, [P, P, P, C.c_uint32, P]),
         "or_spec_get_drafts": (None, [P, P]),
         "or_spec_logits_row": (None, [P, sz, P]),
         "or_state_pos": (C.c_uint32, [P]),
@@ -227,6 +245,77 @@ class Model:
             self.h = None
 
 
+class AqSamplerConfig(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("seed", C.c_uint64)]
+
+
+def sampler_config(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, seed=0):
+    return AqSamplerConfig(temperature, top_k, top_p, min_p, seed)
+
+
+class Sampler:
+    """The oracle's Sampler (sample.rs:148-303)."""
+
+    def __init__(self, cfg, vocab):
+        self.vocab = vocab
+        self.cfg = cfg
+        self.h = lib().or_sampler_new(C.byref(cfg), vocab)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_sampler_free(self.h)
+            self.h = None
+
+    def reseed(self, seed):
+        lib().or_sampler_reseed(self.h, seed)
+
+    def rng(self):
+        out = np.zeros(4, np.uint64)
+        lib().or_sampler_rng(self.h, ptr(out))
+        return out
+
+    def process(self, logits):
+        logits = np.ascontiguousarray(logits, np.float32)
+        n = lib().or_sampler_process(self.h, ptr(logits))
+        ids, probs = np.zeros(n, np.uint32), np.zeros(n, np.float32)
+        lib().or_sampler_kept(self.h, ptr(ids), ptr(probs))
+        return ids, probs
+
+    def kept(self):
+        n = lib().or_sampler_kept(self.h, None, None)
+        ids, probs = np.zeros(n, np.uint32), np.zeros(n, np.float32)
+        lib().or_sampler_kept(self.h, ptr(ids), ptr(probs))
+        return ids, probs
+
+    def draw(self):
+        return lib().or_sampler_draw(self.h)
+
+    def sample(self, logits):
+        return lib().or_sampler_sample(self.h, ptr(np.ascontiguousarray(logits, np.float32)))
+
+    def write_dense(self):
+        out = np.zeros(self.vocab, np.float32)
+        lib().or_sampler_write_dense(self.h, ptr(out))
+        return out
+
+    def accept_or_resample(self, target, q, d):
+        tok = C.c_uint32(0)
+        ok = lib().or_sampler_accept_or_resample(self.h, ptr(np.ascontiguousarray(target, np.float32)),
+                                                 ptr(np.ascontiguousarray(q, np.float32)), d, C.byref(tok))
+        return bool(ok), tok.value
+
+
+def rng_seed(seed):
+    s = np.zeros(4, np.uint64)
+    lib().or_rng_seed(seed, ptr(s))
+    return s
+
+
+def _sp(sampler):
+    return None if sampler is None else sampler.h
+
+
 class State:
     def __init__(self, model: Model, spec_k=0, max_pos=512):
         self.model = model
@@ -242,25 +331,25 @@ class State:
     def pos(self):
         return lib().or_state_pos(self.h)
 
-    def forward_token(self, tok, want_logits=False):
+    def forward_token(self, tok, want_logits=False, sampler=None):
         lg = np.zeros(self.model.cfg.vocab, np.float32) if want_logits else None
-        a = lib().or_forward_token(self.model.h, self.h, tok, ptr(lg))
+        a = lib().or_forward_token_s(self.model.h, self.h, _sp(sampler), tok, ptr(lg))
         return (a, lg) if want_logits else a
 
-    def prefill(self, ids, want_logits=False):
+    def prefill(self, ids, want_logits=False, sampler=None):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         lg = np.zeros(self.model.cfg.vocab, np.float32) if want_logits else None
-        a = lib().or_prefill(self.model.h, self.h, ptr(ids), ids.size, ptr(lg))
+        a = lib().or_prefill_s(self.model.h, self.h, _sp(sampler), ptr(ids), ids.size, ptr(lg))
         return (a, lg) if want_logits else a
 
-    def spec_prefill(self, ids):
+    def spec_prefill(self, ids, sampler=None):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
-        return lib().or_spec_prefill(self.model.h, self.h, ptr(ids), ids.size)
+        return lib().or_spec_prefill_s(self.model.h, self.h, _sp(sampler), ptr(ids), ids.size)
 
-    def spec_round(self, x_p):
+    def spec_round(self, x_p, sampler=None):
         em = np.zeros(self.k + 1, np.uint32)
         n = C.c_uint32(0)
-        m = lib().or_spec_round(self.model.h, self.h, x_p, ptr(em), C.byref(n))
+        m = lib().or_spec_round_s(self.model.h, self.h, _sp(sampler), x_p, ptr(em), C.byref(n))
         return m, em[: n.value].tolist()
 
     def set_drafts(self, d):
