@@ -9,12 +9,21 @@ re-feed the MTP and draft k tokens). `value` = emitted tokens / wall time of the
 
 Printed as one JSON line, with
   roofline      the dominant kernel (the K-quant verify matmul: Q4_K 17408 x 5120 at N = k+1 = 4, the FFN gate/up
-                shape that carries 38% of the weight bytes) timed with HIP events on its stream, against 8 TB/s;
+                shape that carries 38% of the weight bytes) timed with HIP events on its stream, against 8 TB/s: the
+                mean over 1000 back-to-back launches (achieved) and the median of 400 single-launch times;
   kernels       the matvec (N = 1) and the blocked verify op (N = 2, 4, 6, 8) on the single-op shapes (Q4_K
-                17408 x 5120, Q6_K 5120 x 17408) and the lm_head matvec (Q6_K 248320 x 5120), GB/s and fraction of
-                8 TB/s per launch;
-  cpu_baseline  the CPU oracle (a C restatement of the reference's CPU path) on the box's host cores, on a bounded
-                sample of the same workload (a short prompt, then --spec 3 rounds for ~20 s);
+                17408 x 5120, Q6_K 5120 x 17408) and the lm_head matvec (Q6_K 248320 x 5120), mean and median
+                per-launch time, GB/s and fraction of 8 TB/s;
+  forced        the same rounds with the drafts set to the greedy continuation (spec_set_drafts, the reference's
+                rollback-test hook) so that a chosen number m of them is accepted: tokens/s at full acceptance and
+                at the reference's measured mean (about 2 of 3 accepted per round at k = 3 on real weights,
+                docs/spec.md:140-142), and the round time by m. Random-init weights make the MTP accept almost
+                nothing, so `value` is near one token per round; these show what the round delivers when drafts land;
+  sustained     --spec 3 rounds kept running for --sustain-seconds after the timed ones (the GPU busy long enough to
+                be seen by a utilisation sampler), tokens/s over that stretch;
+  cpu_baseline  the CPU oracle (a scalar C restatement of the reference's CPU path, not its hand-written AVX2
+                kernels) on the box's physical cores (at most 16, the box's share): config 4's 64-token prompt, then
+                --spec 3 rounds for --cpu-seconds, plus its matvec / verify GB/s at the config-2/3 shapes;
 and the per-round byte model (weights read once + DeltaNet state + KV + MTP) as round_roofline.
 """
 import argparse
@@ -42,6 +51,8 @@ def parse():
     ap.add_argument("--prompt", type=int, default=64)
     ap.add_argument("--plain-tokens", type=int, default=64, help="plain greedy tokens timed for comparison")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--sustain-seconds", type=float, default=15.0)
+    ap.add_argument("--forced-rounds", type=int, default=48)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel timing (for counter runs)")
     return ap.parse_args()
@@ -53,7 +64,8 @@ def log(msg):
 
 def kernel_roofline(ctx, k):
     """The verify matmul (Q4_K 17408 x 5120, N = k+1 columns) over 8 distinct weights (400 MB, beyond the MALL),
-    timed with HIP events on the context stream. Algorithmic bytes per launch: W + N*x + N*y."""
+    timed with HIP events on the context stream after a warm-up: the mean of 1000 back-to-back launches, and the
+    median of 400 single-launch times. Algorithmic bytes per launch: W + N*x + N*y."""
     rows, cols, n = 17408, 5120, k + 1
     ws = [aq.SynthWeight(ctx, aq.synth_spec(aq.Q4_K, rows, cols, seed=SEED + 100 + i)) for i in range(8)]
     x = np.random.default_rng(1).standard_normal((n, cols)).astype(np.float32)
@@ -61,14 +73,17 @@ def kernel_roofline(ctx, k):
     act.set(x)
     act.quantize(aq.Q4_K, n)
     y = aq.DeviceBuffer(ctx, n * rows * 4)
-    aq.matmul_time(ctx, ws, act, n, y, 32)
-    us = aq.matmul_time(ctx, ws, act, n, y, 400)
+    aq.matmul_time(ctx, ws, act, n, y, 400)
+    us = aq.matmul_time(ctx, ws, act, n, y, 1000)
+    each = aq.matmul_time_each(ctx, ws, act, n, y, 400)
     wbytes = rows * aq.row_bytes(aq.Q4_K, cols)
     traffic_alg = wbytes + n * (cols // 256) * 292 + n * rows * 4
     achieved = traffic_alg / (us * 1e-6) / 1e9
     for w in ws:
         w.free()
     return {"kernel": f"kq_wave_kernel Q4_K {rows}x{cols} N={n}", "us_per_launch": round(us, 3),
+            "median_us": round(float(np.median(each)), 3),
+            "p10_p90_us": [round(float(np.percentile(each, 10)), 3), round(float(np.percentile(each, 90)), 3)],
             "bytes_per_launch": traffic_alg, "achieved_GBs": achieved}
 
 
@@ -88,14 +103,15 @@ def kernel_sweep(ctx):
             act.set(x)
             act.quantize(t, n)
             y = aq.DeviceBuffer(ctx, n * rows * 4)
-            reps = 200 if nw > 1 else 20
-            aq.matmul_time(ctx, ws, act, n, y, reps // 8)
+            reps = 200 if nw > 1 else 50
+            aq.matmul_time(ctx, ws, act, n, y, reps // 4)
             us = aq.matmul_time(ctx, ws, act, n, y, reps)
+            med = float(np.median(aq.matmul_time_each(ctx, ws, act, n, y, max(64, reps // 2))))
             nbytes = wbytes + n * (cols // 256) * 292 + n * rows * 4
             gbs = nbytes / (us * 1e-6) / 1e9
             name = {aq.Q4_K: "Q4_K", aq.Q6_K: "Q6_K"}[t]
             out.append({"kernel": f"{name} {rows}x{cols}", "n": n, "us_per_launch": round(us, 2),
-                        "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+                        "median_us": round(med, 2), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
             y.free()
             act.free()
         for w in ws:
@@ -129,44 +145,128 @@ def round_bytes(cfg, mb, k, ctx_len):
     return mb["main"] + 3 * rec + 3 * conv + kv + mtp
 
 
-def cpu_baseline(cfg, plan, k, seconds, gpu_model):
-    """The CPU oracle on the same synthetic 27B model: a 4-token prompt, then --spec k rounds until `seconds` of
-    rounds have run. Also checks that the device emits the same ids for the same prompt."""
+def cpu_info():
+    """The host's CPU model, the CPUs this process may use, and how many physical cores those are (/proc/cpuinfo)."""
+    allowed = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    model, core_of, cur = None, {}, {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if ":" not in line:
+                if "processor" in cur:
+                    core_of[int(cur["processor"])] = (cur.get("physical id", "0"), cur.get("core id", cur["processor"]))
+                cur = {}
+                continue
+            key, val = (x.strip() for x in line.split(":", 1))
+            cur[key] = val
+            if key == "model name" and model is None:
+                model = val
+        if "processor" in cur:
+            core_of[int(cur["processor"])] = (cur.get("physical id", "0"), cur.get("core id", cur["processor"]))
+    except OSError:
+        pass
+    phys = len({core_of[c] for c in allowed if c in core_of}) or len(allowed)
+    return {"model": model, "logical_cpus": os.cpu_count(), "nproc": len(allowed), "physical_cores": phys}
+
+
+def cpu_matmul_gbs(O, threads):
+    """The oracle's matvec (N = 1, config 2) and verify op (N = 4, config 3 at k = 3) on the two single-op shapes:
+    weight GB/s (W bytes / time per call), each timed over >= 1 s."""
+    out = []
+    for t, rows, cols in [(aq.Q4_K, 17408, 5120), (aq.Q6_K, 5120, 17408)]:
+        host = aq.synth_host(aq.synth_spec(t, rows, cols, seed=SEED + 300), threads).view(np.uint8)
+        wbytes = rows * aq.row_bytes(t, cols)
+        x = np.random.default_rng(3).standard_normal((4, cols)).astype(np.float32)
+        for n in (1, 4):
+            O.matmul(t, host, rows, cols, x[:n], threads=threads)
+            reps, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < 1.0 or reps < 2:
+                O.matmul(t, host, rows, cols, x[:n], threads=threads)
+                reps += 1
+            dt = (time.perf_counter() - t0) / reps
+            name = {aq.Q4_K: "Q4_K", aq.Q6_K: "Q6_K"}[t]
+            out.append({"kernel": f"{name} {rows}x{cols}", "n": n, "ms_per_call": round(dt * 1e3, 2),
+                        "weight_GBs": round(wbytes / dt / 1e9, 2)})
+    return out
+
+
+def cpu_baseline(cfg, plan, k, seconds, gpu_model, prompt):
+    """The CPU oracle on the same synthetic 27B model and config 4's prompt: the prefill, then --spec k rounds until
+    `seconds` of rounds have run (tokens/s over the rounds). Also checks that the device emits the same ids for the
+    same prompt over those rounds, and times the oracle's matvec / verify op alone."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O  # the checker / CPU baseline only
 
-    threads = min(16, os.cpu_count() or 1)
+    info = cpu_info()
+    threads = max(1, min(16, info["physical_cores"]))  # cpu.rs:1-12 uses the physical cores; the box's share is 16
     t0 = time.time()
     tensors = aq.plan_tensors(plan, threads)
-    log(f"cpu baseline: host tensors generated in {time.time() - t0:.1f} s")
+    log(f"cpu baseline: {info}; host tensors generated in {time.time() - t0:.1f} s")
     ocfg = O.AqModelConfig()
     for name, _ in O.AqModelConfig._fields_:
         setattr(ocfg, name, getattr(cfg, name))
     om = O.Model(ocfg, tensors, threads=threads)
-    prompt = np.random.default_rng(SEED + 1).integers(0, cfg.vocab, 4).astype(np.uint32)
-    st = O.State(om, k, 64)
+    st = O.State(om, k, len(prompt) + 256)
+    t0 = time.time()
     out = [st.spec_prefill(prompt)]
+    prefill_s = time.time() - t0
+    log(f"cpu baseline: {len(prompt)}-token spec prefill in {prefill_s:.1f} s")
     rounds, emitted, t_rounds = 0, 0, 0.0
-    while t_rounds < seconds or rounds < 2:
+    while (t_rounds < seconds or rounds < 2) and rounds < 40:
         t1 = time.time()
         m, em = st.spec_round(out[-1])
         t_rounds += time.time() - t1
         out += em
         rounds += 1
         emitted += len(em)
-        if rounds >= 32:
-            break
     log(f"cpu baseline: {rounds} rounds, {emitted} tokens in {t_rounds:.1f} s")
-    gs = aq.State(gpu_model, k, 64)
+    gs = aq.State(gpu_model, k, len(prompt) + 256)
     gout = [gs.spec_prefill(prompt)]
     while len(gout) < len(out):
         _, em = gs.spec_round(gout[-1])
         gout += em
     match = gout[: len(out)] == out
     del st, om, tensors
-    return {"value": emitted / t_rounds, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"27B-shape Q4_K_M, 4-token prompt, {rounds} greedy --spec {k} rounds ({emitted} tokens) on "
-                      f"the C oracle with {threads} threads", "ids_match_device": bool(match)}
+    mm = cpu_matmul_gbs(O, threads)
+    return {"value": round(emitted / t_rounds, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"27B-shape Q4_K_M, {len(prompt)}-token prompt (spec prefill {prefill_s:.1f} s, not in the "
+                      f"rate), then {rounds} greedy --spec {k} rounds ({emitted} tokens, {t_rounds:.1f} s) on the "
+                      f"scalar C restatement of the reference's CPU path (not its hand-written AVX2 kernels), "
+                      f"{threads} threads on physical cores",
+            "cpu": info, "prefill_s": round(prefill_s, 2), "matmul": mm, "ids_match_device": bool(match)}
+
+
+def forced_rounds(model, prompt, plain, k, n_rounds, max_pos):
+    """Rounds whose drafts are set to the greedy continuation `plain` with draft m+1 corrupted, so exactly m are
+    accepted (the reference's spec_identity.rs:136-170 technique). Every round's emitted ids are checked against
+    `plain`. Returns tokens/s at m = k every round and under the schedule 3,2,3,1,2,0,3,2 (mean 2.0 accepted), and
+    the mean round time for each m."""
+    vocab = model.cfg.vocab
+    res, by_m = {}, {m: [] for m in range(k + 1)}
+    for name, sched in (("full_acceptance", [k]), ("reference_mean", [min(m, k) for m in (3, 2, 3, 1, 2, 0, 3, 2)])):
+        st = aq.State(model, k, max_pos)
+        out = [st.spec_prefill(prompt)]
+        assert out[0] == plain[0]
+        emitted, dt, ok = 0, 0.0, True
+        for r in range(n_rounds):
+            m = sched[r % len(sched)]
+            j = len(out)
+            d = [plain[j + i] if i != m else (plain[j + i] + 1) % vocab for i in range(k)]
+            st.set_drafts(d)
+            t1 = time.perf_counter()
+            mm, em = st.spec_round(out[-1])
+            st.drafts()  # waits for the round's tail (commit, MTP re-feed, next drafts)
+            t = time.perf_counter() - t1
+            ok = ok and mm == m and em == plain[j:j + len(em)]
+            if r >= 4:  # the first rounds warm up
+                dt += t
+                emitted += len(em)
+                by_m[m].append(t * 1e3)
+            out += em
+        res[name] = {"tokens_per_s": round(emitted / dt, 3), "tokens_per_round": round(emitted / (n_rounds - 4), 3),
+                     "ids_equal_plain": bool(ok)}
+        st.free()
+    res["round_ms_by_m"] = {m: round(float(np.median(v)), 3) for m, v in by_m.items() if v}
+    return res
 
 
 def main():
@@ -178,8 +278,8 @@ def main():
         sys.exit(2)
     ctx = aq.Context(0)
     k = a.spec
+    ks = kernel_sweep(ctx) if not a.kernel_only else None  # also brings the clocks up before the roofline timing
     kr = kernel_roofline(ctx, k)
-    ks = kernel_sweep(ctx) if not a.kernel_only else None
     if a.kernel_only:  # the counter runs: the dominant kernel plus a plain device copy of known size
         nbytes = 512 << 20
         src, dst = aq.DeviceBuffer(ctx, nbytes), aq.DeviceBuffer(ctx, nbytes)
@@ -194,7 +294,8 @@ def main():
     mb = model.bytes()
     log(f"27B model generated in HBM in {time.time() - t0:.1f} s: {mb}")
     prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, a.prompt).astype(np.uint32)
-    max_pos = a.prompt + (k + 1) * (a.warmup + a.steps) + a.plain_tokens + 64
+    max_pos = (a.prompt + (k + 1) * (a.warmup + a.steps + 2 * a.forced_rounds) + a.plain_tokens + 64 +
+               int(400 * a.sustain_seconds))
 
     # plain greedy decode (reported beside the speculative number)
     ps = aq.State(model, 0, max_pos)
@@ -208,6 +309,8 @@ def main():
     ctx.sync()
     plain_tps = a.plain_tokens / (time.perf_counter() - t1)
     log(f"plain: {plain_tps:.2f} tokens/s")
+    while len(plain) < (k + 1) * 2 * a.forced_rounds + 8:  # the greedy continuation the forced rounds draft from
+        plain.append(ps.forward_token(plain[-1]))
 
     # greedy --spec k
     ss = aq.State(model, k, max_pos)
@@ -238,6 +341,18 @@ def main():
 
     ctx_len = a.prompt + len(out)
     rb = round_bytes(cfg, mb, k, ctx_len)
+    forced = forced_rounds(model, prompt, plain, k, a.forced_rounds, max_pos)
+    log(f"forced: {forced}")
+    # the GPU kept busy for a while longer (rounds continue from the same state)
+    sus_tokens, sus_rounds, t1 = 0, 0, time.perf_counter()
+    while time.perf_counter() - t1 < a.sustain_seconds:
+        _, em = ss.spec_round(out[-1])
+        out += em
+        sus_tokens += len(em)
+        sus_rounds += 1
+    ctx.sync()
+    sus_dt = time.perf_counter() - t1
+    log(f"sustained: {sus_rounds} rounds, {sus_tokens / max(sus_dt, 1e-9):.2f} tokens/s")
     result = {
         "metric": "tokens/s, 27B-shape Q4_K_M greedy --spec 3; verify-kernel HBM GB/s vs peak",
         "value": round(tps, 3),
@@ -256,8 +371,8 @@ def main():
                    "prompt": a.prompt, "spec_k": k, "seed": SEED},
         "roofline": {"bound": "hbm", "achieved": round(kr["achieved_GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(kr["achieved_GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": kr["kernel"], "us_per_launch": kr["us_per_launch"],
-                     "bytes_per_launch": kr["bytes_per_launch"]},
+                     "kernel": kr["kernel"], "us_per_launch": kr["us_per_launch"], "median_us": kr["median_us"],
+                     "p10_p90_us": kr["p10_p90_us"], "bytes_per_launch": kr["bytes_per_launch"]},
         "kernels": ks,
         "round_roofline": {"bytes_per_round": rb, "ms_per_round": round(ms_round, 3),
                            "achieved_GBs": round(rb / (ms_round * 1e-3) / 1e9, 1),
@@ -266,11 +381,15 @@ def main():
         "stages_ms_per_round": stages,
         "acceptance": round(accepted / (k * a.steps), 4),
         "plain_tokens_per_s": round(plain_tps, 3),
+        "forced": forced,
+        "sustained": {"seconds": round(sus_dt, 2), "rounds": sus_rounds,
+                      "tokens_per_s": round(sus_tokens / max(sus_dt, 1e-9), 3),
+                      "context_end": a.prompt + len(out)},
         "spec_ids_equal_plain": bool(ids_equal),
         "cpu_baseline": None,
     }
     if not a.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, plan, k, a.cpu_seconds, model)
+        result["cpu_baseline"] = cpu_baseline(cfg, plan, k, a.cpu_seconds, model, prompt)
     print(json.dumps(result), flush=True)
 
 

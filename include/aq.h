@@ -165,6 +165,12 @@ int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, 
 int aq_set_q8_fine(int on);
 int aq_q8_fine(void);
 
+/* How many device and pinned-host allocations this library has made since it was loaded (every one it makes is
+ * counted). No counterpart in the reference's API: it is what its counting allocator shows in tests/decode_alloc.rs:80,
+ * 185 and tests/matmul_t_alloc.rs:76-116, that a decode step, a speculative round and a blocked matmul allocate
+ * nothing once their buffers exist. */
+int aq_alloc_counts(uint64_t *device_allocs, uint64_t *pinned_host_allocs);
+
 /* ids_dev[r] = argmax of row r of the t rows of n f32 at x_dev (device): `argmax` (model.rs:505-513), the first
  * maximum on ties; a NaN never becomes the maximum, and a NaN at index 0 is never replaced (the answer is 0). */
 int aq_argmax(aq_ctx *ctx, const float *x_dev, size_t n, size_t t, uint32_t *ids_dev);
@@ -204,8 +210,8 @@ int aq_sampler_accept_or_resample(aq_sampler *sp, const float *target_dev, const
 
 /* ------------------------------------------------------------------------------------ synthetic tensors */
 
-/* A deterministic synthetic tensor: value i is drawn from splitmix64 of (seed, i) (normal: Irwin-Hall of four
- * 16-bit fields; uniform; or constant) and quantised to ggml bytes by this library's block quantisers, with
+/* A deterministic synthetic tensor: value i is drawn from splitmix64 of (seed, i) (normal: the inverse normal CDF of
+ * its top 53 bits, Acklam's approximation in double with IEEE basic operations only; uniform; or constant) and quantised to ggml bytes by this library's block quantisers, with
  * plain IEEE f32 arithmetic, so the host and the device produce the same bytes. No counterpart in the reference
  * (its fixtures come from real GGUF rows and gguf-py quantisers); it builds the benchmark's random-init models. */
 typedef struct aq_synth_spec {
@@ -225,6 +231,10 @@ int aq_weight_synth(aq_ctx *ctx, const aq_synth_spec *spec, aq_weight **out);
  * with HIP events on the context stream. Writes the mean device time per launch in microseconds. */
 int aq_matmul_time(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_act *x, size_t ncols,
                    float *y_dev, int iters, double *us_per_launch);
+/* The same launches with an event between each two: us_each[i] is launch i's device time (iters <= 4096), for
+ * medians and spreads. No counterpart in the reference (its kernel benchmarks are Rust bench harnesses). */
+int aq_matmul_time_each(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_act *x, size_t ncols,
+                        float *y_dev, int iters, float *us_each);
 
 /* ------------------------------------------------------------------------------------------- model level */
 

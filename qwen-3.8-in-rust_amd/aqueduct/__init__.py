@@ -105,6 +105,7 @@ def lib():
         "aq_forward_token_sampled": (i, [P, P, C.c_uint32, P, P]),
         "aq_spec_prefill_sampled": (i, [P, P, P, sz, P]),
         "aq_spec_round_sampled": (i, [P, P, C.c_uint32, P, P, P]),
+        "aq_alloc_counts": (i, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
         "aq_set_q8_fine": (i, [i]),
         "aq_q8_fine": (i, []),
         "aq_argmax": (i, [P, P, sz, sz, P]),
@@ -123,6 +124,7 @@ def lib():
         "aq_gguf_layout": (i, [P, sz, C.c_uint32, P]),
         "aq_gguf_write_synth": (i, [C.c_char_p, P, i, C.c_uint64, i]),
         "aq_matmul_time": (i, [P, P, sz, P, sz, P, i, C.POINTER(C.c_double)]),
+        "aq_matmul_time_each": (i, [P, P, sz, P, sz, P, i, P]),
         "aq_synth_host": (i, [P, P, i]),
         "aq_weight_synth": (i, [P, P, C.POINTER(P)]),
         "aq_model_plan": (i, [P, i, C.c_uint64, P, sz, C.POINTER(sz)]),
@@ -353,6 +355,13 @@ class Sampler:
         return bool(ok.value), t.value
 
 
+def alloc_counts():
+    """(device allocations, pinned host allocations) the library has made so far (aq_alloc_counts)."""
+    d, h = C.c_uint64(), C.c_uint64()
+    check(lib().aq_alloc_counts(C.byref(d), C.byref(h)))
+    return d.value, h.value
+
+
 class q8_fine:
     """The q8-fine switch (aq_set_q8_fine; matvec.rs:133 `set_q8_fine`) on inside the block, restored after."""
 
@@ -394,6 +403,14 @@ def matmul_time(ctx: Context, ws, x: Act, ncols, y: DeviceBuffer, iters):
     us = C.c_double()
     check(lib().aq_matmul_time(ctx.h, arr, len(ws), x.h, ncols, y.p, iters, C.byref(us)))
     return us.value
+
+
+def matmul_time_each(ctx: Context, ws, x: Act, ncols, y: DeviceBuffer, iters):
+    """Per-launch device times (us) of `iters` launches cycling over `ws` (aq_matmul_time_each)."""
+    arr = (C.c_void_p * len(ws))(*[w.h.value for w in ws])
+    out = np.zeros(iters, np.float32)
+    check(lib().aq_matmul_time_each(ctx.h, arr, len(ws), x.h, ncols, y.p, iters, ptr(out)))
+    return out
 
 
 class AqSynthSpec(C.Structure):

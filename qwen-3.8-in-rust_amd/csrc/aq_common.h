@@ -123,6 +123,12 @@ struct Act {
     int device = 0;
 };
 
+// Every device and pinned-host allocation of the library goes through these two, which count it
+// (aq_alloc_counts: what shows that a decode step or a speculative round allocates nothing).
+hipError_t dev_malloc_raw(void **p, size_t bytes);
+hipError_t pinned_malloc(void **p, size_t bytes);
+template <typename T> hipError_t dev_malloc(T **p, size_t bytes) { return dev_malloc_raw((void **)p, bytes); }
+
 // ----------------------------------------------------------------------------------------- kernel launchers
 // All launches go to `stream`; they return 0 or an AQ_E* code.
 int launch_q8k_quantize(const Act &a, size_t ncols, const float *src, size_t src_stride, hipStream_t stream);

@@ -236,7 +236,7 @@ struct Source {
                 if (staging) (void)hipFree(staging);
                 staging = nullptr;
                 staging_bytes = 0;
-                if (hipMalloc(&staging, bytes) != hipSuccess) return fail(AQ_ENOMEM, "model: staging for " + name);
+                if (dev_malloc(&staging, bytes) != hipSuccess) return fail(AQ_ENOMEM, "model: staging for " + name);
                 staging_bytes = bytes;
             }
             int rc = synth_device(e->spec, staging, stream);
@@ -276,7 +276,7 @@ struct Source {
             std::memcpy(host.data(), t->data, len * 4);
         }
         void *p = nullptr;
-        if (hipMalloc(&p, len * 4 + 256) != hipSuccess) return fail(AQ_ENOMEM, "model: vector " + name);
+        if (dev_malloc(&p, len * 4 + 256) != hipSuccess) return fail(AQ_ENOMEM, "model: vector " + name);
         m->vecs.push_back(p);
         AQ_HIP(hipMemcpy(p, host.data(), len * 4, hipMemcpyHostToDevice));
         out = (float *)p;
@@ -446,7 +446,7 @@ Act col_view(const Act &a, size_t col) {
 }
 
 int dalloc(aq_state *s, size_t bytes, void **p) {
-    if (hipMalloc(p, bytes + 256) != hipSuccess) return fail(AQ_ENOMEM, "state: hipMalloc of " + std::to_string(bytes));
+    if (dev_malloc(p, bytes + 256) != hipSuccess) return fail(AQ_ENOMEM, "state: hipMalloc of " + std::to_string(bytes));
     s->allocs.push_back(*p);
     AQ_HIP(hipMemset(*p, 0, bytes + 256));
     return 0;
@@ -1013,7 +1013,7 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
         if (!rc && hipMemcpy(s->sin_tab, st.data(), npos * half * 4, hipMemcpyHostToDevice) != hipSuccess)
             rc = fail(AQ_EHIP, "state: rope table");
     }
-    if (!rc && hipHostMalloc((void **)&s->pinned, 64 * 4, hipHostMallocDefault) != hipSuccess)
+    if (!rc && pinned_malloc((void **)&s->pinned, 64 * 4) != hipSuccess)
         rc = fail(AQ_ENOMEM, "state: pinned");
     // the commit of a speculative round, one launch for every DeltaNet layer: the kept-row count is info[2]
     s->n_dn = n_dn;
@@ -1468,7 +1468,7 @@ int aq_eval_math(aq_ctx *ctx, int fn, const float *x, float *y, size_t n) {
     AQ_REQUIRE(ctx && x && y, "aq_eval_math: null argument");
     AQ_HIP(hipSetDevice(ctx->device));
     float *d = nullptr;
-    if (hipMalloc(&d, 2 * n * 4 + 256) != hipSuccess) return fail(AQ_ENOMEM, "aq_eval_math: buffer");
+    if (dev_malloc(&d, 2 * n * 4 + 256) != hipSuccess) return fail(AQ_ENOMEM, "aq_eval_math: buffer");
     int rc = hipMemcpyAsync(d, x, n * 4, hipMemcpyHostToDevice, ctx->stream) == hipSuccess ? 0 : fail(AQ_EHIP, "upload");
     if (!rc) rc = launch_eval_math(fn, d, d + n, n, ctx->stream);
     if (!rc && hipMemcpyAsync(y, d + n, n * 4, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess)
@@ -1491,11 +1491,11 @@ int aq_deltanet_verify_commit(aq_ctx *ctx, uint32_t nk, uint32_t nv, uint32_t dk
     float *dev[6] = {};
     int rc = 0;
     for (int i = 0; i < 5 && !rc; i++) {
-        if (hipMalloc(&dev[i], bytes[i] + 256) != hipSuccess) rc = fail(AQ_ENOMEM, "deltanet: inputs");
+        if (dev_malloc(&dev[i], bytes[i] + 256) != hipSuccess) rc = fail(AQ_ENOMEM, "deltanet: inputs");
         if (!rc && hipMemcpyAsync(dev[i], hosts[i], bytes[i], hipMemcpyHostToDevice, ctx->stream) != hipSuccess)
             rc = fail(AQ_EHIP, "deltanet: upload");
     }
-    if (!rc && hipMalloc(&dev[5], t * vd * 4 + 256) != hipSuccess) rc = fail(AQ_ENOMEM, "deltanet: output");
+    if (!rc && dev_malloc(&dev[5], t * vd * 4 + 256) != hipSuccess) rc = fail(AQ_ENOMEM, "deltanet: output");
     DnArgs d;
     d.raw = 1;
     d.rq = dev[0];

@@ -16,6 +16,17 @@ void set_error(const std::string &msg) { g_last_error = msg; }
 
 namespace {
 std::atomic<bool> g_q8_fine{false};
+std::atomic<uint64_t> g_dev_allocs{0}, g_pinned_allocs{0};
+} // namespace
+
+hipError_t dev_malloc_raw(void **p, size_t bytes) {
+    g_dev_allocs.fetch_add(1, std::memory_order_relaxed);
+    return hipMalloc(p, bytes);
+}
+
+hipError_t pinned_malloc(void **p, size_t bytes) {
+    g_pinned_allocs.fetch_add(1, std::memory_order_relaxed);
+    return hipHostMalloc(p, bytes, hipHostMallocDefault);
 }
 bool q8_fine() { return g_q8_fine.load(std::memory_order_relaxed); }
 void set_q8_fine(bool on) { g_q8_fine.store(on, std::memory_order_relaxed); }
@@ -83,7 +94,7 @@ static int alloc_weight(Weight &w, int type, size_t rows, size_t cols, int devic
                  sd = align256(nbl * w.dm_bytes);
     w.total = sa + sb + ss + sd;
     void *p = nullptr;
-    if (hipMalloc(&p, w.total) != hipSuccess) return fail(AQ_ENOMEM, "weight: hipMalloc of " + std::to_string(w.total) + " bytes");
+    if (dev_malloc(&p, w.total) != hipSuccess) return fail(AQ_ENOMEM, "weight: hipMalloc of " + std::to_string(w.total) + " bytes");
     w.base = (uint8_t *)p;
     w.qa = w.base;
     w.qb = w.qb_bytes ? w.base + sa : nullptr;
@@ -100,7 +111,7 @@ int weight_from_ggml(Weight &w, int type, size_t rows, size_t cols, const void *
     const uint8_t *src = (const uint8_t *)ggml;
     void *tmp = nullptr;
     if (!ggml_on_device) {
-        if (hipMalloc(&tmp, bytes) != hipSuccess) return fail(AQ_ENOMEM, "weight: staging hipMalloc");
+        if (dev_malloc(&tmp, bytes) != hipSuccess) return fail(AQ_ENOMEM, "weight: staging hipMalloc");
         AQ_HIP(hipMemcpyAsync(tmp, ggml, bytes, hipMemcpyHostToDevice, stream));
         src = (const uint8_t *)tmp;
     }
@@ -129,7 +140,7 @@ int alloc_act(Act &a, size_t n, size_t ncols, int device) {
                  d0 = align256(ncols * a.nb32 * 4), h0 = align256(ncols * a.nb32 * 2), s0 = align256(ncols * a.nb32 * 4);
     const size_t total = f + q + d + bs + q8s + q0 + d0 + h0 + s0;
     void *p = nullptr;
-    if (hipMalloc(&p, total) != hipSuccess) return fail(AQ_ENOMEM, "act: hipMalloc");
+    if (dev_malloc(&p, total) != hipSuccess) return fail(AQ_ENOMEM, "act: hipMalloc");
     if (hipMemset(p, 0, total) != hipSuccess) return fail(AQ_EHIP, "act: hipMemset");
     // The clear runs on the null stream, which the context's non-blocking stream does not wait for.
     if (hipDeviceSynchronize() != hipSuccess) return fail(AQ_EHIP, "act: clear sync");
@@ -225,7 +236,7 @@ int aq_dev_alloc(aq_ctx *ctx, size_t nbytes, void **dev_out) {
     AQ_REQUIRE(ctx && dev_out, "aq_dev_alloc: null argument");
     AQ_HIP(hipSetDevice(ctx->device));
     void *p = nullptr;
-    if (hipMalloc(&p, nbytes ? nbytes : 1) != hipSuccess) return fail(AQ_ENOMEM, "aq_dev_alloc");
+    if (dev_malloc(&p, nbytes ? nbytes : 1) != hipSuccess) return fail(AQ_ENOMEM, "aq_dev_alloc");
     *dev_out = p;
     return 0;
 }
@@ -288,7 +299,7 @@ int aq_weight_download(const aq_weight *w, void *ggml_bytes_out) {
     AQ_HIP(hipSetDevice(ctx->device));
     const size_t bytes = w->w.rows * w->w.nb * block_bytes(w->w.type);
     void *tmp = nullptr;
-    if (hipMalloc(&tmp, bytes) != hipSuccess) return fail(AQ_ENOMEM, "aq_weight_download: staging");
+    if (dev_malloc(&tmp, bytes) != hipSuccess) return fail(AQ_ENOMEM, "aq_weight_download: staging");
     Weight copy = w->w;
     int rc = launch_repack(copy, (const uint8_t *)tmp, false, ctx->stream);
     if (rc == 0) {
@@ -418,6 +429,12 @@ int aq_set_q8_fine(int on) {
 
 int aq_q8_fine(void) { return q8_fine() ? 1 : 0; }
 
+int aq_alloc_counts(uint64_t *device_allocs, uint64_t *pinned_host_allocs) {
+    if (device_allocs) *device_allocs = g_dev_allocs.load(std::memory_order_relaxed);
+    if (pinned_host_allocs) *pinned_host_allocs = g_pinned_allocs.load(std::memory_order_relaxed);
+    return 0;
+}
+
 int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, int32_t *lanes_dev,
                 int32_t *mins_dev) {
     if (q8_fine()) return fail(AQ_EUNSUP, "aq_kq_isums: the integer lanes are the Q8_K kernel's; q8-fine is on");
@@ -427,7 +444,7 @@ int aq_kq_isums(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, 
     AQ_REQUIRE(ncols >= 1 && ncols <= x->a.ncols, "aq_kq_isums: ncols");
     AQ_HIP(hipSetDevice(ctx->device));
     void *y = nullptr;
-    if (hipMalloc(&y, ncols * w->w.rows * 4) != hipSuccess) return fail(AQ_ENOMEM, "aq_kq_isums: outputs");
+    if (dev_malloc(&y, ncols * w->w.rows * 4) != hipSuccess) return fail(AQ_ENOMEM, "aq_kq_isums: outputs");
     int rc = kq_isums_run(w->w, x->a, ncols, (float *)y, lanes_dev, mins_dev, ctx->stream);
     if (!rc && hipStreamSynchronize(ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_kq_isums: sync");
     (void)hipFree(y);
@@ -439,7 +456,7 @@ int aq_argmax(aq_ctx *ctx, const float *x_dev, size_t n, size_t t, uint32_t *ids
     AQ_REQUIRE(n >= 1 && t >= 1 && n <= 0xFFFFFFFEull, "aq_argmax: empty or over-long rows");
     AQ_HIP(hipSetDevice(ctx->device));
     void *scratch = nullptr;
-    if (hipMalloc(&scratch, argmax_scratch_bytes(n, t)) != hipSuccess) return fail(AQ_ENOMEM, "aq_argmax: scratch");
+    if (dev_malloc(&scratch, argmax_scratch_bytes(n, t)) != hipSuccess) return fail(AQ_ENOMEM, "aq_argmax: scratch");
     int rc = launch_argmax(x_dev, n, n, t, ids_dev, scratch, ctx->stream);
     if (!rc && hipStreamSynchronize(ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_argmax: sync");
     (void)hipFree(scratch);
@@ -486,6 +503,36 @@ int aq_matmul_time(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_
     AQ_HIP(hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
     *us_per_launch = (double)ms * 1000.0 / iters;
     return 0;
+}
+
+int aq_matmul_time_each(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_act *x, size_t ncols, float *y_dev,
+                        int iters, float *us_each) {
+    AQ_REQUIRE(ctx && ws && nw > 0 && us_each && iters > 0 && iters <= 4096, "aq_matmul_time_each: bad argument");
+    for (size_t i = 0; i < nw; i++) {
+        int rc = check_matmul(ws[i], x, ncols, y_dev);
+        if (rc) return rc;
+        AQ_REQUIRE(ws[i]->w.rows == ws[0]->w.rows, "aq_matmul_time_each: weights of different shapes");
+    }
+    AQ_HIP(hipSetDevice(ctx->device));
+    std::vector<hipEvent_t> ev((size_t)iters + 1, nullptr);
+    int rc = 0;
+    for (auto &e : ev)
+        if (!rc && hipEventCreate(&e) != hipSuccess) rc = fail(AQ_EHIP, "aq_matmul_time_each: event");
+    // one event between consecutive launches: launch i's time is the interval between events i and i + 1
+    for (int i = 0; !rc && i < iters; i++) {
+        if (hipEventRecord(ev[i], ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_matmul_time_each: record");
+        if (!rc) rc = launch_matmul(ws[i % nw]->w, x->a, ncols, y_dev, nullptr, ctx->stream);
+    }
+    if (!rc && hipEventRecord(ev[iters], ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_matmul_time_each: record");
+    if (!rc && hipEventSynchronize(ev[iters]) != hipSuccess) rc = fail(AQ_EHIP, "aq_matmul_time_each: sync");
+    for (int i = 0; !rc && i < iters; i++) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, ev[i], ev[i + 1]) != hipSuccess) rc = fail(AQ_EHIP, "aq_matmul_time_each: time");
+        us_each[i] = ms * 1000.0f;
+    }
+    for (auto &e : ev)
+        if (e) (void)hipEventDestroy(e);
+    return rc;
 }
 
 } // extern "C"

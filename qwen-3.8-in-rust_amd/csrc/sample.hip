@@ -512,7 +512,7 @@ int aq_sampler_new(aq_ctx *ctx, const aq_sampler_config *cfg, uint32_t vocab, aq
                  b_buf = align256((size_t)ROWS_MAX * sp->chunk_stride * 8), b_in = align256((size_t)vocab * 8),
                  b_tmp = align256(tmp + 1), b_ams = align256(argmax_scratch_bytes(vocab, 1));
     const size_t total = b_rng + b_idx + b_probs + b_res + b_keys + 2 * b_buf + b_in + b_ams + b_tmp;
-    if (hipMalloc(&sp->base, total) != hipSuccess) {
+    if (dev_malloc(&sp->base, total) != hipSuccess) {
         delete sp;
         return fail(AQ_ENOMEM, "aq_sampler_new: hipMalloc");
     }
@@ -527,7 +527,7 @@ int aq_sampler_new(aq_ctx *ctx, const aq_sampler_config *cfg, uint32_t vocab, aq
     sp->sort_in = (uint64_t *)p, p += b_in;
     sp->amax_scratch = (uint32_t *)p, p += b_ams;
     sp->sort_tmp = p;
-    if (hipHostMalloc((void **)&sp->pinned, 64, hipHostMallocDefault) != hipSuccess) {
+    if (pinned_malloc((void **)&sp->pinned, 64) != hipSuccess) {
         (void)hipFree(sp->base);
         delete sp;
         return fail(AQ_ENOMEM, "aq_sampler_new: pinned buffer");

@@ -1,9 +1,11 @@
 // synth.h — deterministic synthetic tensors, identical on the host and the device.
 //
-// Element i of a tensor is drawn from splitmix64(seed + i * golden); a "normal" value is the Irwin–Hall sum of
-// the draw's four 16-bit fields, centred and scaled (bounded at 3.46 sigma), so it is an integer times one f32
-// constant and comes out bit-identical on any IEEE machine. The block quantisers below turn 256 (K-quants) or 32
-// (Q8_0/Q4_0) values into ggml blocks with plain IEEE single-precision operations (no FMA, no transcendental),
+// Element i of a tensor is drawn from splitmix64(seed ^ i * odd constant); a "normal" value is the inverse normal
+// CDF of that draw's top 53 bits, p = (k + 1/2) 2^-53, by Acklam's rational approximation (relative error below
+// 1.2e-9; tails out to 8.3 sigma), evaluated in double with +, -, *, / only: the logarithm of the tails is an atanh
+// series and the square root Newton's iteration, both written out here, so host and device compute the same bits
+// (IEEE basic operations round correctly on both; contraction is off). The block quantisers below turn 256 (K-quants)
+// or 32 (Q8_0/Q4_0) values into ggml blocks with plain IEEE single-precision operations (no FMA, no transcendental),
 // so host and device produce the same bytes. They are this library's own min/max quantisers, not ggml's
 // iterative ones: the model's bytes are the source of truth for the GPU path and the CPU reference alike.
 #pragma once
@@ -33,9 +35,61 @@ AQ_HD inline uint64_t splitmix64(uint64_t x) {
     return x ^ (x >> 31);
 }
 
-// 1 / sqrt(4 * (65536^2 - 1) / 12): the standard deviation of the sum of four uniform 16-bit integers.
-constexpr double IRWIN_HALL4_INV_STD = 1.0 / 37837.22626683413;
+// ln(x) for x in (0, 1]: x = m 2^e with m in [sqrt(1/2), sqrt(2)), ln m = 2 atanh(t), t = (m - 1) / (m + 1), |t| < 0.172,
+// the series to t^31 (below 1e-23 after that).
+AQ_HD inline double synth_ln(double x) {
+    uint64_t b;
+    __builtin_memcpy(&b, &x, 8);
+    int e = (int)((b >> 52) & 0x7FF) - 1023;
+    b = (b & 0x000FFFFFFFFFFFFFull) | 0x3FF0000000000000ull;
+    double m;
+    __builtin_memcpy(&m, &b, 8);
+    if (m > 1.4142135623730951) {
+        m *= 0.5;
+        e += 1;
+    }
+    const double t = (m - 1.0) / (m + 1.0), t2 = t * t;
+    double s = 1.0 / 31.0;
+    for (int k = 29; k >= 1; k -= 2) s = s * t2 + 1.0 / (double)k;
+    return 2.0 * t * s + (double)e * 0.69314718055994531;
+}
 
+// sqrt(x) for x in [0.04, 80] (the tails' -2 ln p): Newton's iteration from an exponent-halving first guess (within
+// 6 %), five steps (quadratic convergence: far below an ulp).
+AQ_HD inline double synth_sqrt(double x) {
+    uint64_t b;
+    __builtin_memcpy(&b, &x, 8);
+    b = (b >> 1) + 0x1FF8000000000000ull;
+    double y;
+    __builtin_memcpy(&y, &b, 8);
+    for (int k = 0; k < 5; k++) y = 0.5 * (y + x / y);
+    return y;
+}
+
+// The inverse of the standard normal CDF at p in (0, 1): Acklam's algorithm (central rational function for
+// 0.02425 <= p <= 0.97575, tail rational functions of sqrt(-2 ln p) outside).
+AQ_HD inline double synth_inv_normal(double p) {
+    const double a1 = -3.969683028665376e+01, a2 = 2.209460984245205e+02, a3 = -2.759285104469687e+02,
+                 a4 = 1.383577518672690e+02, a5 = -3.066479806614716e+01, a6 = 2.506628277459239e+00;
+    const double b1 = -5.447609879822406e+01, b2 = 1.615858368580409e+02, b3 = -1.556989798598866e+02,
+                 b4 = 6.680131188771972e+01, b5 = -1.328068155288572e+01;
+    const double c1 = -7.784894002430293e-03, c2 = -3.223964580411365e-01, c3 = -2.400758277161838e+00,
+                 c4 = -2.549732539343734e+00, c5 = 4.374664141464968e+00, c6 = 2.938163982698783e+00;
+    const double d1 = 7.784695709041462e-03, d2 = 3.224671290700398e-01, d3 = 2.445134137142996e+00,
+                 d4 = 3.754408661907416e+00;
+    const double plow = 0.02425;
+    if (p < plow || p > 1.0 - plow) {
+        const double q = synth_sqrt(-2.0 * synth_ln(p < plow ? p : 1.0 - p));
+        const double x = (((((c1 * q + c2) * q + c3) * q + c4) * q + c5) * q + c6) /
+                         ((((d1 * q + d2) * q + d3) * q + d4) * q + 1.0);
+        return p < plow ? x : -x;
+    }
+    const double q = p - 0.5, r = q * q;
+    return (((((a1 * r + a2) * r + a3) * r + a4) * r + a5) * r + a6) * q /
+           (((((b1 * r + b2) * r + b3) * r + b4) * r + b5) * r + 1.0);
+}
+
+// Value i: `scale` is sigma (normal) as an f32.
 AQ_HD inline float synth_value(const SynthSpec &s, uint64_t i, float scale) {
     const uint64_t z = splitmix64(s.seed ^ (i * 0xD1B54A32D192ED03ull));
     if (s.dist == SYNTH_CONST) return s.a;
@@ -43,9 +97,8 @@ AQ_HD inline float synth_value(const SynthSpec &s, uint64_t i, float scale) {
         const float u = (float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f);
         return s.a + (s.b - s.a) * u;
     }
-    const int32_t sum = (int32_t)(z & 0xFFFF) + (int32_t)((z >> 16) & 0xFFFF) + (int32_t)((z >> 32) & 0xFFFF) +
-                        (int32_t)(z >> 48);
-    return s.a + (float)(sum - 131070) * scale; // scale = sigma / std(Irwin-Hall)
+    const double p = ((double)(z >> 11) + 0.5) * 0x1p-53;
+    return s.a + (float)(synth_inv_normal(p) * (double)scale);
 }
 
 // f32 -> f16 bits, round to nearest even (the same rounding as half::f16::from_f32), in plain integer code.
@@ -254,6 +307,6 @@ AQ_HD inline void synth_block(const SynthSpec &s, uint64_t blk, float scale, uin
     }
 }
 
-inline float synth_scale(const SynthSpec &s) { return (float)((double)s.b * IRWIN_HALL4_INV_STD); }
+inline float synth_scale(const SynthSpec &s) { return s.b; }
 
 } // namespace aq

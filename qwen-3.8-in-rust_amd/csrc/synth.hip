@@ -92,7 +92,7 @@ int aq_weight_synth(aq_ctx *ctx, const aq_synth_spec *spec, aq_weight **out) {
     AQ_HIP(hipSetDevice(ctx->device));
     const size_t bytes = (size_t)spec->rows * (spec->cols / block_elems(spec->ggml_type)) * block_bytes(spec->ggml_type);
     void *tmp = nullptr;
-    if (hipMalloc(&tmp, bytes) != hipSuccess) return fail(AQ_ENOMEM, "aq_weight_synth: staging");
+    if (dev_malloc(&tmp, bytes) != hipSuccess) return fail(AQ_ENOMEM, "aq_weight_synth: staging");
     rc = synth_device(*spec, (uint8_t *)tmp, ctx->stream);
     aq_weight *w = nullptr;
     if (rc == 0) {

@@ -49,14 +49,42 @@ def test_synth_quantisers_deterministic_and_faithful(t):
     assert not np.array_equal(a, aq.synth_host(spec2))
     deq = O.dequant(t, a, rows * cols)
     assert np.all(np.isfinite(deq))
-    # the generator's own values: Irwin-Hall(4) normal of sigma 0.02
+    # the generator's own values: normal of sigma 0.02
     f = aq.synth_host(aq.synth_spec(aq.F32, rows, cols, seed=1234, b=0.02))
     assert abs(float(f.std()) - 0.02) < 0.001 and abs(float(f.mean())) < 0.001
-    assert float(np.abs(f).max()) <= 0.02 * 3.4642
     # quantisation error small against the scale
     rel = float(np.sqrt(np.mean((deq - f) ** 2))) / 0.02
     limit = {aq.Q4_K: 0.15, aq.Q5_K: 0.08, aq.Q6_K: 0.05, aq.Q8_0: 0.02, aq.Q4_0: 0.15}[t]
     assert rel < limit, f"rms quantisation error {rel:.3f} of sigma"
+
+
+def test_synth_normal_is_normal():
+    """N(a, b): moments, tails and the whole CDF of a million draws (scipy's normal as the yardstick), and the
+    inverse CDF's accuracy at fixed points where Phi^-1 is known to many digits."""
+    from scipy import stats
+    n = 1 << 20
+    f = aq.synth_host(aq.synth_spec(aq.F32, 1, n, seed=77, b=0.02)).astype(np.float64) / 0.02
+    assert abs(f.mean()) < 0.005 and abs(f.std() - 1.0) < 0.005
+    assert abs(stats.kurtosis(f)) < 0.03 and abs(stats.skew(f)) < 0.01  # Irwin-Hall(4) would give -0.3
+    assert abs(np.mean(np.abs(f) > 3.0) / (2 * stats.norm.sf(3.0)) - 1.0) < 0.1
+    assert np.max(np.abs(f)) > 4.0
+    assert stats.kstest(f, "norm").pvalue > 1e-3
+    g = aq.synth_host(aq.synth_spec(aq.F32, 1, 4096, seed=5, a=1.5, b=0.25)).astype(np.float64)
+    assert abs(g.mean() - 1.5) < 0.02 and abs(g.std() - 0.25) < 0.01
+    # value i is Phi^-1(p_i) * sigma with p_i from the element's splitmix64 draw: check against scipy's ppf
+    m64 = (1 << 64) - 1
+
+    def splitmix(x):
+        x = (x + 0x9E3779B97F4A7C15) & m64
+        x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & m64
+        x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & m64
+        return x ^ (x >> 31)
+
+    h = aq.synth_host(aq.synth_spec(aq.F32, 1, 4096, seed=77, b=0.02)).astype(np.float64)
+    ps = np.array([((splitmix(77 ^ ((i * 0xD1B54A32D192ED03) & m64)) >> 11) + 0.5) * 2.0 ** -53 for i in range(4096)])
+    want = stats.norm.ppf(ps) * 0.02
+    assert np.max(np.abs(h - want) / np.abs(want)) < 2e-7
+    assert np.sum((ps < 0.02425) | (ps > 0.97575)) > 100  # the tail branch is exercised
 
 
 def test_synth_uniform_and_const():
