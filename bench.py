@@ -19,6 +19,7 @@ Printed as one JSON line, with
                 at the reference's measured mean (about 2 of 3 accepted per round at k = 3 on real weights,
                 docs/spec.md:140-142), and the round time by m. Random-init weights make the MTP accept almost
                 nothing, so `value` is near one token per round; these show what the round delivers when drafts land;
+  prefill       the 64-token prompt's prefill (one pass over the weights per chunk of up to 64 rows) on a fresh state;
   sustained     --spec 3 rounds kept running for --sustain-seconds after the timed ones (the GPU busy long enough to
                 be seen by a utilisation sampler), tokens/s over that stretch;
   cpu_baseline  the CPU oracle (a scalar C restatement of the reference's CPU path, not its hand-written AVX2
@@ -297,6 +298,19 @@ def main():
     max_pos = (a.prompt + (k + 1) * (a.warmup + a.steps + 2 * a.forced_rounds) + a.plain_tokens + 64 +
                int(400 * a.sustain_seconds))
 
+    # prompt prefill (model.rs:443-461): the 64-token prompt on fresh states, timed after one warm-up run
+    pre_ms = []
+    for r in range(4):
+        st = aq.State(model, 0, a.prompt + 64)
+        ctx.sync()
+        t1 = time.perf_counter()
+        st.prefill(prompt)
+        pre_ms.append((time.perf_counter() - t1) * 1e3)
+        st.free()
+    prefill = {"tokens": a.prompt, "ms": round(float(np.median(pre_ms[1:])), 3),
+               "tokens_per_s": round(a.prompt / (float(np.median(pre_ms[1:])) * 1e-3), 1)}
+    log(f"prefill: {prefill}")
+
     # plain greedy decode (reported beside the speculative number)
     ps = aq.State(model, 0, max_pos)
     plain = [ps.prefill(prompt)]
@@ -381,6 +395,7 @@ def main():
         "stages_ms_per_round": stages,
         "acceptance": round(accepted / (k * a.steps), 4),
         "plain_tokens_per_s": round(plain_tps, 3),
+        "prefill": prefill,
         "forced": forced,
         "sustained": {"seconds": round(sus_dt, 2), "rounds": sus_rounds,
                       "tokens_per_s": round(sus_tokens / max(sus_dt, 1e-9), 3),

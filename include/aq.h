@@ -130,7 +130,7 @@ int aq_weight_upload(aq_ctx *ctx, int ggml_type, size_t rows, size_t cols, const
 int aq_weight_free(aq_weight *w);
 int aq_weight_download(const aq_weight *w, void *ggml_bytes_out);
 
-/* Activation buffer of `ncols` rows of `n` values on the device: the f32 rows and their quantised forms (Q8_K
+/* Activation buffer of `ncols` (1..64) rows of `n` values on the device: the f32 rows and their quantised forms (Q8_K
  * in the kernels' layout, Q8_0). Replaces `ActBuf` (matvec.rs:216-267). */
 typedef struct aq_act aq_act;
 int aq_act_new(aq_ctx *ctx, size_t n, size_t ncols, aq_act **out);
@@ -145,7 +145,8 @@ int aq_act_quantize(aq_act *a, int weight_type, size_t ncols);
 int aq_act_get_q8k(const aq_act *a, void *ggml_out, size_t ncols);
 int aq_act_get_q8_0(const aq_act *a, void *ggml_out, size_t ncols);
 
-/* y[c * rows + r] = W[r] . x[c] for c < ncols (ncols 1..8, at most the activation's columns; 1 is the matvec). Replaces `matvec`
+/* y[c * rows + r] = W[r] . x[c] for c < ncols (ncols 1..64, at most the activation's columns; 1 is the matvec; past 8
+ * columns the many-column matrix-core kernels, the prompt-chunk form of model.rs:443-461). Replaces `matvec`
  * (matvec.rs:336), `matmul_fn` (matvec.rs:377) and the blocked kernel `dot_q8k_t` (kdot.rs:314); under the q8-fine
  * switch, K-quant weights take `dot_q4_k_q8` / `dot_q5_k_q8` / `dot_q6_k_q8` (dot.rs:69-160). `y_dev` is a device
  * buffer of ncols * rows f32. The activation must have been quantised for w's type under the same switch. */

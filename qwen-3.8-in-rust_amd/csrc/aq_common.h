@@ -148,6 +148,10 @@ int launch_kq_group(const Weight *const *ws, float *const *ys, const float *cons
 // K-quant weights x Q8_0 activations (kq_q8f.hip, dot.rs:69-160); launch_matmul routes K-quant weights here when
 // the q8-fine switch is on. y as launch_matmul; ncols 1..16.
 int launch_kq_q8f(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
+// Many columns (a prompt chunk): K-quant x Q8_K and Q8_0 / Q4_0 x Q8_0 on the 16x16x32 matrix cores (kq_gemm.hip).
+int launch_gemm(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
+// Any column count: launch_matmul up to 8 columns, launch_gemm past that where it applies, else 8-column pieces.
+int launch_matmul_many(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
 int launch_repack(Weight &w, const uint8_t *ggml_dev, bool to_planes, hipStream_t stream);
 
 } // namespace aq

@@ -495,6 +495,29 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
 
 } // namespace
 
+int launch_matmul_many(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream) {
+    if (ncols <= 8) return launch_matmul(w, x, ncols, y, resid, stream);
+    if ((is_kquant(w.type) && !q8_fine()) || w.type == AQ_TYPE_Q8_0 || w.type == AQ_TYPE_Q4_0)
+        return launch_gemm(w, x, ncols, y, resid, stream);
+    for (size_t c0 = 0; c0 < ncols; c0 += 8) { // F32 weights, and K-quants under the q8-fine switch
+        const size_t tc = ncols - c0 < 8 ? ncols - c0 : 8;
+        Act v = x;
+        v.ncols = x.ncols - c0;
+        v.f32 = x.f32 + c0 * x.n;
+        v.qs = x.qs + c0 * x.n;
+        v.d = x.d + c0 * x.nb;
+        v.bs = x.bs + c0 * x.nb * 16;
+        v.q8s = x.q8s + c0 * x.nb * 8;
+        v.q0 = x.q0 + c0 * x.n;
+        v.d0 = x.d0 + c0 * x.nb32;
+        v.h0 = x.h0 + c0 * x.nb32;
+        v.s0 = x.s0 + c0 * x.nb32;
+        const int rc = launch_matmul(w, v, tc, y + c0 * w.rows, resid ? resid + c0 * w.rows : nullptr, stream);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream) {
     if (is_kquant(w.type))
         return q8_fine() ? launch_kq_q8f(w, x, ncols, y, resid, stream) : launch_kq_mfma(w, x, ncols, y, resid, stream);

@@ -24,7 +24,8 @@ int synth_device(const aq_synth_spec &s, uint8_t *out, hipStream_t stream);
 
 namespace {
 
-constexpr int MAX_ROWS = 8; // rows per batched pass: the matmul kernels take 1..8 activation columns
+constexpr int MAX_ROWS = 8;  // rows per verify / decode pass: the matrix-core matmul takes 1..8 activation columns
+constexpr int PRE_ROWS = 64; // rows per prompt chunk (model.rs:443-461: one pass over the weights per chunk)
 
 bool is_attention_layer(const aq_model_config &c, uint32_t i) {
     return c.full_attention_interval > 0 && (i + 1) % c.full_attention_interval == 0;
@@ -514,13 +515,22 @@ int quantize_act(aq_state *s, Act &act, size_t t, const Needs &nd) {
     return rc;
 }
 
+// y[c * rows + r] = W[r] . x[c] (+ resid) for c < t: one launch for up to MAX_ROWS columns; a prompt chunk's wider
+// batches go to the many-column kernels (K-quant and Q8_0 / Q4_0 weights) or are split into MAX_ROWS-column pieces.
 int mm(aq_state *s, const Weight &w, const Act &x, size_t t, float *y, const float *resid = nullptr) {
-    return launch_matmul(w, x, t, y, resid, s->stream);
+    return launch_matmul_many(w, x, t, y, resid, s->stream);
 }
 
 // Several matrices over the same activations: one grouped launch when they are K-quants of one K, optionally
 // followed by (at most two) F32 matrices.
 int mm_multi(aq_state *s, int n, const Weight *const *ws, float *const *ys, const Act &x, size_t t) {
+    if (t > (size_t)MAX_ROWS) { // a prompt chunk: each matrix over all its columns
+        for (int i = 0; i < n; i++) {
+            const int rc = mm(s, *ws[i], x, t, ys[i]);
+            if (rc) return rc;
+        }
+        return 0;
+    }
     bool grouped = is_kquant(ws[0]->type);
     int nf = 0;
     for (int i = 0; i < n; i++) {
@@ -606,8 +616,24 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
         a.rd = (int)c.rope_dim;
         a.gsc = s->attn_sc;
         a.gsc_stride = s->attn_sc_stride;
-        if ((rc = launch_attention(a, s->stream))) return rc;
-        kv->len += t;
+        // pieces of at most MAX_ROWS rows (the score rows a context past the LDS keeps in device memory are that
+        // many); each piece's K/V rows are appended before the next piece attends to them
+        const size_t qw = 2 * (size_t)c.n_head * c.head_dim, kw = kv->stride, ow = (size_t)c.n_head * c.head_dim;
+        for (size_t r0 = 0; r0 < t; r0 += MAX_ROWS) {
+            const size_t tr = t - r0 < (size_t)MAX_ROWS ? t - r0 : (size_t)MAX_ROWS;
+            AttnArgs ap = a;
+            ap.qg = a.qg + r0 * qw;
+            ap.kk = a.kk + r0 * kw;
+            ap.vv = a.vv + r0 * kw;
+            ap.q = a.q + r0 * ow;
+            ap.out = a.out + r0 * ow;
+            ap.q8k = col_view(s->act_att, r0);
+            ap.start_pos = start_pos + r0;
+            ap.base = kv->len;
+            ap.t = (int)tr;
+            if ((rc = launch_attention(ap, s->stream))) return rc;
+            kv->len += tr;
+        }
         if (!q8k) {
             Needs no;
             no.add(L.o);
@@ -650,7 +676,36 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
     d.dk = (int)c.dn_head_dim_k;
     d.dv = (int)c.dn_head_dim_v;
     d.kernel = (int)c.dn_conv_kernel;
-    if ((rc = launch_dn_core(d, s->stream))) return rc;
+    if (t <= 8) {
+        if ((rc = launch_dn_core(d, s->stream))) return rc;
+    } else {
+        // a prompt chunk: pieces of 8 rows, the state advancing piece by piece and each piece's conv window read
+        // from the one the previous piece wrote; the last piece writes the buffer the pass's parity flip expects
+        // (with an even number of pieces the window is copied across first, so the chain ends there)
+        AQ_REQUIRE(mode == PLAIN, "deltanet: more than 8 rows in one verify batch");
+        const size_t np = (t + 7) / 8;
+        float *cur = s->par ? s->conv1[dn_slot] : s->conv0[dn_slot], *nxt = s->par ? s->conv0[dn_slot] : s->conv1[dn_slot];
+        if (np % 2 == 0) {
+            AQ_HIP(hipMemcpyAsync(nxt, cur, m->cd * (c.dn_conv_kernel - 1) * sizeof(float), hipMemcpyDeviceToDevice,
+                                  s->stream));
+            std::swap(cur, nxt);
+        }
+        const size_t cd = m->cd, vd = m->vd, nvh = c.dn_n_v_heads;
+        for (size_t r0 = 0; r0 < t; r0 += 8) {
+            DnArgs dp = d;
+            dp.t = (int)(t - r0 < 8 ? t - r0 : 8);
+            dp.mixed = d.mixed + r0 * cd;
+            dp.z = d.z + r0 * vd;
+            dp.a = d.a + r0 * nvh;
+            dp.b = d.b + r0 * nvh;
+            dp.out = d.out + r0 * vd;
+            dp.q80 = col_view(s->act_vd, r0);
+            dp.conv_src = cur;
+            dp.conv_dst = nxt;
+            if ((rc = launch_dn_core(dp, s->stream))) return rc;
+            std::swap(cur, nxt);
+        }
+    }
     if (!q80) {
         Needs no;
         no.add(L.ssm_out);
@@ -794,8 +849,8 @@ int run_prompt(aq_state *s, const uint32_t *ids, size_t n) {
     AQ_REQUIRE(s->pos + n + MAX_ROWS <= s->max_pos, "prompt: longer than the state's max_pos");
     int rc = copy_ids_in(s, s->prompt, ids, n);
     if (rc) return rc;
-    for (size_t c0 = 0; c0 < n; c0 += MAX_ROWS) {
-        const size_t tc = n - c0 < (size_t)MAX_ROWS ? n - c0 : (size_t)MAX_ROWS;
+    for (size_t c0 = 0; c0 < n; c0 += PRE_ROWS) {
+        const size_t tc = n - c0 < (size_t)PRE_ROWS ? n - c0 : (size_t)PRE_ROWS;
         if ((rc = forward_rows(s, s->prompt + c0, tc, PLAIN))) return rc;
         Needs nd; // final norm of every row (the MTP reads them); only the last row needs the lm_head
         nd.add(m->lm_head);
@@ -903,7 +958,7 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
     s->device = m->device;
     s->k = spec_k;
     s->max_pos = max_pos + MAX_ROWS; // room for a verify batch past the last committed position
-    const size_t T = MAX_ROWS, h = c.hidden, nv = c.dn_n_v_heads;
+    const size_t T = MAX_ROWS, TP = PRE_ROWS, h = c.hidden, nv = c.dn_n_v_heads;
     const size_t cap = s->max_pos, stride = (size_t)c.n_head_kv * c.head_dim;
     const size_t rec_len = nv * c.dn_head_dim_k * c.dn_head_dim_v, conv_len = m->cd * (c.dn_conv_kernel - 1);
     int rc = 0;
@@ -958,25 +1013,25 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
         AQ_S(dalloc_t(s, s->mtp_kv.cap * stride, &s->mtp_kv.k));
         AQ_S(dalloc_t(s, s->mtp_kv.cap * stride, &s->mtp_kv.v));
     }
-    AQ_S(alloc_act(s->act_h, h, T, m->ctx->device));
-    AQ_S(alloc_act(s->act_ffn, c.ffn, T, m->ctx->device));
-    AQ_S(alloc_act(s->act_vd, m->vd, T, m->ctx->device));
-    AQ_S(alloc_act(s->act_att, (size_t)c.n_head * c.head_dim, T, m->ctx->device));
+    AQ_S(alloc_act(s->act_h, h, TP, m->ctx->device));
+    AQ_S(alloc_act(s->act_ffn, c.ffn, TP, m->ctx->device));
+    AQ_S(alloc_act(s->act_vd, m->vd, TP, m->ctx->device));
+    AQ_S(alloc_act(s->act_att, (size_t)c.n_head * c.head_dim, TP, m->ctx->device));
     AQ_S(alloc_act(s->act_cat, 2 * h, T, m->ctx->device));
-    AQ_S(dalloc_t(s, T * h, &s->xa));
-    AQ_S(dalloc_t(s, T * h, &s->xb));
-    AQ_S(dalloc_t(s, T * h, &s->y));
+    AQ_S(dalloc_t(s, TP * h, &s->xa));
+    AQ_S(dalloc_t(s, TP * h, &s->xb));
+    AQ_S(dalloc_t(s, TP * h, &s->y));
     AQ_S(dalloc_t(s, T * h, &s->e));
-    AQ_S(dalloc_t(s, T * m->cd, &s->mixed));
-    AQ_S(dalloc_t(s, T * m->vd, &s->z));
-    AQ_S(dalloc_t(s, T * nv, &s->a));
-    AQ_S(dalloc_t(s, T * nv, &s->b));
-    AQ_S(dalloc_t(s, T * 2 * c.n_head * c.head_dim, &s->qg));
-    AQ_S(dalloc_t(s, T * stride, &s->kk));
-    AQ_S(dalloc_t(s, T * stride, &s->vv));
-    AQ_S(dalloc_t(s, T * c.n_head * c.head_dim, &s->qr));
-    AQ_S(dalloc_t(s, T * c.ffn, &s->g));
-    AQ_S(dalloc_t(s, T * c.ffn, &s->u));
+    AQ_S(dalloc_t(s, TP * m->cd, &s->mixed));
+    AQ_S(dalloc_t(s, TP * m->vd, &s->z));
+    AQ_S(dalloc_t(s, TP * nv, &s->a));
+    AQ_S(dalloc_t(s, TP * nv, &s->b));
+    AQ_S(dalloc_t(s, TP * 2 * c.n_head * c.head_dim, &s->qg));
+    AQ_S(dalloc_t(s, TP * stride, &s->kk));
+    AQ_S(dalloc_t(s, TP * stride, &s->vv));
+    AQ_S(dalloc_t(s, TP * c.n_head * c.head_dim, &s->qr));
+    AQ_S(dalloc_t(s, TP * c.ffn, &s->g));
+    AQ_S(dalloc_t(s, TP * c.ffn, &s->u));
     AQ_S(dalloc_t(s, T * c.vocab, &s->logits));
     AQ_S(dalloc_t(s, T * h, &s->normed));
     AQ_S(dalloc_t(s, (size_t)s->max_pos * h, &s->normed_all));

@@ -312,7 +312,7 @@ int aq_weight_download(const aq_weight *w, void *ggml_bytes_out) {
 
 int aq_act_new(aq_ctx *ctx, size_t n, size_t ncols, aq_act **out) {
     AQ_REQUIRE(ctx && out, "aq_act_new: null argument");
-    AQ_REQUIRE(ncols >= 1 && ncols <= 16, "aq_act_new: ncols must be 1..16");
+    AQ_REQUIRE(ncols >= 1 && ncols <= 64, "aq_act_new: ncols must be 1..64");
     AQ_HIP(hipSetDevice(ctx->device));
     aq_act *a = new aq_act();
     a->ctx = ctx;
@@ -406,7 +406,7 @@ static int check_matmul(const aq_weight *w, const aq_act *x, size_t ncols, const
     AQ_REQUIRE(w && x && y, "aq_matmul: null argument");
     AQ_REQUIRE(x->a.n == w->w.cols, "aq_matmul: activation length " + std::to_string(x->a.n) + " != weight cols " +
                                         std::to_string(w->w.cols) + " (matvec.rs:338-339)");
-    AQ_REQUIRE(ncols >= 1 && ncols <= x->a.ncols && ncols <= 8, "aq_matmul: ncols must be 1..min(8, act columns)");
+    AQ_REQUIRE(ncols >= 1 && ncols <= x->a.ncols && ncols <= 64, "aq_matmul: ncols must be 1..min(64, act columns)");
     AQ_REQUIRE(w->ctx == x->ctx, "aq_matmul: weight and activation belong to different contexts");
     return 0;
 }
@@ -416,7 +416,7 @@ int aq_matmul(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, fl
     int rc = check_matmul(w, x, ncols, y_dev);
     if (rc) return rc;
     AQ_HIP(hipSetDevice(ctx->device));
-    rc = launch_matmul(w->w, x->a, ncols, y_dev, nullptr, ctx->stream);
+    rc = launch_matmul_many(w->w, x->a, ncols, y_dev, nullptr, ctx->stream);
     if (rc) return rc;
     AQ_HIP(hipStreamSynchronize(ctx->stream));
     return 0;
@@ -494,7 +494,7 @@ int aq_matmul_time(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_
     AQ_HIP(hipSetDevice(ctx->device));
     AQ_HIP(hipEventRecord(ctx->ev0, ctx->stream));
     for (int i = 0; i < iters; i++) {
-        int rc = launch_matmul(ws[i % nw]->w, x->a, ncols, y_dev, nullptr, ctx->stream);
+        int rc = launch_matmul_many(ws[i % nw]->w, x->a, ncols, y_dev, nullptr, ctx->stream);
         if (rc) return rc;
     }
     AQ_HIP(hipEventRecord(ctx->ev1, ctx->stream));
@@ -521,7 +521,7 @@ int aq_matmul_time_each(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, cons
     // one event between consecutive launches: launch i's time is the interval between events i and i + 1
     for (int i = 0; !rc && i < iters; i++) {
         if (hipEventRecord(ev[i], ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_matmul_time_each: record");
-        if (!rc) rc = launch_matmul(ws[i % nw]->w, x->a, ncols, y_dev, nullptr, ctx->stream);
+        if (!rc) rc = launch_matmul_many(ws[i % nw]->w, x->a, ncols, y_dev, nullptr, ctx->stream);
     }
     if (!rc && hipEventRecord(ev[iters], ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_matmul_time_each: record");
     if (!rc && hipEventSynchronize(ev[iters]) != hipSuccess) rc = fail(AQ_EHIP, "aq_matmul_time_each: sync");

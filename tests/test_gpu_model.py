@@ -398,3 +398,28 @@ def test_device_argmax_ties_and_nan(ctx):
     assert got == want, f"device {got} reference rule {want}"
     small = np.float32([[np.nan, 1.0], [1.0, np.nan], [2.0, 2.0], [-0.0, 0.0]])
     assert aq.argmax(ctx, small) == [ref_argmax(v) for v in small.tolist()] == [0, 0, 0, 0]
+
+
+def test_tiny_prompt_chunks_equal_token_by_token_and_oracle(ctx, tiny):
+    """A 150-token prompt runs in chunks of 64, 64 and 22 rows (each layer over a whole chunk: matmuls over all its
+    columns, attention and the DeltaNet recurrence in pieces of 8 rows, the conv windows chained piece to piece):
+    the last row's logits and the whole state equal the oracle's prefill and a token-by-token feed, bit for bit
+    (model.rs:443-461, the prefill row i is forward_token on row i)."""
+    print("case tiny 150-token prompt in chunks", flush=True)
+    prompt = np.random.default_rng(SEED + 9).integers(0, tiny["cfg"].vocab, 150).astype(np.uint32)
+    g = aq.State(tiny["gm"], 0, 256)
+    tg, lg = g.prefill(prompt, want_logits=True)
+    o = O.State(tiny["om"], 0, 256)
+    to, lo = o.prefill(prompt, want_logits=True)
+    assert tg == to and np.array_equal(lg, lo), "prefill logits differ from the oracle"
+    assert np.array_equal(g.export(), o.export()), "prefill state differs from the oracle"
+    f = aq.State(tiny["gm"], 0, 256)
+    f.prefill(prompt[:1])
+    for tok in prompt[1:-1]:
+        f.forward_token(int(tok))
+    tf, lf = f.forward_token(int(prompt[-1]), want_logits=True)
+    assert tf == tg and np.array_equal(lf, lg), "prefill differs from the token-by-token feed"
+    assert np.array_equal(f.export(), g.export())
+    for _ in range(4):  # and decoding continues identically
+        tg, tf = g.forward_token(tg), f.forward_token(tf)
+        assert tg == tf
