@@ -40,18 +40,6 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 // Each byte of x (values <= 126) negated, as int8: (0x80 - v) without borrows, then the top bit flipped.
 __device__ __forceinline__ uint32_t neg_bytes(uint32_t x) { return (0x80808080u - x) ^ 0x80808080u; }
 
-// The 6-bit scale and min of sub-block s from a Q4_K / Q5_K record's 12 packed bytes (quant.rs:45-51).
-__device__ __forceinline__ void scale_min(const uint32_t w[3], int s, int &sc, int &m) {
-    const uint8_t *q = reinterpret_cast<const uint8_t *>(w);
-    if (s < 4) {
-        sc = q[s] & 63;
-        m = q[s + 4] & 63;
-    } else {
-        sc = (q[s + 4] & 0xF) | ((q[s - 4] >> 6) << 4);
-        m = (q[s + 4] >> 4) | ((q[s] >> 6) << 4);
-    }
-}
-
 // Balanced base-5 digits (each in -2..2, low digit first) of a signed 8-bit scale, as four signed bytes.
 __device__ __forceinline__ uint32_t digits5(int v) {
     uint32_t out = 0;
@@ -65,9 +53,15 @@ __device__ __forceinline__ uint32_t digits5(int v) {
     }
     return out;
 }
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+// Bytes of x times a small factor f, per byte (every product < 256, so no carry leaves its byte): one packed 16-bit
+// multiply with f in both halves.
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t x, uint32_t f) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, x) * __builtin_bit_cast(u16x2, f * 0x00010001u));
+}
 // The operand bytes x (codes <= 63) times a digit in -2..2.
 __device__ __forceinline__ uint32_t times_digit(uint32_t x, int d) {
-    const uint32_t p = x * (uint32_t)(d < 0 ? -d : d);
+    const uint32_t p = mul_bytes(x, (uint32_t)(d < 0 ? -d : d));
     return d < 0 ? neg_bytes(p) : p;
 }
 
@@ -88,74 +82,111 @@ __device__ __forceinline__ int sdot2(uint32_t a, uint32_t b) {
     typedef short s16x2 __attribute__((ext_vector_type(2)));
     return __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b), 0, false);
 }
-// Two signed bytes of w (byte k and k + 1) as an i16 pair.
-__device__ __forceinline__ uint32_t i8pair(uint32_t w, int k) {
-    const int lo = (int)(int8_t)(w >> (8 * k)), hi = (int)(int8_t)(w >> (8 * k + 8));
-    return ((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16);
+// Signed bytes k, k + 1 of w (k = 0 or 2) as an i16 pair: a byte permute of (w << 8, w) whose sign-fill selectors
+// (10 / 11: bit 15 / 31 of the first source, 8 / 9: of the second) supply each byte's sign.
+__device__ __forceinline__ uint32_t i8pair(uint32_t w, uint32_t w8, int k) {
+    return __builtin_amdgcn_perm(w8, w, k == 0 ? 0x08010A00u : 0x09030B02u);
 }
 
-// What one super-block step of a wave reads: the weight operand's codes (row li, lanes 0..7, sub-blocks 2g and
-// 2g + 1) and its scale record, the scale records of the lane's four output rows, and the column's activation
-// operand, scale and group / sub-block sums. Loaded one super-block ahead of its use.
+// ---- LDS staging ----
+// Operands reach the LDS by direct global-to-LDS copies (global_load_lds_*: each active lane's 16 or 4 bytes land at
+// m0 + 16 * lane or m0 + 4 * lane), issued GEMM_STAGES - 1 steps ahead into a ring of GEMM_STAGES buffers, so the
+// loads' latency is covered without holding the data in registers. Every wave issues the same number of copies per
+// step (a whole wave never skips one), so its count of outstanding vector-memory operations says which step has
+// landed; a work-group barrier after the wait makes every wave's copies of that step visible and, at the same
+// time, frees the buffer read one step earlier for the next copies.
+constexpr int GEMM_STAGES = 3;
+
+__device__ __forceinline__ void dma16(uint32_t lds, const void *g) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(uint32_t lds, const void *g) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+// Wait until at most N of this wave's vector-memory operations are outstanding (and its LDS operations are done),
+// then meet the work-group; one asm statement, so no memory access moves across it.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+
+// One super-block step of a K-quant work-group (16 rows, 4 waves x 16 columns) in the LDS, in 16-byte units:
+//   weight codes: unit c * 4 + k = byte chunk c of row tile k (rows r0 + 4k .. + 3) — the four tiles interleaved,
+//     qa (32 chunks a tile), then qb (Q5_K 8, Q6_K 16 chunks a tile);
+//   scale records: unit W_UNITS - 16 + i = row r0 + i's 16-byte record; Q6_K then the 4 tiles' f16 d (8 B each);
+//   per wave: codes unit q * 16 + c = byte chunk q of column c's super-block (c = 0..15); f32 dx per column;
+//     Q4_K / Q5_K the 8 sub-block sums (16 B) per column, Q6_K the 16 group sums (32 B).
 template <int T>
-struct GemmLd {
-    uint32_t w[8], w2[8], h[8];
-    uint4 sa, se[4];
-    uint32_t d6[4];
-    uint64_t bx[8];
-    float dx;
-    uint4 s8a, s8b;
+struct KqStage { // every W_UNITS / 4 <= 64: one weight copy per wave
+    static constexpr int QB_UNITS = T == AQ_TYPE_Q4_K ? 0 : (T == AQ_TYPE_Q5_K ? 32 : 64);
+    static constexpr int W_UNITS = 128 + QB_UNITS + 16;
+    static constexpr int WL = W_UNITS / 4; // weight units per wave
+    static constexpr int WB = W_UNITS * 16 + (T == AQ_TYPE_Q6_K ? 32 : 0);
+    static constexpr int XSUM = T == AQ_TYPE_Q6_K ? 512 : 256;
+    static constexpr int XB = 4096 + 64 + XSUM;
+    static constexpr int BYTES = WB + 4 * XB;
+    static constexpr int NDMA = T == AQ_TYPE_Q6_K ? 8 : 7; // copies per wave per step
 };
 
 template <int T>
-__device__ __forceinline__ void gemm_load(const GemmArgs &a, GemmLd<T> &L, size_t sb, size_t ra, const int rj[4],
-                                          size_t col, int g) {
+__device__ __forceinline__ void kq_issue(const GemmArgs &a, uint32_t buf, size_t sb, int r0, int c0w, int wave,
+                                         int lane) {
+    using S = KqStage<T>;
     const size_t nb = (size_t)a.nb;
-#pragma unroll
-    for (int l = 0; l < 8; l++) {
-        if constexpr (T == AQ_TYPE_Q6_K) {
-            const uint2 w = *reinterpret_cast<const uint2 *>(a.qa + kq_qa_off(ra, sb, nb, l) + 8 * (g >> 1));
-            L.w[l] = w.x;
-            L.w2[l] = w.y;
-            L.h[l] = *reinterpret_cast<const uint32_t *>(a.qb + kq_qb6_off(ra, sb, nb, l) + 4 * (g >> 1));
+    if (lane < S::WL) {
+        const int u = wave * S::WL + lane;
+        const uint8_t *src;
+        if (u < 128) {
+            src = a.qa + kq_tile((size_t)min(r0 + 4 * (u & 3), a.rows - 1), sb, nb) * 512 + (size_t)(u >> 2) * 16;
+        } else if (u < 128 + S::QB_UNITS) {
+            const int v = u - 128;
+            src = a.qb + kq_tile((size_t)min(r0 + 4 * (v & 3), a.rows - 1), sb, nb) * (S::QB_UNITS * 4) +
+                  (size_t)(v >> 2) * 16;
         } else {
-            L.w[l] = *reinterpret_cast<const uint32_t *>(a.qa + kq_qa_off(ra, sb, nb, l) + 4 * g);
-            if constexpr (T == AQ_TYPE_Q5_K) L.h[l] = *reinterpret_cast<const uint32_t *>(a.qb + kq_qb5_off(ra, sb, nb, l));
+            src = a.sc + kq_sc_off((size_t)min(r0 + u - 128 - S::QB_UNITS, a.rows - 1), sb, nb);
         }
-        L.bx[l] = *reinterpret_cast<const uint64_t *>(a.xq + col * a.n + sb * 256 + (size_t)lane_slot(l) * 32 + 8 * g);
+        dma16(uni(buf + (uint32_t)(wave * S::WL * 16)), src);
     }
-    L.sa = *reinterpret_cast<const uint4 *>(a.sc + kq_sc_off(ra, sb, nb));
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        L.se[j] = *reinterpret_cast<const uint4 *>(a.sc + kq_sc_off((size_t)rj[j], sb, nb));
-        if constexpr (T == AQ_TYPE_Q6_K) L.d6[j] = *reinterpret_cast<const uint16_t *>(a.dm + kq_dm_off((size_t)rj[j], sb, nb));
-    }
-    L.dx = a.xd[col * nb + sb];
     if constexpr (T == AQ_TYPE_Q6_K) {
-        L.s8a = reinterpret_cast<const uint4 *>(a.xbs + (col * nb + sb) * 16)[0];
-        L.s8b = reinterpret_cast<const uint4 *>(a.xbs + (col * nb + sb) * 16)[1];
+        if (lane < 2) {
+            const int d = 2 * wave + lane; // tile d >> 1, its rows 2 (d & 1) .. + 1
+            dma4(uni(buf + (uint32_t)(S::W_UNITS * 16 + wave * 8)),
+                 a.dm + kq_tile((size_t)min(r0 + 4 * (d >> 1), a.rows - 1), sb, nb) * 8 + 4 * (d & 1));
+        }
+    }
+    const uint32_t xw = buf + (uint32_t)(S::WB + wave * S::XB);
+    const size_t col = (size_t)min(c0w + (lane & 15), a.ncols - 1);
+    const int8_t *xs = a.xq + col * a.n + sb * 256;
+#pragma unroll
+    for (int i = 0; i < 4; i++) dma16(uni(xw + (uint32_t)(i * 1024)), xs + (size_t)(i * 4 + (lane >> 4)) * 16);
+    if (lane < 16) dma4(uni(xw + 4096), a.xd + col * nb + sb);
+    if constexpr (T == AQ_TYPE_Q6_K) {
+        if (lane < 32) {
+            const size_t c2 = (size_t)min(c0w + (lane >> 1), a.ncols - 1);
+            dma16(uni(xw + 4160), a.xbs + (c2 * nb + sb) * 16 + 8 * (lane & 1));
+        }
     } else {
-        L.s8a = *reinterpret_cast<const uint4 *>(a.xq8s + (col * nb + sb) * 8);
+        if (lane < 16) dma16(uni(xw + 4160), a.xq8s + (col * nb + sb) * 8);
     }
 }
 
-// K-quant x Q8_K, one 16-row x 16-column tile per wave: the work-group's four waves take four column tiles of the
-// same rows (their weight reads share the caches).
+// K-quant x Q8_K: a work-group owns 16 rows x 64 columns, wave w the 16 x 16 tile of columns c0 + 16w; lane
+// (li = lane & 15, g = lane >> 4) feeds weight row li / column li into the products (k-group g = sub-blocks 2g,
+// 2g + 1 of each lane slot) and owns the outputs of rows 4g .. 4g + 3 in column li.
 template <int T>
-__global__ void __launch_bounds__(256) kq_gemm_kernel(GemmArgs a) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) kq_gemm_kernel(GemmArgs a) {
+    using S = KqStage<T>;
     constexpr int ND = T == AQ_TYPE_Q4_K ? 2 : (T == AQ_TYPE_Q5_K ? 3 : 4); // digits
     constexpr int BASE = T == AQ_TYPE_Q4_K ? 8 : (T == AQ_TYPE_Q5_K ? 4 : 5);
+    extern __shared__ __align__(16) uint8_t gm_lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int g = lane >> 4, li = lane & 15;
+    const int g = lane >> 4, li = lane & 15, k4 = li >> 2, r4 = li & 3;
     const int r0 = (int)blockIdx.x * 16;
-    const int c0 = ((int)blockIdx.y * 4 + wave) * 16;
-    if (c0 >= a.ncols) return; // whole waves past the end (no barriers in this kernel)
-    const size_t nb = (size_t)a.nb;
-    const size_t ra = (size_t)min(r0 + li, a.rows - 1); // this lane's weight-operand row
-    int rj[4];                                           // the rows of this lane's outputs: 4g + j
-#pragma unroll
-    for (int j = 0; j < 4; j++) rj[j] = min(r0 + 4 * g + j, a.rows - 1);
-    const size_t col = (size_t)min(c0 + li, a.ncols - 1);
+    const int c0w = (int)blockIdx.y * 64 + wave * 16;
+    const bool live = c0w < a.ncols; // a wave past the last column copies and waits but computes nothing
+    const int nb = a.nb;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)gm_lds;
 
     float acc[4][8], accm[4][4];
 #pragma unroll
@@ -165,15 +196,62 @@ __global__ void __launch_bounds__(256) kq_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) accm[j][i] = 0.0f;
     }
-    GemmLd<T> cur, nxt;
-    gemm_load<T>(a, cur, 0, ra, rj, col, g);
-    for (size_t sb = 0; sb < nb; sb++) {
-        gemm_load<T>(a, nxt, sb + 1 < nb ? sb + 1 : sb, ra, rj, col, g); // in flight during this step
+#pragma unroll
+    for (int s = 0; s < GEMM_STAGES - 1; s++)
+        if (s < nb) kq_issue<T>(a, lds0 + (uint32_t)(s * S::BYTES), (size_t)s, r0, c0w, wave, lane);
+
+    for (int sb = 0; sb < nb; sb++) {
+        if (sb + GEMM_STAGES - 2 < nb) wait_vm_barrier<(GEMM_STAGES - 2) * S::NDMA>();
+        else wait_vm_barrier<0>();
+        if (sb + GEMM_STAGES - 1 < nb)
+            kq_issue<T>(a, lds0 + (uint32_t)(((sb + GEMM_STAGES - 1) % GEMM_STAGES) * S::BYTES),
+                        (size_t)(sb + GEMM_STAGES - 1), r0, c0w, wave, lane);
+        if (!live) continue;
+        const uint8_t *W = gm_lds + (sb % GEMM_STAGES) * S::BYTES;
+        const uint8_t *X = W + S::WB + wave * S::XB;
+        const uint8_t *SC = W + (S::W_UNITS - 16) * 16;
+
+        // every LDS operand of the step, read up front: the weight codes of row li (lane slots 0..7), the column's
+        // activation codes, the scale records of row li and of the output rows 4g .. 4g + 3, dx and the sums
+        uint32_t wa[8], wb[8], wh[8];
+        uint64_t bx[8];
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const int h = l >> 2, p = l & 3;
+            const int cq = h * 16 + p * 4 + r4; // the lane's qa chunk in its row tile
+            if constexpr (T == AQ_TYPE_Q6_K) {
+                const uint2 w = *reinterpret_cast<const uint2 *>(W + (cq * 4 + k4) * 16 + 8 * (g >> 1));
+                wa[l] = w.x;
+                wb[l] = w.y;
+                wh[l] = *reinterpret_cast<const uint32_t *>(W + 2048 + ((p * 4 + r4) * 4 + k4) * 16 + h * 8 + 4 * (g >> 1));
+            } else {
+                wa[l] = *reinterpret_cast<const uint32_t *>(W + (cq * 4 + k4) * 16 + 4 * g);
+                if constexpr (T == AQ_TYPE_Q5_K) {
+                    const int e = p * 4 + r4;
+                    wh[l] = *reinterpret_cast<const uint32_t *>(W + 2048 + ((e >> 1) * 4 + k4) * 16 + (e & 1) * 8 + h * 4);
+                }
+            }
+            bx[l] = *reinterpret_cast<const uint64_t *>(X + ((lane_slot(l) * 2 + (g >> 1)) * 16 + li) * 16 + 8 * (g & 1));
+        }
+        const uint4 sa = *reinterpret_cast<const uint4 *>(SC + li * 16);
+        uint4 se[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) se[j] = *reinterpret_cast<const uint4 *>(SC + (4 * g + j) * 16);
+        const float dx = *reinterpret_cast<const float *>(X + 4096 + 4 * li);
+        uint4 xs0, xs1;
+        uint2 d6;
+        if constexpr (T == AQ_TYPE_Q6_K) {
+            d6 = *reinterpret_cast<const uint2 *>(W + S::W_UNITS * 16 + 8 * g);
+            xs0 = *reinterpret_cast<const uint4 *>(X + 4160 + 32 * li);
+            xs1 = *reinterpret_cast<const uint4 *>(X + 4160 + 32 * li + 16);
+        } else {
+            xs0 = *reinterpret_cast<const uint4 *>(X + 4160 + 16 * li);
+        }
 
         // the weight operand's digits: the scales of sub-blocks 2g and 2g + 1 (Q6_K: per lane half, l < 4 / l >= 4)
         int dga[ND], dgb[ND], dgc[ND], dgd[ND];
         if constexpr (T == AQ_TYPE_Q6_K) {
-            const uint32_t sw = g == 0 ? cur.sa.x : g == 1 ? cur.sa.y : g == 2 ? cur.sa.z : cur.sa.w;
+            const uint32_t sw = g == 0 ? sa.x : g == 1 ? sa.y : g == 2 ? sa.z : sa.w;
             const uint32_t da = digits5((int8_t)sw), dc = digits5((int8_t)(sw >> 8));
             const uint32_t db = digits5((int8_t)(sw >> 16)), dd = digits5((int8_t)(sw >> 24));
 #pragma unroll
@@ -184,10 +262,11 @@ __global__ void __launch_bounds__(256) kq_gemm_kernel(GemmArgs a) {
                 dgd[i] = (int8_t)(dd >> (8 * i));
             }
         } else {
-            const uint32_t w3[3] = {cur.sa.y, cur.sa.z, cur.sa.w};
-            int sca, scb, mdum;
-            scale_min(w3, 2 * g, sca, mdum);
-            scale_min(w3, 2 * g + 1, scb, mdum);
+            // 6-bit scales of sub-blocks 2g, 2g + 1 (quant.rs:45-51): bytes 2g, 2g + 1 of the low or high word
+            const uint32_t sc_lo = sa.y & 0x3F3F3F3Fu;
+            const uint32_t sc_hi = (sa.w & 0x0F0F0F0Fu) | ((sa.y >> 2) & 0x30303030u);
+            const uint32_t scw = g < 2 ? sc_lo : sc_hi;
+            const int sca = (int)((scw >> (16 * (g & 1))) & 0xFF), scb = (int)((scw >> (16 * (g & 1) + 8)) & 0xFF);
             constexpr int BB = T == AQ_TYPE_Q4_K ? 3 : 2;
 #pragma unroll
             for (int i = 0; i < ND; i++) {
@@ -196,80 +275,84 @@ __global__ void __launch_bounds__(256) kq_gemm_kernel(GemmArgs a) {
             }
         }
 
-        // the exact lane sums of the tile: sumi[l][j] for output rows 4g + j of this lane's column
-        int sumi[8][4];
+        // the codes of sub-blocks 2g (lo) and 2g + 1 (hi) per lane slot, as unsigned bytes
+        uint32_t lo[8], hi[8];
 #pragma unroll
         for (int l = 0; l < 8; l++) {
-            uint32_t lo, hi;
             if constexpr (T == AQ_TYPE_Q6_K) {
                 const int sh = 4 * (g & 1);
-                lo = ((cur.w[l] >> sh) & 0x0F0F0F0Fu) | (((cur.h[l] >> sh) & 0x03030303u) << 4);
-                hi = ((cur.w2[l] >> sh) & 0x0F0F0F0Fu) | (((cur.h[l] >> (sh + 2)) & 0x03030303u) << 4);
+                lo[l] = ((wa[l] >> sh) & 0x0F0F0F0Fu) | (((wh[l] >> sh) & 0x03030303u) << 4);
+                hi[l] = ((wb[l] >> sh) & 0x0F0F0F0Fu) | (((wh[l] >> (sh + 2)) & 0x03030303u) << 4);
             } else {
-                lo = cur.w[l] & 0x0F0F0F0Fu;
-                hi = (cur.w[l] >> 4) & 0x0F0F0F0Fu;
+                lo[l] = wa[l] & 0x0F0F0F0Fu;
+                hi[l] = (wa[l] >> 4) & 0x0F0F0F0Fu;
                 if constexpr (T == AQ_TYPE_Q5_K) {
-                    lo |= ((cur.h[l] >> (2 * g)) & 0x01010101u) << 4;
-                    hi |= ((cur.h[l] >> (2 * g + 1)) & 0x01010101u) << 4;
+                    lo[l] |= ((wh[l] >> (2 * g)) & 0x01010101u) << 4;
+                    hi[l] |= ((wh[l] >> (2 * g + 1)) & 0x01010101u) << 4;
                 }
             }
-            const int *da = l < 4 ? dga : dgc, *db = l < 4 ? dgb : dgd;
-            v4i c = {0, 0, 0, 0};
+        }
+
+        // the exact lane sums of the tile, digit by digit over all eight lane slots (eight independent products in
+        // flight): c[l][j] = lane l's sum for output row 4g + j of this lane's column
+        v4i c[8];
 #pragma unroll
-            for (int i = ND - 1; i >= 0; i--) {
-                if (i < ND - 1) {
+        for (int i = ND - 1; i >= 0; i--) {
 #pragma unroll
-                    for (int e = 0; e < 4; e++) c[e] *= BASE;
-                }
+            for (int l = 0; l < 8; l++) {
+                const int *da = l < 4 ? dga : dgc, *db = l < 4 ? dgb : dgd;
                 uint32_t alo, ahi;
                 if constexpr (T == AQ_TYPE_Q6_K) {
-                    alo = times_digit(lo, da[i]);
-                    ahi = times_digit(hi, db[i]);
+                    alo = times_digit(lo[l], da[i]);
+                    ahi = times_digit(hi[l], db[i]);
                 } else {
-                    alo = lo * (uint32_t)da[i];
-                    ahi = hi * (uint32_t)db[i];
+                    alo = mul_bytes(lo[l], (uint32_t)da[i]);
+                    ahi = mul_bytes(hi[l], (uint32_t)db[i]);
                 }
-                c = mma(pack2(alo, ahi), cur.bx[l], c);
-            }
+                v4i cin = {0, 0, 0, 0};
+                if (i < ND - 1) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) sumi[l][j] = c[j];
+                    for (int e = 0; e < 4; e++) cin[e] = c[l][e] * BASE;
+                }
+                c[l] = mma(pack2(alo, ahi), bx[l], cin);
+            }
         }
 
         // the f32 chains of the lane's four outputs (kdot.rs:37-140), in super-block order
-        const float dx = cur.dx;
+        if constexpr (T == AQ_TYPE_Q6_K) {
+            const uint32_t bsw[8] = {xs0.x, xs0.y, xs0.z, xs0.w, xs1.x, xs1.y, xs1.z, xs1.w};
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            if constexpr (T == AQ_TYPE_Q6_K) {
-                const float d = dx * h2f(cur.d6[j]);
-                const uint32_t sw[4] = {cur.se[j].x, cur.se[j].y, cur.se[j].z, cur.se[j].w};
-                const uint32_t bsw[8] = {cur.s8a.x, cur.s8a.y, cur.s8a.z, cur.s8a.w,
-                                         cur.s8b.x, cur.s8b.y, cur.s8b.z, cur.s8b.w};
+            for (int j = 0; j < 4; j++) {
+                const uint32_t sw[4] = {se[j].x, se[j].y, se[j].z, se[j].w};
+                const float d = dx * h2f((j < 2 ? d6.x : d6.y) >> (16 * (j & 1)));
 #pragma unroll
                 for (int l = 0; l < 8; l++) {
                     // kdot.rs:125-129: lane l less 32 * (bs[2l] sc[2l] + bs[2l + 1] sc[2l + 1])
-                    const int off = sdot2(bsw[l], i8pair(sw[l >> 1], 2 * (l & 1)));
-                    acc[j][l] += d * (float)(sumi[l][j] - 32 * off);
+                    const int off = sdot2(bsw[l], i8pair(sw[l >> 1], sw[l >> 1] << 8, 2 * (l & 1)));
+                    acc[j][l] += d * (float)(c[l][j] - 32 * off);
                 }
-            } else {
-                const float d = dx * h2f(cur.se[j].x), dmin = -dx * h2f(cur.se[j].x >> 16);
-                // the 8 mins as bytes (quant.rs:45-51): sub-blocks 0..3 from bytes 4..7, 4..7 from bytes 8..11 + 0..3
-                const uint32_t mlo = cur.se[j].z & 0x3F3F3F3Fu;
-                const uint32_t mhi = ((cur.se[j].w >> 4) & 0x0F0F0F0Fu) | ((cur.se[j].z >> 2) & 0x30303030u);
-                const uint32_t q8w[4] = {cur.s8a.x, cur.s8a.y, cur.s8a.z, cur.s8a.w};
+            }
+        } else {
+            const uint32_t q8w[4] = {xs0.x, xs0.y, xs0.z, xs0.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float d = dx * h2f(se[j].x), dmin = -dx * h2f(se[j].x >> 16);
+                // the 8 mins as bytes (quant.rs:45-51): sub-blocks 0..3 from bytes 4..7, 4..7 from bytes 8..11 + 4..7
+                const uint32_t mlo = se[j].z & 0x3F3F3F3Fu;
+                const uint32_t mhi = ((se[j].w >> 4) & 0x0F0F0F0Fu) | ((se[j].z >> 2) & 0x30303030u);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const uint32_t m2 = __builtin_amdgcn_perm(0u, i < 2 ? mlo : mhi, (i & 1) ? 0x0C030C02u : 0x0C010C00u);
                     accm[j][i] += dmin * (float)sdot2(m2, q8w[i]); // m[2i] q8s[2i] + m[2i+1] q8s[2i+1]
                 }
 #pragma unroll
-                for (int l = 0; l < 8; l++) acc[j][l] += d * (float)sumi[l][j];
+                for (int l = 0; l < 8; l++) acc[j][l] += d * (float)c[l][j];
             }
         }
-        cur = nxt;
     }
 
-    const int ocol = c0 + li;
-    if (ocol < a.ncols) {
+    const int ocol = c0w + li;
+    if (live && ocol < a.ncols) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int row = r0 + 4 * g + j;
@@ -286,45 +369,109 @@ __global__ void __launch_bounds__(256) kq_gemm_kernel(GemmArgs a) {
     }
 }
 
-// Q8_0 / Q4_0 weights x Q8_0 activations: one block per product, on the same tiles (eight waves per SIMD hide the
-// loads' latency).
+// One step of a Q8_0 / Q4_0 work-group = 8 blocks (256 elements), in 16-byte units: codes unit q * 16 + i = byte
+// chunk q of row r0 + i's 8 blocks (Q8_0: 16 chunks, Q4_0: 8), then row i's 8 f16 d at unit NQ + i; per wave the
+// activation codes as for the K-quants, then each column's 8 f32 d (32 B) and, for Q4_0, its 8 i32 code sums.
 template <int T>
-__global__ void __launch_bounds__(256) q8_gemm_kernel(GemmArgs a) {
+struct Q8Stage {
+    static constexpr int QC = T == AQ_TYPE_Q8_0 ? 16 : 8; // code chunks per row
+    static constexpr int W_UNITS = 16 * QC + 16;
+    static constexpr int WL = W_UNITS / 4;          // weight units per wave
+    static constexpr int WI = (WL + 63) / 64;       // copies they take
+    static constexpr int WB = W_UNITS * 16;
+    static constexpr int XB = 4096 + 512 + (T == AQ_TYPE_Q4_0 ? 512 : 0);
+    static constexpr int BYTES = WB + 4 * XB;
+    static constexpr int NDMA = WI + 5 + (T == AQ_TYPE_Q4_0 ? 1 : 0);
+};
+
+template <int T>
+__device__ __forceinline__ void q8_issue(const GemmArgs &a, uint32_t buf, size_t st, int r0, int c0w, int wave,
+                                         int lane) {
+    using S = Q8Stage<T>;
+    const size_t nb = (size_t)a.nb; // 32-blocks per row
+#pragma unroll
+    for (int i = 0; i < S::WI; i++) {
+        if (i * 64 + lane < S::WL) { // every copy has active lanes: WL > 64 (WI - 1)
+            const int u = wave * S::WL + i * 64 + lane;
+            const uint8_t *src;
+            if (u < 16 * S::QC) {
+                const size_t row = (size_t)min(r0 + (u & 15), a.rows - 1);
+                src = a.qa + (row * nb + st * 8) * (S::QC * 2) + (size_t)(u >> 4) * 16;
+            } else {
+                const size_t row = (size_t)min(r0 + u - 16 * S::QC, a.rows - 1);
+                src = a.dm + (row * nb + st * 8) * 2;
+            }
+            dma16(uni(buf + (uint32_t)((wave * S::WL + i * 64) * 16)), src);
+        }
+    }
+    const uint32_t xw = buf + (uint32_t)(S::WB + wave * S::XB);
+    const size_t col = (size_t)min(c0w + (lane & 15), a.ncols - 1);
+    const int8_t *xs = a.xq + col * a.n + st * 256;
+#pragma unroll
+    for (int i = 0; i < 4; i++) dma16(uni(xw + (uint32_t)(i * 1024)), xs + (size_t)(i * 4 + (lane >> 4)) * 16);
+    const size_t c2 = (size_t)min(c0w + (lane >> 1), a.ncols - 1);
+    if (lane < 32) dma16(uni(xw + 4096), a.xd + c2 * nb + st * 8 + 4 * (lane & 1));
+    if constexpr (T == AQ_TYPE_Q4_0) {
+        if (lane < 32) dma16(uni(xw + 4608), a.xs0 + c2 * nb + st * 8 + 4 * (lane & 1));
+    }
+}
+
+// Q8_0 / Q4_0 weights x Q8_0 activations: the same work-group and lane roles; one product over K = 32 per block.
+template <int T>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) q8_gemm_kernel(GemmArgs a) {
+    using S = Q8Stage<T>;
+    extern __shared__ __align__(16) uint8_t gm_lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, li = lane & 15;
     const int r0 = (int)blockIdx.x * 16;
-    const int c0 = ((int)blockIdx.y * 4 + wave) * 16;
-    if (c0 >= a.ncols) return;
-    const size_t nb = (size_t)a.nb; // 32-blocks per row
-    const size_t ra = (size_t)min(r0 + li, a.rows - 1);
-    int rj[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) rj[j] = min(r0 + 4 * g + j, a.rows - 1);
-    const size_t col = (size_t)min(c0 + li, a.ncols - 1);
-    constexpr int BB = T == AQ_TYPE_Q8_0 ? 32 : 16; // code bytes per block
+    const int c0w = (int)blockIdx.y * 64 + wave * 16;
+    const bool live = c0w < a.ncols;
+    const int nst = a.nb / 8; // steps
+    const uint32_t lds0 = (uint32_t)(uintptr_t)gm_lds;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto load_w = [&](size_t b) -> uint64_t {
-        if constexpr (T == AQ_TYPE_Q8_0) return *reinterpret_cast<const uint64_t *>(a.qa + (ra * nb + b) * BB + 8 * g);
-        // elements 8g .. 8g + 7: bytes 8 (g & 1) .., low nibbles for g < 2, high for g >= 2
-        const uint64_t w = *reinterpret_cast<const uint64_t *>(a.qa + (ra * nb + b) * BB + 8 * (g & 1));
-        return (w >> (4 * (g >> 1))) & 0x0F0F0F0F0F0F0F0Full;
-    };
-    for (size_t b = 0; b < nb; b++) {
-        const uint64_t wa = load_w(b);
-        const uint64_t bx = *reinterpret_cast<const uint64_t *>(a.xq + col * a.n + b * 32 + 8 * g);
-        float dw[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) dw[j] = h2f(*reinterpret_cast<const uint16_t *>(a.dm + ((size_t)rj[j] * nb + b) * 2));
-        const float dx = a.xd[col * nb + b];
-        int off = 0;
-        if constexpr (T == AQ_TYPE_Q4_0) off = 8 * a.xs0[col * nb + b]; // dot.rs:48-66: codes less 8
-        v4i c = {0, 0, 0, 0};
-        c = mma(wa, bx, c);
+    for (int s = 0; s < GEMM_STAGES - 1; s++)
+        if (s < nst) q8_issue<T>(a, lds0 + (uint32_t)(s * S::BYTES), (size_t)s, r0, c0w, wave, lane);
+
+    for (int st = 0; st < nst; st++) {
+        if (st + GEMM_STAGES - 2 < nst) wait_vm_barrier<(GEMM_STAGES - 2) * S::NDMA>();
+        else wait_vm_barrier<0>();
+        if (st + GEMM_STAGES - 1 < nst)
+            q8_issue<T>(a, lds0 + (uint32_t)(((st + GEMM_STAGES - 1) % GEMM_STAGES) * S::BYTES),
+                        (size_t)(st + GEMM_STAGES - 1), r0, c0w, wave, lane);
+        if (!live) continue;
+        const uint8_t *W = gm_lds + (st % GEMM_STAGES) * S::BYTES;
+        const uint8_t *X = W + S::WB + wave * S::XB;
+        uint4 dwr[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[j] += (dw[j] * dx) * (float)(c[j] - off);
+        for (int j = 0; j < 4; j++) dwr[j] = *reinterpret_cast<const uint4 *>(W + (16 * S::QC + 4 * g + j) * 16);
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            uint64_t wa;
+            if constexpr (T == AQ_TYPE_Q8_0) {
+                wa = *reinterpret_cast<const uint64_t *>(W + ((2 * b + (g >> 1)) * 16 + li) * 16 + 8 * (g & 1));
+            } else {
+                // elements 8g .. 8g + 7: bytes 8 (g & 1) .., low nibbles for g < 2, high for g >= 2
+                const uint64_t w = *reinterpret_cast<const uint64_t *>(W + (b * 16 + li) * 16 + 8 * (g & 1));
+                wa = (w >> (4 * (g >> 1))) & 0x0F0F0F0F0F0F0F0Full;
+            }
+            const uint64_t bx =
+                *reinterpret_cast<const uint64_t *>(X + ((2 * b + (g >> 1)) * 16 + li) * 16 + 8 * (g & 1));
+            const float dx = *reinterpret_cast<const float *>(X + 4096 + 32 * li + 4 * b);
+            int off = 0;
+            if constexpr (T == AQ_TYPE_Q4_0) // dot.rs:48-66: codes less 8
+                off = 8 * *reinterpret_cast<const int32_t *>(X + 4608 + 32 * li + 4 * b);
+            v4i c = {0, 0, 0, 0};
+            c = mma(wa, bx, c);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t dww = (b >> 1) == 0 ? dwr[j].x : (b >> 1) == 1 ? dwr[j].y : (b >> 1) == 2 ? dwr[j].z : dwr[j].w;
+                acc[j] += (h2f(dww >> (16 * (b & 1))) * dx) * (float)(c[j] - off);
+            }
+        }
     }
-    const int ocol = c0 + li;
-    if (ocol < a.ncols) {
+    const int ocol = c0w + li;
+    if (live && ocol < a.ncols) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int row = r0 + 4 * g + j;
@@ -335,17 +482,17 @@ __global__ void __launch_bounds__(256) q8_gemm_kernel(GemmArgs a) {
     }
 }
 
-template <int T>
-int launch_kq_t(const GemmArgs &ga, hipStream_t stream) {
+template <typename K>
+int launch_staged(K kernel, int bytes, const GemmArgs &ga, hipStream_t stream, const char *what) {
     const dim3 grid((unsigned)((ga.rows + 15) / 16), (unsigned)((ga.ncols + 63) / 64));
-    hipLaunchKernelGGL((kq_gemm_kernel<T>), grid, dim3(256), 0, stream, ga);
-    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_gemm launch");
-}
-template <int T>
-int launch_q8_t(const GemmArgs &ga, hipStream_t stream) {
-    const dim3 grid((unsigned)((ga.rows + 15) / 16), (unsigned)((ga.ncols + 63) / 64));
-    hipLaunchKernelGGL((q8_gemm_kernel<T>), grid, dim3(256), 0, stream, ga);
-    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "q8_gemm launch");
+    const size_t lds = (size_t)bytes * GEMM_STAGES;
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return fail(AQ_EHIP, what);
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(256), lds, stream, ga);
+    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, what);
 }
 
 } // namespace
@@ -372,18 +519,22 @@ int launch_gemm(const Weight &w, const Act &x, size_t ncols, float *y, const flo
         ga.xbs = x.bs;
         ga.xq8s = x.q8s;
         switch (w.type) {
-        case AQ_TYPE_Q4_K: return launch_kq_t<AQ_TYPE_Q4_K>(ga, stream);
-        case AQ_TYPE_Q5_K: return launch_kq_t<AQ_TYPE_Q5_K>(ga, stream);
-        default: return launch_kq_t<AQ_TYPE_Q6_K>(ga, stream);
+        case AQ_TYPE_Q4_K:
+            return launch_staged(kq_gemm_kernel<AQ_TYPE_Q4_K>, KqStage<AQ_TYPE_Q4_K>::BYTES, ga, stream, "kq_gemm launch");
+        case AQ_TYPE_Q5_K:
+            return launch_staged(kq_gemm_kernel<AQ_TYPE_Q5_K>, KqStage<AQ_TYPE_Q5_K>::BYTES, ga, stream, "kq_gemm launch");
+        default:
+            return launch_staged(kq_gemm_kernel<AQ_TYPE_Q6_K>, KqStage<AQ_TYPE_Q6_K>::BYTES, ga, stream, "kq_gemm launch");
         }
     }
     AQ_REQUIRE(w.type == AQ_TYPE_Q8_0 || w.type == AQ_TYPE_Q4_0, "gemm: weight type");
-    AQ_REQUIRE(w.cols % 32 == 0, "gemm: Q8_0 / Q4_0 columns must be a multiple of 32");
+    AQ_REQUIRE(w.cols % 256 == 0, "gemm: Q8_0 / Q4_0 columns must be a multiple of 256");
     ga.xq = x.q0;
     ga.xd = x.d0;
     ga.xs0 = x.s0;
-    if (w.type == AQ_TYPE_Q8_0) return launch_q8_t<AQ_TYPE_Q8_0>(ga, stream);
-    return launch_q8_t<AQ_TYPE_Q4_0>(ga, stream);
+    if (w.type == AQ_TYPE_Q8_0)
+        return launch_staged(q8_gemm_kernel<AQ_TYPE_Q8_0>, Q8Stage<AQ_TYPE_Q8_0>::BYTES, ga, stream, "q8_gemm launch");
+    return launch_staged(q8_gemm_kernel<AQ_TYPE_Q4_0>, Q8Stage<AQ_TYPE_Q4_0>::BYTES, ga, stream, "q8_gemm launch");
 }
 
 } // namespace aq

@@ -497,9 +497,10 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
 
 int launch_matmul_many(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream) {
     if (ncols <= 8) return launch_matmul(w, x, ncols, y, resid, stream);
-    if ((is_kquant(w.type) && !q8_fine()) || w.type == AQ_TYPE_Q8_0 || w.type == AQ_TYPE_Q4_0)
+    if ((is_kquant(w.type) && !q8_fine()) || ((w.type == AQ_TYPE_Q8_0 || w.type == AQ_TYPE_Q4_0) && w.cols % 256 == 0))
         return launch_gemm(w, x, ncols, y, resid, stream);
-    for (size_t c0 = 0; c0 < ncols; c0 += 8) { // F32 weights, and K-quants under the q8-fine switch
+    // F32 weights, K-quants under the q8-fine switch, Q8_0 / Q4_0 rows not a multiple of 256 long
+    for (size_t c0 = 0; c0 < ncols; c0 += 8) {
         const size_t tc = ncols - c0 < 8 ? ncols - c0 : 8;
         Act v = x;
         v.ncols = x.ncols - c0;

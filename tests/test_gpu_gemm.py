@@ -69,3 +69,12 @@ def test_gemm_columns_equal_single_column_kernel(ctx, t, rows, cols):
     # and a few columns straight against the oracle
     want = O.matmul(t, host, rows, cols, x[[0, ncols // 2, ncols - 1]], threads=8)
     assert np.array_equal(bits(y[[0, ncols // 2, ncols - 1]]), bits(want))
+
+
+@pytest.mark.parametrize("t", [aq.Q8_0, aq.Q4_0])
+def test_rows_not_a_multiple_of_256_take_column_pieces(ctx, t):
+    rows, cols, ncols = 45, 160, 20
+    print(f"case gemm pieces type {t} {rows}x{cols} N={ncols}", flush=True)
+    host, w, a, x, y = run(ctx, t, rows, cols, ncols, 77 + t)
+    want = O.matmul(t, host, rows, cols, x, threads=8)
+    assert np.array_equal(bits(y), bits(want))
