@@ -148,7 +148,7 @@ __global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
     int8_t *sx = reinterpret_cast<int8_t *>(q8_lds);                   // [nb][XS]: column c at c * 32
     float *sxd = reinterpret_cast<float *>(q8_lds + (size_t)nb * XS);  // [NC][nb]
     int32_t *sxs = reinterpret_cast<int32_t *>(sxd + (size_t)nb * NC); // [NC][nb]
-    float *xch = reinterpret_cast<float *>(sxs + (size_t)nb * NC);     // [waves][NC][RPW rows][KS]
+    float *xch = reinterpret_cast<float *>(sxs + (size_t)nb * NC);     // [waves][NC][RPW rows][KS + 1]
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int r = lane / KS, ks = lane % KS;
     const int nwv = (int)(blockDim.x >> 6); // waves per work-group
@@ -211,7 +211,9 @@ __global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
     }
     __syncthreads();
     if (row0 >= a.rows) return; // no barrier follows
-    float *xw = xch + (size_t)wid * NC * 64;
+    // one float of padding per (column, row) record: the chain owners' reads fall in different banks
+    constexpr int KP = KS + 1;
+    float *xw = xch + (size_t)wid * NC * RPW * KP;
     const int oc = lane / RPW, orr = lane % RPW; // as a chain owner (lane < RPW * NC): column oc, row orr
     float acc = 0.0f;
     const int nr = (nb + KS - 1) / KS;
@@ -249,11 +251,11 @@ __global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int c = 0; c < NC; c++) xw[(c * RPW + r) * KS + ks] = pr[c];
+        for (int c = 0; c < NC; c++) xw[(c * RPW + r) * KP + ks] = pr[c];
         __asm__ volatile("" ::: "memory");
         if (lane < RPW * NC) {
             const int live = nb - rd * KS < KS ? nb - rd * KS : KS;
-            const float *pv = xw + (oc * RPW + orr) * KS;
+            const float *pv = xw + (oc * RPW + orr) * KP;
 #pragma unroll
             for (int u0 = 0; u0 < KS; u0 += 16) { // 16 reads in flight, the sum in block order
                 float v[16];
@@ -422,6 +424,14 @@ inline long q8_capacity(const void *fn, int threads, size_t lds) {
     return cache[key] = (long)per_cu * cus;
 }
 
+// Compute units of the current device (0 if the query fails).
+inline long q8_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 1;
+    return cus > 0 ? cus : 1;
+}
+
 template <int NC>
 int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
     if (args.type == AQ_TYPE_F32) {
@@ -432,7 +442,8 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
     }
     {
         // the wave kernel: activations staged in LDS
-        const size_t stage = (size_t)args.nb32 * (q8w_xs(NC) + NC * 8), xw = (size_t)NC * 64 * 4; // per wave
+        // per wave: NC x RPW records of 64 / RPW + 1 floats (at most NC * 68)
+        const size_t stage = (size_t)args.nb32 * (q8w_xs(NC) + NC * 8), xw = (size_t)NC * 68 * 4;
         if (stage + 4 * xw <= 64 * 1024) {
             // rows per wave: the most that still give the grid about four waves per SIMD (one column: two rows
             // from 4096, measured faster for the MTP's Q4_0 matrices)
@@ -445,14 +456,19 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
             const void *k1[2] = {(const void *)&q8_wave_kernel<AQ_TYPE_Q8_0, NC, 1>,
                                  (const void *)&q8_wave_kernel<AQ_TYPE_Q4_0, NC, 1>};
             const void *fn = (rpw == 4 ? k4 : rpw == 2 ? k2 : k1)[q4 ? 1 : 0];
-            // waves per work-group: the largest of 16, 8, 4 whose grid is resident in one pass
+            // waves per work-group: of 16, 8, 4 (grids resident in one pass), the one whose busiest CU holds the
+            // fewest waves (work-groups are dealt to the CUs in turn), the larger on a tie (less staging)
             int nwv = 4;
-            for (int w : {16, 8}) {
+            long best = -1;
+            const long cus = q8_cus();
+            for (int w : {16, 8, 4}) {
                 const size_t lds = stage + w * xw;
                 const long grid = (args.rows + (long)w * rpw - 1) / ((long)w * rpw);
-                if (lds <= 64 * 1024 && grid <= q8_capacity(fn, 64 * w, lds)) {
+                if (lds > 64 * 1024 || grid > q8_capacity(fn, 64 * w, lds)) continue;
+                const long busiest = (grid + cus - 1) / cus * w;
+                if (best < 0 || busiest < best) {
+                    best = busiest;
                     nwv = w;
-                    break;
                 }
             }
             const size_t lds = stage + nwv * xw;
