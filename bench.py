@@ -56,6 +56,7 @@ def parse():
     ap.add_argument("--forced-rounds", type=int, default=48)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel timing (for counter runs)")
+    ap.add_argument("--sweep-only", action="store_true", help="only the matmul sweep (for kernel-trace runs)")
     return ap.parse_args()
 
 
@@ -90,12 +91,16 @@ def kernel_roofline(ctx, k):
 
 def kernel_sweep(ctx):
     """The matvec (N = 1) and the blocked verify op (N = k+1 in {2, 4, 6, 8}) on the single-op shapes: Q4_K
-    17408 x 5120 and Q6_K 5120 x 17408 over 8 distinct weights each (beyond the MALL), and the Q6_K lm_head
-    248320 x 5120 at N = 1 (the draft chain's matvec). HIP-event time per launch on the context stream; GB/s from
-    the algorithmic bytes W + N*x + N*y. Flat GB/s against N means each weight super-block is read once per launch."""
+    17408 x 5120 and Q6_K 5120 x 17408 over 8 distinct weights each (beyond the MALL), the Q6_K lm_head
+    248320 x 5120 at N = 1 (the draft chain's matvec), the Q8_0 ssm_out (N = 1, 4) and the MTP's Q4_0 eh_proj
+    (N = 1); then the prompt-chunk product (N = 64, the prefill's matrix-core GEMM) on three of them. HIP-event time
+    per launch on the context stream; GB/s from the algorithmic bytes W + N*x + N*y. Flat GB/s against N means each
+    weight super-block is read once per launch."""
     out = []
     for t, rows, cols, nw, ns in [(aq.Q4_K, 17408, 5120, 8, (1, 2, 4, 6, 8)), (aq.Q6_K, 5120, 17408, 8, (1, 2, 4, 6, 8)),
-                                  (aq.Q6_K, 248320, 5120, 1, (1,))]:
+                                  (aq.Q6_K, 248320, 5120, 1, (1,)), (aq.Q8_0, 5120, 6144, 8, (1, 4)),
+                                  (aq.Q4_0, 5120, 10240, 8, (1,)), (aq.Q4_K, 17408, 5120, 4, (64,)),
+                                  (aq.Q6_K, 5120, 17408, 4, (64,)), (aq.Q8_0, 5120, 6144, 4, (64,))]:
         ws = [aq.SynthWeight(ctx, aq.synth_spec(t, rows, cols, seed=SEED + 200 + i)) for i in range(nw)]
         wbytes = rows * aq.row_bytes(t, cols)
         for n in ns:
@@ -108,9 +113,10 @@ def kernel_sweep(ctx):
             aq.matmul_time(ctx, ws, act, n, y, reps // 4)
             us = aq.matmul_time(ctx, ws, act, n, y, reps)
             med = float(np.median(aq.matmul_time_each(ctx, ws, act, n, y, max(64, reps // 2))))
-            nbytes = wbytes + n * (cols // 256) * 292 + n * rows * 4
+            xbytes = (cols // 256) * 292 if t in (aq.Q4_K, aq.Q5_K, aq.Q6_K) else (cols // 32) * 40  # Q8_K / Q8_0 rows
+            nbytes = wbytes + n * xbytes + n * rows * 4
             gbs = nbytes / (us * 1e-6) / 1e9
-            name = {aq.Q4_K: "Q4_K", aq.Q6_K: "Q6_K"}[t]
+            name = {aq.Q4_K: "Q4_K", aq.Q6_K: "Q6_K", aq.Q8_0: "Q8_0", aq.Q4_0: "Q4_0"}[t]
             out.append({"kernel": f"{name} {rows}x{cols}", "n": n, "us_per_launch": round(us, 2),
                         "median_us": round(med, 2), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
             y.free()
@@ -280,6 +286,9 @@ def main():
     ctx = aq.Context(0)
     k = a.spec
     ks = kernel_sweep(ctx) if not a.kernel_only else None  # also brings the clocks up before the roofline timing
+    if a.sweep_only:
+        print(json.dumps({"kernel_sweep": ks}), flush=True)
+        return
     kr = kernel_roofline(ctx, k)
     if a.kernel_only:  # the counter runs: the dominant kernel plus a plain device copy of known size
         nbytes = 512 << 20
