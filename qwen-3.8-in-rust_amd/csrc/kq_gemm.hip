@@ -6,14 +6,16 @@
 // K-quants x Q8_K (kdot.rs:37-140, 176-333) on v_mfma_i32_16x16x32_i8. The reference's lane l of a super-block is
 // the 32 elements 32s + 4l + b (s = sub-block, b = 0..3), and its sum is sum_s sc[s] * sum_b q * x. One matrix-core
 // product over K = 32 covers exactly lane l: k-group g of the operands (lanes 16g .. 16g + 15) takes sub-blocks 2g and
-// 2g + 1, four elements each; the scale goes into the weight operand as digits small enough that digit * code fits
-// an int8 (Q4_K: 6-bit scales in two base-8 digits, codes <= 15; Q5_K: three base-4 digits, codes <= 31; Q6_K:
-// signed 8-bit group scales in four balanced base-5 digits in -2..2, unsigned codes <= 63, and the reference's -32
-// offset taken from the activation's 16-element group sums into lane l exactly as kdot.rs:125-129 does). The digit
-// products chain through the accumulator (c = digit_hi product; c = c * base + next digit's product ...), so the
-// result is the exact lane sum for a 16-row x 16-column tile. The f32 part then runs per output in the lanes that
-// hold it (4 rows x 1 column per lane): acc[l] += (dx * d) * f32(sumi[l]), accm[i] += (-dx * dmin) * f32(prod[i]),
-// no FMA, and reduce8(acc) [+ reduce4(accm)] at the end.
+// 2g + 1, four elements each. Q4_K / Q5_K (v_mfma_i32_16x16x32_i8): the scale goes into the weight operand as digits
+// small enough that digit * code fits an int8 (6-bit scales in two base-8 digits, codes <= 15; three base-4 digits,
+// codes <= 31), the digit products chained through the accumulator (c = digit_hi product; c = c * base + next
+// digit's product ...). Q6_K (v_mfma_f32_16x16x32_f16): the signed 8-bit group scale sc = 16 hi + lo goes into two
+// f16 weight operands q * lo and q * hi (unsigned codes <= 63: both exact in f16), the activation codes as f16, both
+// sums exact in f32, taken to i32 as 16 * hi_sum + lo_sum, and the reference's -32 offset taken from the activation's
+// 16-element group sums into lane l exactly as kdot.rs:125-129 does (the reference's lane split of it). Either
+// way the result is the exact lane sum for a 16-row x 16-column tile. The f32 part then runs per output in the lanes
+// that hold it (4 rows x 1 column per lane): acc[l] += (dx * d) * f32(sumi[l]), accm[i] += (-dx * dmin) *
+// f32(prod[i]), no FMA, and reduce8(acc) [+ reduce4(accm)] at the end.
 //
 // Q8_0 / Q4_0 x Q8_0 (dot.rs:29-66): one product over K = 32 is one block's exact i32 sum for the tile (Q4_0: the
 // unsigned codes, less 8 * the activation block's code sum), then acc += (dw * dx) * f32(isum) per output.
@@ -37,32 +39,42 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
     __builtin_memcpy(&f, &h, 2);
     return (float)f;
 }
-// Each byte of x (values <= 126) negated, as int8: (0x80 - v) without borrows, then the top bit flipped.
-__device__ __forceinline__ uint32_t neg_bytes(uint32_t x) { return (0x80808080u - x) ^ 0x80808080u; }
-
-// Balanced base-5 digits (each in -2..2, low digit first) of a signed 8-bit scale, as four signed bytes.
-__device__ __forceinline__ uint32_t digits5(int v) {
-    uint32_t out = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        int d = v % 5; // in -4..4 (C truncation)
-        if (d > 2) d -= 5;
-        if (d < -2) d += 5;
-        v = (v - d) / 5;
-        out |= (uint32_t)(uint8_t)(int8_t)d << (8 * i);
-    }
-    return out;
-}
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 // Bytes of x times a small factor f, per byte (every product < 256, so no carry leaves its byte): one packed 16-bit
 // multiply with f in both halves.
 __device__ __forceinline__ uint32_t mul_bytes(uint32_t x, uint32_t f) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, x) * __builtin_bit_cast(u16x2, f * 0x00010001u));
 }
-// The operand bytes x (codes <= 63) times a digit in -2..2.
-__device__ __forceinline__ uint32_t times_digit(uint32_t x, int d) {
-    const uint32_t p = mul_bytes(x, (uint32_t)(d < 0 ? -d : d));
-    return d < 0 ? neg_bytes(p) : p;
+
+// f16 operands of the matrix-core f16 product (Q6_K). Small integers are exact in f16 (|v| <= 2048, and multiples of
+// 2^k up to 2048 * 2^k), the products of two f16 are exact in f32 and every partial sum of a lane (an integer below
+// 2^24 in magnitude) is exact in f32, so v_mfma_f32_16x16x32_f16 returns the exact integer lane sums as floats.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t h2bits(float a, float b) {
+    return __builtin_bit_cast(uint32_t, f16x2{(_Float16)a, (_Float16)b});
+}
+// Unsigned bytes 0, 1 (k = 0) or 2, 3 (k = 1) of w as the f16 pair (1024 + byte): the byte under an exponent of 2^10.
+__device__ __forceinline__ uint32_t magic_pair(uint32_t w, int k) {
+    return __builtin_amdgcn_perm(0x64646464u, w, k == 0 ? 0x04010400u : 0x04030402u);
+}
+// a * b + c on f16 pairs, one rounding (v_pk_fma_f16): exact whenever the result is representable.
+__device__ __forceinline__ uint32_t h2fma(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b),
+                                                                  __builtin_bit_cast(f16x2, c)));
+}
+// Eight signed activation codes (bytes of x, in k order) as f16: (1024 + 128 + x) - 1152.
+__device__ __forceinline__ f16x8 codes_f16(uint64_t x) {
+    const uint32_t w0 = (uint32_t)x ^ 0x80808080u, w1 = (uint32_t)(x >> 32) ^ 0x80808080u;
+    const f16x2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const f16x2 p0 = __builtin_bit_cast(f16x2, magic_pair(w0, 0)) + off, p1 = __builtin_bit_cast(f16x2, magic_pair(w0, 1)) + off;
+    const f16x2 p2 = __builtin_bit_cast(f16x2, magic_pair(w1, 0)) + off, p3 = __builtin_bit_cast(f16x2, magic_pair(w1, 1)) + off;
+    return __builtin_bit_cast(f16x8, uint4{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                                           __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)});
+}
+__device__ __forceinline__ f32x4 mma_f16(f16x8 a, f16x8 b) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 }
 
 struct GemmArgs {
@@ -87,6 +99,7 @@ __device__ __forceinline__ int sdot2(uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint32_t i8pair(uint32_t w, uint32_t w8, int k) {
     return __builtin_amdgcn_perm(w8, w, k == 0 ? 0x08010A00u : 0x09030B02u);
 }
+
 
 // ---- LDS staging ----
 // Operands reach the LDS by direct global-to-LDS copies (global_load_lds_*: each active lane's 16 or 4 bytes land at
@@ -248,18 +261,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
             xs0 = *reinterpret_cast<const uint4 *>(X + 4160 + 16 * li);
         }
 
-        // the weight operand's digits: the scales of sub-blocks 2g and 2g + 1 (Q6_K: per lane half, l < 4 / l >= 4)
+        // the weight operand's scales: Q4_K / Q5_K as digits of the scales of sub-blocks 2g and 2g + 1; Q6_K as f16
+        // factor pairs of its group scales sc = 16 hi + lo (lo in 0..15, hi in -8..7): (1024 + q) * f - 1024 * f =
+        // q * f, exact (|.| <= 945). Group scale k of the word: 0 = sub-block 2g lanes 0-3, 1 = lanes 4-7, 2 and 3
+        // the same for sub-block 2g + 1.
         int dga[ND], dgb[ND], dgc[ND], dgd[ND];
+        uint32_t flo[4], clo[4], fhi[4], chi[4];
         if constexpr (T == AQ_TYPE_Q6_K) {
             const uint32_t sw = g == 0 ? sa.x : g == 1 ? sa.y : g == 2 ? sa.z : sa.w;
-            const uint32_t da = digits5((int8_t)sw), dc = digits5((int8_t)(sw >> 8));
-            const uint32_t db = digits5((int8_t)(sw >> 16)), dd = digits5((int8_t)(sw >> 24));
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                dga[i] = (int8_t)(da >> (8 * i));
-                dgb[i] = (int8_t)(db >> (8 * i));
-                dgc[i] = (int8_t)(dc >> (8 * i));
-                dgd[i] = (int8_t)(dd >> (8 * i));
+            for (int k = 0; k < 4; k++) {
+                const int sc = (int8_t)(sw >> (8 * k)), lo = sc & 15, hi = sc >> 4;
+                flo[k] = h2bits((float)lo, (float)lo);
+                clo[k] = h2bits((float)(-1024 * lo), (float)(-1024 * lo));
+                fhi[k] = h2bits((float)hi, (float)hi);
+                chi[k] = h2bits((float)(-1024 * hi), (float)(-1024 * hi));
             }
         } else {
             // 6-bit scales of sub-blocks 2g, 2g + 1 (quant.rs:45-51): bytes 2g, 2g + 1 of the low or high word
@@ -293,28 +309,42 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
             }
         }
 
-        // the exact lane sums of the tile, digit by digit over all eight lane slots (eight independent products in
-        // flight): c[l][j] = lane l's sum for output row 4g + j of this lane's column
+        // the exact lane sums of the tile: c[l][j] = lane l's sum for output row 4g + j of this lane's column.
+        // Q4_K / Q5_K: int8 products digit by digit over all eight lane slots (eight independent products in flight).
+        // Q6_K: two f16 products per lane slot (the lo and hi scale parts; each sum exact in f32, |.| < 2^22), taken
+        // to i32 and combined there as 16 hi + lo, before the reference's -32 group-sum term (kdot.rs:97-140).
         v4i c[8];
-#pragma unroll
-        for (int i = ND - 1; i >= 0; i--) {
+        if constexpr (T == AQ_TYPE_Q6_K) {
 #pragma unroll
             for (int l = 0; l < 8; l++) {
-                const int *da = l < 4 ? dga : dgc, *db = l < 4 ? dgb : dgd;
-                uint32_t alo, ahi;
-                if constexpr (T == AQ_TYPE_Q6_K) {
-                    alo = times_digit(lo[l], da[i]);
-                    ahi = times_digit(hi[l], db[i]);
-                } else {
-                    alo = mul_bytes(lo[l], (uint32_t)da[i]);
-                    ahi = mul_bytes(hi[l], (uint32_t)db[i]);
-                }
-                v4i cin = {0, 0, 0, 0};
-                if (i < ND - 1) {
+                const int ka = l < 4 ? 0 : 1, kb = l < 4 ? 2 : 3;
+                const uint32_t la = magic_pair(lo[l], 0), lb = magic_pair(lo[l], 1);
+                const uint32_t ha = magic_pair(hi[l], 0), hb = magic_pair(hi[l], 1);
+                const f16x8 alo = __builtin_bit_cast(
+                    f16x8, uint4{h2fma(la, flo[ka], clo[ka]), h2fma(lb, flo[ka], clo[ka]), h2fma(ha, flo[kb], clo[kb]),
+                                 h2fma(hb, flo[kb], clo[kb])});
+                const f16x8 ahi = __builtin_bit_cast(
+                    f16x8, uint4{h2fma(la, fhi[ka], chi[ka]), h2fma(lb, fhi[ka], chi[ka]), h2fma(ha, fhi[kb], chi[kb]),
+                                 h2fma(hb, fhi[kb], chi[kb])});
+                const f16x8 b = codes_f16(bx[l]);
+                const f32x4 dl = mma_f16(alo, b), dh = mma_f16(ahi, b);
 #pragma unroll
-                    for (int e = 0; e < 4; e++) cin[e] = c[l][e] * BASE;
+                for (int e = 0; e < 4; e++) c[l][e] = 16 * (int)dh[e] + (int)dl[e];
+            }
+        } else {
+#pragma unroll
+            for (int i = ND - 1; i >= 0; i--) {
+#pragma unroll
+                for (int l = 0; l < 8; l++) {
+                    const int *da = l < 4 ? dga : dgc, *db = l < 4 ? dgb : dgd;
+                    const uint32_t alo = mul_bytes(lo[l], (uint32_t)da[i]), ahi = mul_bytes(hi[l], (uint32_t)db[i]);
+                    v4i cin = {0, 0, 0, 0};
+                    if (i < ND - 1) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) cin[e] = c[l][e] * BASE;
+                    }
+                    c[l] = mma(pack2(alo, ahi), bx[l], cin);
                 }
-                c[l] = mma(pack2(alo, ahi), bx[l], cin);
             }
         }
 
