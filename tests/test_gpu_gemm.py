@@ -78,3 +78,15 @@ def test_rows_not_a_multiple_of_256_take_column_pieces(ctx, t):
     host, w, a, x, y = run(ctx, t, rows, cols, ncols, 77 + t)
     want = O.matmul(t, host, rows, cols, x, threads=8)
     assert np.array_equal(bits(y), bits(want))
+
+
+@pytest.mark.parametrize("t", [aq.Q4_K, aq.Q6_K])
+def test_many_columns_under_q8_fine_equal_the_oracle(ctx, t):
+    """Under the q8-fine switch (Q8_0-grain activations for K-quant weights, dot.rs:69-160) a 33-column product runs
+    as 8-column pieces of the q8-fine kernel; every column equals the oracle's q8-fine dot."""
+    rows, cols, ncols = 130, 512, 33
+    print(f"case q8-fine many columns type {t}", flush=True)
+    with aq.q8_fine(), O.q8_fine():
+        host, w, a, x, y = run(ctx, t, rows, cols, ncols, 555 + t)
+        want = O.matmul(t, host, rows, cols, x, threads=8)
+    assert np.array_equal(bits(y), bits(want))

@@ -129,3 +129,24 @@ def test_27b_forced_drafts_rollback_state(big):
         assert np.array_equal(a[: b.size], b), f"round {r}: spec state differs from the plain state"
         assert np.array_equal(a, os_.export()), f"round {r}: spec state differs from the oracle's"
         assert gs.drafts() == os_.drafts()
+
+
+def test_27b_prompt_chunks_equal_token_by_token_feed(big):
+    """A 70-token prompt at the full shape: one chunk of 64 rows (every projection through the matrix-core prompt
+    GEMM, csrc/kq_gemm.hip, the DeltaNet recurrence and attention in 8-row pieces) and one of 6; the last row's logits
+    and every per-layer state tensor equal those of the same prompt fed one token at a time through the decode
+    kernels (themselves bit-exact to the oracle above) — model.rs:443-461, prefill row i is forward_token on row i."""
+    print("case 27B 70-token prompt in chunks vs one token at a time", flush=True)
+    cfg = big["cfg"]
+    prompt = np.random.default_rng(SEED + 7).integers(0, cfg.vocab, 70).astype(np.uint32)
+    g = aq.State(big["gm"], 0, 96)
+    tg, lg = g.prefill(prompt, want_logits=True)
+    f = aq.State(big["gm"], 0, 96)
+    f.prefill(prompt[:1])
+    for tok in prompt[1:-1]:
+        f.forward_token(int(tok))
+    tf, lf = f.forward_token(int(prompt[-1]), want_logits=True)
+    assert tf == tg and np.array_equal(lf.view(np.uint32), lg.view(np.uint32)), "chunked prefill logits differ"
+    assert np.array_equal(g.export(), f.export()), "chunked prefill state differs"
+    g.free()
+    f.free()
