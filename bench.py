@@ -249,6 +249,7 @@ def forced_rounds(model, prompt, plain, k, n_rounds, max_pos):
     the mean round time for each m."""
     vocab = model.cfg.vocab
     res, by_m = {}, {m: [] for m in range(k + 1)}
+    warm = min(4, n_rounds // 2)  # the first rounds warm up (half of a short run)
     for name, sched in (("full_acceptance", [k]), ("reference_mean", [min(m, k) for m in (3, 2, 3, 1, 2, 0, 3, 2)])):
         st = aq.State(model, k, max_pos)
         out = [st.spec_prefill(prompt)]
@@ -264,12 +265,13 @@ def forced_rounds(model, prompt, plain, k, n_rounds, max_pos):
             st.drafts()  # waits for the round's tail (commit, MTP re-feed, next drafts)
             t = time.perf_counter() - t1
             ok = ok and mm == m and em == plain[j:j + len(em)]
-            if r >= 4:  # the first rounds warm up
+            if r >= warm:
                 dt += t
                 emitted += len(em)
                 by_m[m].append(t * 1e3)
             out += em
-        res[name] = {"tokens_per_s": round(emitted / dt, 3), "tokens_per_round": round(emitted / (n_rounds - 4), 3),
+        res[name] = {"tokens_per_s": round(emitted / dt, 3) if dt > 0 else None,
+                     "tokens_per_round": round(emitted / (n_rounds - warm), 3) if n_rounds > warm else None,
                      "ids_equal_plain": bool(ok)}
         st.free()
     res["round_ms_by_m"] = {m: round(float(np.median(v)), 3) for m, v in by_m.items() if v}
