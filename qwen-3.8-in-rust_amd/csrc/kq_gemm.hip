@@ -24,6 +24,8 @@
 // work-group the same 16 rows x 64 columns. Rows and columns past the ends are read clamped and not written.
 #include "aq_common.h"
 
+#include <atomic>
+
 namespace aq {
 namespace {
 
@@ -516,10 +518,14 @@ template <typename K>
 int launch_staged(K kernel, int bytes, const GemmArgs &ga, hipStream_t stream, const char *what) {
     const dim3 grid((unsigned)((ga.rows + 15) / 16), (unsigned)((ga.ncols + 63) / 64));
     const size_t lds = (size_t)bytes * GEMM_STAGES;
-    if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return fail(AQ_EHIP, what);
+    if (lds > 64 * 1024) { // once per kernel and process: allow the ring's dynamic LDS (up to the CU's 160 KB)
+        static std::atomic<bool> raised{false};
+        if (!raised.load()) {
+            const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return fail(AQ_EHIP, what);
+            raised.store(true);
+        }
     }
     hipLaunchKernelGGL(kernel, grid, dim3(256), lds, stream, ga);
     return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, what);

@@ -37,6 +37,7 @@ struct Q8Args {
     size_t n;
     float *y;
     const float *resid;
+    int ncols; // columns of the launch (the F32 kernel: groups of NC along grid y)
 };
 
 template <int NC, int RPB>
@@ -350,6 +351,7 @@ __global__ void __launch_bounds__(256) f32_matmul_kernel(Q8Args a) {
     extern __shared__ float prods[]; // nb32 x NC
     const int row = blockIdx.x, nb = a.nb32;
     const size_t n = a.n;
+    const int c0 = (int)blockIdx.y * NC, nc = a.ncols - c0 < NC ? a.ncols - c0 : NC; // this work-group's columns
     const float *w = reinterpret_cast<const float *>(a.qa) + (size_t)row * n;
     for (int b = threadIdx.x; b < nb; b += 256) {
         const size_t e0 = (size_t)b * 32;
@@ -369,7 +371,8 @@ __global__ void __launch_bounds__(256) f32_matmul_kernel(Q8Args a) {
         }
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            const float *x = a.xf + (size_t)c * n + e0;
+            if (c >= nc) break; // uniform
+            const float *x = a.xf + (size_t)(c0 + c) * n + e0;
             float part = 0.0f;
             if (ne == 32 && n % 4 == 0) {
                 float xv[32];
@@ -390,7 +393,7 @@ __global__ void __launch_bounds__(256) f32_matmul_kernel(Q8Args a) {
         }
     }
     __syncthreads();
-    if (threadIdx.x < NC) {
+    if ((int)threadIdx.x < nc) {
         const int c = threadIdx.x;
         float acc = 0.0f;
         int b = 0;
@@ -403,7 +406,7 @@ __global__ void __launch_bounds__(256) f32_matmul_kernel(Q8Args a) {
         }
         for (; b < nb; b++) acc += prods[b * NC + c];
         if (n % 32 == 0) acc = acc + 0.0f;
-        const size_t o = (size_t)c * a.rows + row;
+        const size_t o = (size_t)(c0 + c) * a.rows + row;
         a.y[o] = a.resid ? a.resid[o] + acc : acc;
     }
 }
@@ -437,7 +440,9 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
     if (args.type == AQ_TYPE_F32) {
         const size_t lds = (size_t)args.nb32 * NC * sizeof(float);
         if (lds > 64 * 1024) return fail(AQ_EUNSUP, "f32 matmul: row too long for the LDS chain");
-        hipLaunchKernelGGL((f32_matmul_kernel<NC>), dim3((unsigned)args.rows), dim3(256), lds, stream, args);
+        // NC columns per work-group, the column groups along grid y (ncols past NC: a prompt chunk's rows)
+        const dim3 grid((unsigned)args.rows, (unsigned)((args.ncols + NC - 1) / NC));
+        hipLaunchKernelGGL((f32_matmul_kernel<NC>), grid, dim3(256), lds, stream, args);
         return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "f32_matmul launch");
     }
     {
@@ -515,7 +520,8 @@ int launch_matmul_many(const Weight &w, const Act &x, size_t ncols, float *y, co
     if (ncols <= 8) return launch_matmul(w, x, ncols, y, resid, stream);
     if ((is_kquant(w.type) && !q8_fine()) || ((w.type == AQ_TYPE_Q8_0 || w.type == AQ_TYPE_Q4_0) && w.cols % 256 == 0))
         return launch_gemm(w, x, ncols, y, resid, stream);
-    // F32 weights, K-quants under the q8-fine switch, Q8_0 / Q4_0 rows not a multiple of 256 long
+    if (w.type == AQ_TYPE_F32) return launch_matmul(w, x, ncols, y, resid, stream); // one launch, column groups
+    // K-quants under the q8-fine switch, Q8_0 / Q4_0 rows not a multiple of 256 long
     for (size_t c0 = 0; c0 < ncols; c0 += 8) {
         const size_t tc = ncols - c0 < 8 ? ncols - c0 : 8;
         Act v = x;
@@ -551,6 +557,8 @@ int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const f
     args.n = x.n;
     args.y = y;
     args.resid = resid;
+    args.ncols = (int)ncols;
+    if (w.type == AQ_TYPE_F32 && ncols > 8) return launch_q8_nc<8>(args, stream); // groups of 8 along grid y
     switch (ncols) {
     case 1: return launch_q8_nc<1>(args, stream);
     case 2: return launch_q8_nc<2>(args, stream);

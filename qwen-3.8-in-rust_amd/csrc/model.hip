@@ -616,11 +616,13 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
         a.rd = (int)c.rope_dim;
         a.gsc = s->attn_sc;
         a.gsc_stride = s->attn_sc_stride;
-        // pieces of at most MAX_ROWS rows (the score rows a context past the LDS keeps in device memory are that
-        // many); each piece's K/V rows are appended before the next piece attends to them
+        // the whole chunk in one launch while its scores fit the LDS; past that, pieces of at most MAX_ROWS rows
+        // (the score rows a context past the LDS keeps in device memory are that many), each piece's K/V rows
+        // appended before the next piece attends to them
         const size_t qw = 2 * (size_t)c.n_head * c.head_dim, kw = kv->stride, ow = (size_t)c.n_head * c.head_dim;
-        for (size_t r0 = 0; r0 < t; r0 += MAX_ROWS) {
-            const size_t tr = t - r0 < (size_t)MAX_ROWS ? t - r0 : (size_t)MAX_ROWS;
+        const size_t piece = kv->len + t <= attn_lds_positions((int)c.head_dim) ? t : (size_t)MAX_ROWS;
+        for (size_t r0 = 0; r0 < t; r0 += piece) {
+            const size_t tr = t - r0 < piece ? t - r0 : piece;
             AttnArgs ap = a;
             ap.qg = a.qg + r0 * qw;
             ap.kk = a.kk + r0 * kw;

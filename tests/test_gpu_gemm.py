@@ -90,3 +90,14 @@ def test_many_columns_under_q8_fine_equal_the_oracle(ctx, t):
         host, w, a, x, y = run(ctx, t, rows, cols, ncols, 555 + t)
         want = O.matmul(t, host, rows, cols, x, threads=8)
     assert np.array_equal(bits(y), bits(want))
+
+
+@pytest.mark.parametrize("ncols", [9, 33, 64])
+def test_f32_many_columns_equal_the_oracle(ctx, ncols):
+    """F32 weights (the DeltaNet ssm_alpha / ssm_beta projections) over a prompt chunk's columns: one launch, eight
+    columns per work-group along the grid's second dimension (dot.rs:180-200 per column)."""
+    rows, cols = 48, 5120
+    print(f"case f32 many columns N={ncols}", flush=True)
+    host, w, a, x, y = run(ctx, aq.F32, rows, cols, ncols, 808 + ncols)
+    want = O.matmul(aq.F32, host, rows, cols, x, threads=8)
+    assert np.array_equal(bits(y), bits(want))
