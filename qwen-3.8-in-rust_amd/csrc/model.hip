@@ -678,36 +678,9 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
     d.dk = (int)c.dn_head_dim_k;
     d.dv = (int)c.dn_head_dim_v;
     d.kernel = (int)c.dn_conv_kernel;
-    if (t <= 8) {
-        if ((rc = launch_dn_core(d, s->stream))) return rc;
-    } else {
-        // a prompt chunk: pieces of 8 rows, the state advancing piece by piece and each piece's conv window read
-        // from the one the previous piece wrote; the last piece writes the buffer the pass's parity flip expects
-        // (with an even number of pieces the window is copied across first, so the chain ends there)
-        AQ_REQUIRE(mode == PLAIN, "deltanet: more than 8 rows in one verify batch");
-        const size_t np = (t + 7) / 8;
-        float *cur = s->par ? s->conv1[dn_slot] : s->conv0[dn_slot], *nxt = s->par ? s->conv0[dn_slot] : s->conv1[dn_slot];
-        if (np % 2 == 0) {
-            AQ_HIP(hipMemcpyAsync(nxt, cur, m->cd * (c.dn_conv_kernel - 1) * sizeof(float), hipMemcpyDeviceToDevice,
-                                  s->stream));
-            std::swap(cur, nxt);
-        }
-        const size_t cd = m->cd, vd = m->vd, nvh = c.dn_n_v_heads;
-        for (size_t r0 = 0; r0 < t; r0 += 8) {
-            DnArgs dp = d;
-            dp.t = (int)(t - r0 < 8 ? t - r0 : 8);
-            dp.mixed = d.mixed + r0 * cd;
-            dp.z = d.z + r0 * vd;
-            dp.a = d.a + r0 * nvh;
-            dp.b = d.b + r0 * nvh;
-            dp.out = d.out + r0 * vd;
-            dp.q80 = col_view(s->act_vd, r0);
-            dp.conv_src = cur;
-            dp.conv_dst = nxt;
-            if ((rc = launch_dn_core(dp, s->stream))) return rc;
-            std::swap(cur, nxt);
-        }
-    }
+    // a prompt chunk (t > 8) runs as 8-row pieces inside the one launch, the state carried from piece to piece
+    AQ_REQUIRE(t <= 8 || mode == PLAIN, "deltanet: more than 8 rows in one verify batch");
+    if ((rc = launch_dn_core(d, s->stream))) return rc;
     if (!q80) {
         Needs no;
         no.add(L.ssm_out);

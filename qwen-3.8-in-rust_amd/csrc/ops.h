@@ -62,6 +62,7 @@ struct DnArgs {
     const float *rq = nullptr, *rk = nullptr, *rv = nullptr, *rg = nullptr, *rbeta = nullptr;
     const uint32_t *t_dev = nullptr; // multi launch: the row count, read on the device (1..8)
 };
+// t rows; more than 8 (a prompt chunk: projected gates, no raw mode) run as 8-row pieces inside one launch.
 int launch_dn_core(const DnArgs &a, hipStream_t stream);
 // n DnArgs (device array, commit form: saved gates, no output), all with the head shape of `like`: one launch.
 int launch_dn_core_multi(const DnArgs *args_dev, const DnArgs &like, int n, hipStream_t stream);

@@ -319,7 +319,17 @@ constexpr int dn_parts() {
 }
 
 template <int DK, int DV>
-__device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const int t) {
+constexpr int dn_kh() { return DK / dn_parts<DK, DV>(); }
+
+// Rows r0 .. r0 + t - 1 (t <= DN_TMAX) of the launch's rows. `s` is the thread's part of the state column: loaded
+// from a.rec when `first`, written back when `last` (and a.write_state), carried in registers between the pieces of
+// one launch otherwise. The conv window of a piece after the first is the three input rows before it.
+template <int DK, int DV, bool CHUNK = false>
+__device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const int t, float (&s)[dn_kh<DK, DV>()],
+                                             const int r0, const bool first, const bool last) {
+    // CHUNK: the host admits no raw rows and no in-kernel gate projection, so both paths compile away
+    const bool raw_ = !CHUNK && a.raw;
+    const float *const ax_ = CHUNK ? nullptr : a.x;
     static_assert(DK <= 256 && DV <= 256 && DN_THREADS >= 448 && DN_TMAX * 2 <= 16, "DeltaNet work-group shape");
     __shared__ float sq[DN_TMAX][DK], sk[DN_TMAX][DK], sv[DN_TMAX][DV], sz[DN_TMAX][DV], so[DN_TMAX][DV];
     __shared__ float part[2][DN_TMAX][DN_BLK_MAX];
@@ -328,18 +338,18 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
     const int kh = p % a.nk;
     const int kd = a.nk * DK, vd = a.nv * DV, cd = 2 * kd + vd;
     const bool has_v = j < DV;
-    const bool gated = a.out && !a.raw;
+    const bool gated = a.out && !raw_;
     // the gate inputs, loaded before phase A so their latency hides behind it: wave 5 computes the decays and
     // wave 7 the betas (lane i = row i), each in its own wave so neither waits for the other's branch
     const bool gate_lane = (wave == 5 || wave == 7) && lane < t;
     const int gr = wave == 5 ? 0 : 1;
     float gv = 0.0f, gsa = 0.0f, gdt = 0.0f;
     if (gate_lane) {
-        if (a.raw)
-            gv = (gr == 0 ? a.rg : a.rbeta)[(size_t)lane * a.nv + p];
-        else if (!a.x)
-            gv = (gr == 0 ? a.a : a.b)[(size_t)lane * a.nv + p];
-        if (gr == 0 && !a.raw) {
+        if (raw_)
+            gv = (gr == 0 ? a.rg : a.rbeta)[(size_t)(r0 + lane) * a.nv + p];
+        else if (!ax_)
+            gv = (gr == 0 ? a.a : a.b)[(size_t)(r0 + lane) * a.nv + p];
+        if (gr == 0 && !raw_) {
             gsa = a.ssm_a[p];
             gdt = a.dt_bias[p];
         }
@@ -347,18 +357,18 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
     const float nrm_w = gated && has_v ? a.ssm_norm[j] : 0.0f; // phase D's norm weight
 
     // ---- A: channels over all rows
-    if (a.raw) {
+    if (raw_) {
         for (int e = j; e < t * DK; e += DN_THREADS) {
             const int i = e / DK, c = e % DK;
-            sq[i][c] = a.rq[(size_t)i * kd + kh * DK + c];
-            sk[i][c] = a.rk[(size_t)i * kd + kh * DK + c];
+            sq[i][c] = a.rq[(size_t)(r0 + i) * kd + kh * DK + c];
+            sk[i][c] = a.rk[(size_t)(r0 + i) * kd + kh * DK + c];
         }
         for (int e = j; e < t * DV; e += DN_THREADS) {
             const int i = e / DV, c = e % DV;
-            sv[i][c] = a.rv[(size_t)i * vd + p * DV + c];
+            sv[i][c] = a.rv[(size_t)(r0 + i) * vd + p * DV + c];
         }
     } else {
-        if (a.x) {
+        if (ax_) {
             // gated_deltanet.rs:271-274 ssm_alpha / ssm_beta rows of this head on the t input rows: per 32-block a
             // left-to-right partial for every row (four rows' chains interleaved)
             const int n = a.hidden, nblk = (n + 31) / 32;
@@ -379,7 +389,7 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             const int i = i0 + q < t ? i0 + q : t - 1;
-                            const float *xr = a.x + (size_t)i * a.x_stride + e0;
+                            const float *xr = ax_ + (size_t)(r0 + i) * a.x_stride + e0;
 #pragma unroll
                             for (int u = 0; u < 8; u++) {
                                 const float4 f = *reinterpret_cast<const float4 *>(xr + 4 * u);
@@ -398,7 +408,7 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
                     }
                 } else {
                     for (int i = 0; i < t; i++) {
-                        const float *xr = a.x + (size_t)i * a.x_stride + e0;
+                        const float *xr = ax_ + (size_t)(r0 + i) * a.x_stride + e0;
                         float pt = 0.0f;
                         for (int e = 0; e < ne; e++) pt += w[e0 + e] * xr[e];
                         part[r][i][b] = pt;
@@ -416,12 +426,13 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
                 const int ch = kind == 0 ? kh * DK + cc : kind == 1 ? kd + kh * DK + cc : 2 * kd + p * DV + cc;
                 float seq[DN_TMAX + 3];
 #pragma unroll
-                for (int e = 0; e < 3; e++) seq[e] = a.conv_src[(size_t)ch * 3 + e];
+                for (int e = 0; e < 3; e++)
+                    seq[e] = first ? a.conv_src[(size_t)ch * 3 + e] : a.mixed[(size_t)(r0 - 3 + e) * cd + ch];
                 float cw[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) cw[e] = a.conv_w[(size_t)ch * 4 + e];
 #pragma unroll
-                for (int i = 0; i < DN_TMAX; i++) seq[3 + i] = a.mixed[(size_t)(i < t ? i : t - 1) * cd + ch];
+                for (int i = 0; i < DN_TMAX; i++) seq[3 + i] = a.mixed[(size_t)(r0 + (i < t ? i : t - 1)) * cd + ch];
                 float *dst = kind == 0 ? &sq[0][cc] : kind == 1 ? &sk[0][cc] : &sv[0][cc];
                 const int dstride = kind == 2 ? DV : DK;
 #pragma unroll
@@ -435,7 +446,7 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
                         dst[i * dstride] = silu_f(acc);
                     }
                 }
-                if (a.conv_dst && (kind == 2 || p == kh)) {
+                if (a.conv_dst && last && (kind == 2 || p == kh)) {
 #pragma unroll
                     for (int i = 0; i <= DN_TMAX; i++) // the window after row t - 1: seq[t .. t + 2]
                         if (i == t)
@@ -445,7 +456,7 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
                 const int cc = c - n_conv;
                 float zr[DN_TMAX];
 #pragma unroll
-                for (int i = 0; i < DN_TMAX; i++) zr[i] = a.z[(size_t)(i < t ? i : t - 1) * vd + p * DV + cc];
+                for (int i = 0; i < DN_TMAX; i++) zr[i] = a.z[(size_t)(r0 + (i < t ? i : t - 1)) * vd + p * DV + cc];
 #pragma unroll
                 for (int i = 0; i < DN_TMAX; i++)
                     if (i < t) sz[i][cc] = silu_f(zr[i]);
@@ -460,7 +471,7 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
         // 6 (8-15): lane m of the chain holds its terms m*T .. m*T + T - 1 as registers and the running sum moves
         // one lane up after each lane's terms (DPP row shift), so lane 7 of the group ends with the whole sum,
         // added in order
-        if ((wave == 4 || wave == 6) && !a.raw) {
+        if ((wave == 4 || wave == 6) && !raw_) {
             constexpr int T = DK / 8;
             const int c = (wave == 4 ? 0 : 8) + (lane >> 3), m = lane & 7, cc = c < 2 * t ? c : 0;
             const float4 *x4 = reinterpret_cast<const float4 *>((cc & 1) ? sk[cc >> 1] : sq[cc >> 1]) + m * (T / 4);
@@ -489,7 +500,7 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
                     rq[c >> 1] = inv;
             }
         }
-    } else if (wave == 4 && !a.raw && lane < 2 * t) { // one sum per lane
+    } else if (wave == 4 && !raw_ && lane < 2 * t) { // one sum per lane
         const int i = lane >> 1;
         const float ss = seq_sum<true>((lane & 1) ? sk[i] : sq[i], 0, DK, 1, 0.0f);
         const float inv = 1.0f / sqrtf(ss + 1e-6f); // deltanet.rs:19-29 l2norm
@@ -501,18 +512,18 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
     if (gate_lane) {
         const int i = lane;
         float v = gv;
-        if (!a.raw && a.x) {
+        if (!raw_ && ax_) {
             // dot.rs:180-200: the block chain, `acc + part` with the short tail (0.0f when there is none)
             const int n = a.hidden, nblk = (n + 31) / 32;
             v = seq_sum<false>(&part[gr][i][0], 0, nblk, 1, 0.0f);
             if (n % 32 == 0) v = v + 0.0f;
-            (gr == 0 ? a.a : a.b)[(size_t)i * a.nv + p] = v; // kept for the commit
+            (gr == 0 ? a.a : a.b)[(size_t)(r0 + i) * a.nv + p] = v; // kept for the commit
         }
         if (gr == 0) {
-            const float g = a.raw ? v : gsa * softplus_f(v + gdt); // deltanet.rs:32-35 gate_g
+            const float g = raw_ ? v : gsa * softplus_f(v + gdt); // deltanet.rs:32-35 gate_g
             rdec[i] = exp_f(g);
         } else {
-            rbeta[i] = a.raw ? v : sigmoid_f(v);
+            rbeta[i] = raw_ ? v : sigmoid_f(v);
         }
     }
     // ---- the state column, split by key: thread j holds keys [h KH, h KH + KH) of column c = j % DV, part
@@ -520,14 +531,13 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
     constexpr int H = dn_parts<DK, DV>(), KH = DK / H;
     const int c = j % DV, h = j / DV;
     const bool has_col = h < H;
-    float s[KH];
     float *srec = a.rec + (size_t)p * DK * DV;
-    if (has_col) {
+    if (has_col && first) {
 #pragma unroll
         for (int k = 0; k < KH; k++) s[k] = srec[(size_t)(h * KH + k) * DV + c];
     }
     __syncthreads();
-    if (!a.raw) {
+    if (!raw_) {
         for (int e = j; e < t * DK; e += DN_THREADS) {
             const int i = e / DK, cc = e % DK;
             sq[i][cc] = (sq[i][cc] * rq[i]) * a.qscale;
@@ -593,8 +603,8 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
                 for (int k = 0; k < KH; k++) ov += pk[k];
                 if (hh + 1 < H) {
                     xfer2[c] = ov;
-                } else if (a.raw) {
-                    if (a.out) a.out[(size_t)i * vd + p * DV + c] = ov;
+                } else if (raw_) {
+                    if (a.out) a.out[(size_t)(r0 + i) * vd + p * DV + c] = ov;
                 } else {
                     so[i][c] = ov;
                 }
@@ -602,7 +612,7 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
             if (hh + 1 < H) __syncthreads();
         }
     }
-    if (has_col && a.write_state) {
+    if (has_col && a.write_state && last) {
 #pragma unroll
         for (int k = 0; k < KH; k++) srec[(size_t)(h * KH + k) * DV + c] = s[k];
     }
@@ -632,15 +642,29 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
         if (has_v)
             for (int i = 0; i < t; i++) {
                 const float v = (nrm_w * (so[i][j] * ro[i])) * sz[i][j];
-                a.out[(size_t)i * vd + p * DV + j] = v;
-                if (a.out_q80) q8_0_block_half(a.q80, i, (size_t)p * (DV / 32) + (j >> 5), v, lane);
+                a.out[(size_t)(r0 + i) * vd + p * DV + j] = v;
+                if (a.out_q80) q8_0_block_half(a.q80, r0 + i, (size_t)p * (DV / 32) + (j >> 5), v, lane);
             }
     }
 }
 
 template <int DK, int DV>
 __global__ void __launch_bounds__(DN_THREADS) dn_core_kernel(DnArgs a) {
-    dn_core_body<DK, DV>(a, (int)blockIdx.x, a.t);
+    float s[dn_kh<DK, DV>()];
+    dn_core_body<DK, DV>(a, (int)blockIdx.x, a.t, s, 0, true, true);
+}
+
+// A prompt chunk of more than DN_TMAX rows in one launch (gated_deltanet.rs:197-199 steps the recurrence token by
+// token): pieces of DN_TMAX rows in order, the state column kept in registers from piece to piece and each piece's
+// conv window taken from the three input rows before it.
+template <int DK, int DV>
+__global__ void __launch_bounds__(DN_THREADS) dn_core_chunk_kernel(DnArgs a) {
+    float s[dn_kh<DK, DV>()];
+    for (int r0 = 0; r0 < a.t; r0 += DN_TMAX) {
+        if (r0 > 0) __syncthreads(); // the previous piece's LDS rows are read to the end before they are rewritten
+        const int tp = a.t - r0 < DN_TMAX ? a.t - r0 : DN_TMAX;
+        dn_core_body<DK, DV, true>(a, (int)blockIdx.x, tp, s, r0, r0 == 0, r0 + DN_TMAX >= a.t);
+    }
 }
 
 // Several layers' heads in one launch (the commit of every DeltaNet layer after a speculative round): work-group
@@ -650,7 +674,8 @@ __global__ void __launch_bounds__(DN_THREADS) dn_core_multi_kernel(const DnArgs 
     const DnArgs &a = args[blockIdx.y];
     const int t = a.t_dev ? (int)*a.t_dev : a.t;
     if (t < 1 || t > DN_TMAX) return; // uniform: a row count the host validates before it is used
-    dn_core_body<DK, DV>(a, (int)blockIdx.x, t);
+    float s[dn_kh<DK, DV>()];
+    dn_core_body<DK, DV>(a, (int)blockIdx.x, t, s, 0, true, true);
 }
 
 // ---------------------------------------------------------------------------------------------- attention
@@ -1027,7 +1052,8 @@ int launch_dn_core(const DnArgs &a, hipStream_t stream) {
     } else {
         AQ_REQUIRE(a.rq && a.rk && a.rv && a.rg && a.rbeta, "deltanet: raw inputs");
     }
-    AQ_REQUIRE(a.t <= DN_TMAX, "deltanet: at most 8 rows per launch");
+    AQ_REQUIRE(a.t <= DN_TMAX || (!a.raw && !a.x && a.t <= 4096),
+               "deltanet: more than 8 rows in one launch need the projected gates (no raw mode, no x) and t <= 4096");
     AQ_REQUIRE(a.raw || a.x || (a.a && a.b), "deltanet: gate inputs");
     AQ_REQUIRE(!a.x || (a.w_alpha && a.w_beta && a.a && a.b && a.hidden > 0 && a.hidden <= 32 * DN_BLK_MAX),
                "deltanet: alpha/beta projection");
@@ -1035,7 +1061,12 @@ int launch_dn_core(const DnArgs &a, hipStream_t stream) {
     const int key = a.dk * 1000 + a.dv;
     switch (key) {
 #define AQ_DN(K, V)                                                                                           \
-    case K * 1000 + V: hipLaunchKernelGGL((dn_core_kernel<K, V>), dim3((unsigned)a.nv), dim3(threads), 0, stream, a); break;
+    case K * 1000 + V:                                                                                        \
+        if (a.t <= DN_TMAX)                                                                                   \
+            hipLaunchKernelGGL((dn_core_kernel<K, V>), dim3((unsigned)a.nv), dim3(threads), 0, stream, a);     \
+        else                                                                                                  \
+            hipLaunchKernelGGL((dn_core_chunk_kernel<K, V>), dim3((unsigned)a.nv), dim3(threads), 0, stream, a); \
+        break;
         AQ_DN(8, 8) AQ_DN(16, 16) AQ_DN(32, 32) AQ_DN(64, 64) AQ_DN(128, 128) AQ_DN(128, 256) AQ_DN(64, 128)
 #undef AQ_DN
     default: return fail(AQ_EUNSUP, "deltanet: head dims (k, v) not built: " + std::to_string(a.dk) + ", " +

@@ -402,7 +402,8 @@ def test_device_argmax_ties_and_nan(ctx):
 
 def test_tiny_prompt_chunks_equal_token_by_token_and_oracle(ctx, tiny):
     """A 150-token prompt runs in chunks of 64, 64 and 22 rows (each layer over a whole chunk: matmuls over all its
-    columns, attention and the DeltaNet recurrence in pieces of 8 rows, the conv windows chained piece to piece):
+    columns, attention per chunk, the DeltaNet recurrence in pieces of 8 rows inside one launch per chunk, the state
+    carried in registers and each piece's conv window read from the rows before it):
     the last row's logits and the whole state equal the oracle's prefill and a token-by-token feed, bit for bit
     (model.rs:443-461, the prefill row i is forward_token on row i)."""
     print("case tiny 150-token prompt in chunks", flush=True)

@@ -133,7 +133,8 @@ def test_27b_forced_drafts_rollback_state(big):
 
 def test_27b_prompt_chunks_equal_token_by_token_feed(big):
     """A 70-token prompt at the full shape: one chunk of 64 rows (every projection through the matrix-core prompt
-    GEMM, csrc/kq_gemm.hip, the DeltaNet recurrence and attention in 8-row pieces) and one of 6; the last row's logits
+    GEMM, csrc/kq_gemm.hip, attention over the whole chunk, the DeltaNet recurrence in 8-row pieces inside one launch)
+    and one of 6; the last row's logits
     and every per-layer state tensor equal those of the same prompt fed one token at a time through the decode
     kernels (themselves bit-exact to the oracle above) — model.rs:443-461, prefill row i is forward_token on row i."""
     print("case 27B 70-token prompt in chunks vs one token at a time", flush=True)
