@@ -10,10 +10,12 @@ re-feed the MTP and draft k tokens). `value` = emitted tokens / wall time of the
 Printed as one JSON line, with
   roofline      the dominant kernel (the K-quant verify matmul: Q4_K 17408 x 5120 at N = k+1 = 4, the FFN gate/up
                 shape that carries 38% of the weight bytes) timed with HIP events on its stream, against 8 TB/s: the
-                mean over 1000 back-to-back launches (achieved) and the median of 400 single-launch times;
+                mean over 1000 back-to-back launches (achieved) and the median of 400 single-launch times; beside
+                it the read floor: a plain streaming-read kernel over the same bytes, timed the same way (the least
+                time any kernel reads that much on this device: launch, ramp and drain included);
   kernels       the matvec (N = 1) and the blocked verify op (N = 2, 4, 6, 8) on the single-op shapes (Q4_K
                 17408 x 5120, Q6_K 5120 x 17408) and the lm_head matvec (Q6_K 248320 x 5120), mean and median
-                per-launch time, GB/s and fraction of 8 TB/s;
+                per-launch time, GB/s, fraction of 8 TB/s and of the read floor of the weights' bytes;
   forced        the same rounds with the drafts set to the greedy continuation (spec_set_drafts, the reference's
                 rollback-test hook) so that a chosen number m of them is accepted: tokens/s at full acceptance and
                 at the reference's measured mean (about 2 of 3 accepted per round at k = 3 on real weights,
@@ -83,10 +85,11 @@ def kernel_roofline(ctx, k):
     achieved = traffic_alg / (us * 1e-6) / 1e9
     for w in ws:
         w.free()
+    floor = aq.read_floor_time(ctx, traffic_alg)  # a plain streaming read of the same bytes, timed the same way
     return {"kernel": f"kq_wave_kernel Q4_K {rows}x{cols} N={n}", "us_per_launch": round(us, 3),
             "median_us": round(float(np.median(each)), 3),
             "p10_p90_us": [round(float(np.percentile(each, 10)), 3), round(float(np.percentile(each, 90)), 3)],
-            "bytes_per_launch": traffic_alg, "achieved_GBs": achieved}
+            "bytes_per_launch": traffic_alg, "achieved_GBs": achieved, "read_floor_us": round(floor, 3)}
 
 
 def kernel_sweep(ctx):
@@ -103,6 +106,7 @@ def kernel_sweep(ctx):
                                   (aq.Q6_K, 5120, 17408, 4, (64,)), (aq.Q8_0, 5120, 6144, 4, (64,))]:
         ws = [aq.SynthWeight(ctx, aq.synth_spec(t, rows, cols, seed=SEED + 200 + i)) for i in range(nw)]
         wbytes = rows * aq.row_bytes(t, cols)
+        floor = aq.read_floor_time(ctx, wbytes, iters=50 if wbytes > (256 << 20) else 500)  # the weights' bytes, plainly read
         for n in ns:
             x = np.random.default_rng(n).standard_normal((n, cols)).astype(np.float32)
             act = aq.Act(ctx, cols, n)
@@ -118,7 +122,8 @@ def kernel_sweep(ctx):
             gbs = nbytes / (us * 1e-6) / 1e9
             name = {aq.Q4_K: "Q4_K", aq.Q6_K: "Q6_K", aq.Q8_0: "Q8_0", aq.Q4_0: "Q4_0"}[t]
             out.append({"kernel": f"{name} {rows}x{cols}", "n": n, "us_per_launch": round(us, 2),
-                        "median_us": round(med, 2), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+                        "median_us": round(med, 2), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "read_floor_us": round(floor, 2), "of_read_floor": round(floor / us, 3)})
             y.free()
             act.free()
         for w in ws:
@@ -397,7 +402,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(kr["achieved_GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(kr["achieved_GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": kr["kernel"], "us_per_launch": kr["us_per_launch"], "median_us": kr["median_us"],
-                     "p10_p90_us": kr["p10_p90_us"], "bytes_per_launch": kr["bytes_per_launch"]},
+                     "p10_p90_us": kr["p10_p90_us"], "bytes_per_launch": kr["bytes_per_launch"],
+                     "read_floor_us": kr["read_floor_us"],
+                     "of_read_floor": round(kr["read_floor_us"] / kr["us_per_launch"], 3)},
         "kernels": ks,
         "round_roofline": {"bytes_per_round": rb, "ms_per_round": round(ms_round, 3),
                            "achieved_GBs": round(rb / (ms_round * 1e-3) / 1e9, 1),

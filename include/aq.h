@@ -236,6 +236,12 @@ int aq_matmul_time(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_
  * medians and spreads. No counterpart in the reference (its kernel benchmarks are Rust bench harnesses). */
 int aq_matmul_time_each(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, const aq_act *x, size_t ncols,
                         float *y_dev, int iters, float *us_each);
+/* Measurement only, no counterpart in the reference: the mean device time of `iters` back-to-back launches of a
+ * plain streaming-read kernel over `bytes` (a multiple of 16) of bufs_dev[i % nbuf] (16-byte aligned), 2048
+ * partial sums into partials_dev (>= 2048 floats) — the least time any kernel needs to read that many bytes, which
+ * bench.py reports beside the dominant kernel. */
+int aq_read_floor_time(aq_ctx *ctx, const void *const *bufs_dev, size_t nbuf, size_t bytes, float *partials_dev,
+                       int iters, double *us_per_launch);
 
 /* ------------------------------------------------------------------------------------------- model level */
 

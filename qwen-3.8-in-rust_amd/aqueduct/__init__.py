@@ -125,6 +125,7 @@ def lib():
         "aq_gguf_write_synth": (i, [C.c_char_p, P, i, C.c_uint64, i]),
         "aq_matmul_time": (i, [P, P, sz, P, sz, P, i, C.POINTER(C.c_double)]),
         "aq_matmul_time_each": (i, [P, P, sz, P, sz, P, i, P]),
+        "aq_read_floor_time": (i, [P, P, sz, sz, P, i, C.POINTER(C.c_double)]),
         "aq_synth_host": (i, [P, P, i]),
         "aq_weight_synth": (i, [P, P, C.POINTER(P)]),
         "aq_model_plan": (i, [P, i, C.c_uint64, P, sz, C.POINTER(sz)]),
@@ -411,6 +412,23 @@ def matmul_time_each(ctx: Context, ws, x: Act, ncols, y: DeviceBuffer, iters):
     out = np.zeros(iters, np.float32)
     check(lib().aq_matmul_time_each(ctx.h, arr, len(ws), x.h, ncols, y.p, iters, ptr(out)))
     return out
+
+
+def read_floor_time(ctx: Context, nbytes, iters=1000, nbuf=8):
+    """Mean device time (us) of a plain streaming read of `nbytes` (rounded down to 16), cycling over `nbuf`
+    buffers so the 256 MB MALL cannot serve it (aq_read_floor_time): the least time any kernel needs to read that
+    many bytes on this device."""
+    nbytes = nbytes // 16 * 16
+    bufs = [DeviceBuffer(ctx, nbytes) for _ in range(nbuf)]
+    part = DeviceBuffer(ctx, 2048 * 4)
+    arr = (C.c_void_p * nbuf)(*[b.p.value for b in bufs])
+    us = C.c_double()
+    check(lib().aq_read_floor_time(ctx.h, arr, nbuf, nbytes, part.p, 50, C.byref(us)))  # warm-up
+    check(lib().aq_read_floor_time(ctx.h, arr, nbuf, nbytes, part.p, iters, C.byref(us)))
+    for b in bufs:
+        b.free()
+    part.free()
+    return us.value
 
 
 class AqSynthSpec(C.Structure):

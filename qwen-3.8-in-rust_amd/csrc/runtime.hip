@@ -171,6 +171,26 @@ void free_act(Act &a) {
     a.base = nullptr;
 }
 
+// The read floor (measurement only): a plain streaming read of n4 float4s, grid-stride, one partial sum per
+// work-group into partials[blockIdx.x] — the least time any kernel needs to read that many bytes on the device.
+constexpr int READ_FLOOR_WGS = 2048;
+__global__ void __launch_bounds__(256) read_floor_kernel(const float4 *p, size_t n4, float *partials) {
+    float acc = 0.0f;
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+        const float4 v = p[i];
+        acc += (v.x + v.y) + (v.z + v.w);
+    }
+    __shared__ float red[256];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int off = 128; off >= 1; off >>= 1) {
+        if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partials[blockIdx.x] = red[0];
+}
+
 } // namespace aq
 
 using namespace aq;
@@ -533,6 +553,33 @@ int aq_matmul_time_each(aq_ctx *ctx, const aq_weight *const *ws, size_t nw, cons
     for (auto &e : ev)
         if (e) (void)hipEventDestroy(e);
     return rc;
+}
+
+int aq_read_floor_time(aq_ctx *ctx, const void *const *bufs_dev, size_t nbuf, size_t bytes, float *partials_dev,
+                       int iters, double *us_per_launch) {
+    AQ_REQUIRE(ctx && bufs_dev && nbuf > 0 && partials_dev && us_per_launch && iters > 0,
+               "aq_read_floor_time: bad argument");
+    AQ_REQUIRE(bytes >= 16 && bytes % 16 == 0, "aq_read_floor_time: bytes must be a positive multiple of 16");
+    for (size_t i = 0; i < nbuf; i++)
+        AQ_REQUIRE(bufs_dev[i] && ((uintptr_t)bufs_dev[i] & 15) == 0, "aq_read_floor_time: buffers must be 16-aligned");
+    AQ_HIP(hipSetDevice(ctx->device));
+    const size_t n4 = bytes / 16;
+    auto launch = [&](int i) {
+        hipLaunchKernelGGL(read_floor_kernel, dim3(READ_FLOOR_WGS), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<const float4 *>(bufs_dev[(size_t)i % nbuf]), n4, partials_dev);
+        return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "read_floor launch");
+    };
+    AQ_HIP(hipEventRecord(ctx->ev0, ctx->stream));
+    for (int i = 0; i < iters; i++) {
+        const int rc = launch(i);
+        if (rc) return rc;
+    }
+    AQ_HIP(hipEventRecord(ctx->ev1, ctx->stream));
+    AQ_HIP(hipEventSynchronize(ctx->ev1));
+    float ms = 0.0f;
+    AQ_HIP(hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
+    *us_per_launch = (double)ms * 1000.0 / iters;
+    return 0;
 }
 
 } // extern "C"

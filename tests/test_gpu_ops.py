@@ -224,3 +224,20 @@ def _single(ctx, xrow, t):
     a.quantize(t, 1)
     _single_cache.setdefault("keep", []).append(a)
     return a
+
+
+def test_read_floor_time(ctx):
+    """The measurement helper aq_read_floor_time (the plain streaming read bench.py reports beside the dominant
+    kernel): a positive time that grows with the bytes read, and a clear error for a size that is not whole
+    16-byte loads."""
+    say("read floor timing")
+    t_small = aq.read_floor_time(ctx, 1 << 20, iters=50, nbuf=2)
+    t_big = aq.read_floor_time(ctx, 64 << 20, iters=50, nbuf=2)
+    assert 0.0 < t_small < t_big
+    buf, part = aq.DeviceBuffer(ctx, 4096), aq.DeviceBuffer(ctx, 2048 * 4)
+    arr = (aq.C.c_void_p * 1)(buf.p.value)
+    us = aq.C.c_double()
+    rc = aq.lib().aq_read_floor_time(ctx.h, arr, 1, 4000 + 8, part.p, 1, aq.C.byref(us))
+    assert rc != 0 and "multiple of 16" in aq.lib().aq_last_error().decode()
+    buf.free()
+    part.free()
