@@ -59,6 +59,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel timing (for counter runs)")
     ap.add_argument("--sweep-only", action="store_true", help="only the matmul sweep (for kernel-trace runs)")
+    ap.add_argument("--prefill-only", action="store_true", help="only the prompt prefill timing (for kernel-trace runs)")
     return ap.parse_args()
 
 
@@ -292,11 +293,12 @@ def main():
         sys.exit(2)
     ctx = aq.Context(0)
     k = a.spec
-    ks = kernel_sweep(ctx) if not a.kernel_only else None  # also brings the clocks up before the roofline timing
+    # the sweep also brings the clocks up before the roofline timing
+    ks = kernel_sweep(ctx) if not (a.kernel_only or a.prefill_only) else None
     if a.sweep_only:
         print(json.dumps({"kernel_sweep": ks}), flush=True)
         return
-    kr = kernel_roofline(ctx, k)
+    kr = kernel_roofline(ctx, k) if not a.prefill_only else None
     if a.kernel_only:  # the counter runs: the dominant kernel plus a plain device copy of known size
         nbytes = 512 << 20
         src, dst = aq.DeviceBuffer(ctx, nbytes), aq.DeviceBuffer(ctx, nbytes)
@@ -326,6 +328,9 @@ def main():
     prefill = {"tokens": a.prompt, "ms": round(float(np.median(pre_ms[1:])), 3),
                "tokens_per_s": round(a.prompt / (float(np.median(pre_ms[1:])) * 1e-3), 1)}
     log(f"prefill: {prefill}")
+    if a.prefill_only:
+        print(json.dumps({"prefill": prefill}), flush=True)
+        return
 
     # plain greedy decode (reported beside the speculative number)
     ps = aq.State(model, 0, max_pos)

@@ -402,6 +402,10 @@ struct aq_state {
     hipStream_t stream = nullptr;
     hipEvent_t ev[5] = {};
     bool ev_pending = false;
+    // a prompt chunk's F32 projections run here beside the chunk's GEMMs (aux_in: their input is ready on `stream`;
+    // aux_out: their outputs are, before `stream` goes on)
+    hipStream_t aux = nullptr;
+    hipEvent_t aux_in = nullptr, aux_out = nullptr;
     uint32_t pos = 0, max_pos = 0, k = 0;
     int par = 0; // which conv window buffer is current
     std::vector<float *> rec, conv0, conv1, sv_mixed, sv_a, sv_b;
@@ -462,6 +466,7 @@ template <typename T> int dalloc_t(aq_state *s, size_t count, T **p) {
 void free_state(aq_state *s) {
     if (!s) return;
     if (s->stream) (void)hipStreamSynchronize(s->stream);
+    if (s->aux) (void)hipStreamSynchronize(s->aux);
     for (void *p : s->allocs) (void)hipFree(p);
     free_act(s->act_h);
     free_act(s->act_ffn);
@@ -471,6 +476,9 @@ void free_state(aq_state *s) {
     if (s->pinned) (void)hipHostFree(s->pinned);
     for (hipEvent_t e : s->ev)
         if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : {s->aux_in, s->aux_out})
+        if (e) (void)hipEventDestroy(e);
+    if (s->aux) (void)hipStreamDestroy(s->aux);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
 }
@@ -524,11 +532,27 @@ int mm(aq_state *s, const Weight &w, const Act &x, size_t t, float *y, const flo
 // Several matrices over the same activations: one grouped launch when they are K-quants of one K, optionally
 // followed by (at most two) F32 matrices.
 int mm_multi(aq_state *s, int n, const Weight *const *ws, float *const *ys, const Act &x, size_t t) {
-    if (t > (size_t)MAX_ROWS) { // a prompt chunk: each matrix over all its columns
+    if (t > (size_t)MAX_ROWS) {
+        // a prompt chunk: each matrix over all its columns; the F32 ones (few rows, latency-bound) on the auxiliary
+        // stream beside the others, joined before anything after this call runs on the state's stream
+        bool f32 = false;
+        for (int i = 0; i < n; i++) f32 = f32 || ws[i]->type == AQ_TYPE_F32;
+        if (f32) {
+            AQ_HIP(hipEventRecord(s->aux_in, s->stream));
+            AQ_HIP(hipStreamWaitEvent(s->aux, s->aux_in, 0));
+            for (int i = 0; i < n; i++) {
+                if (ws[i]->type != AQ_TYPE_F32) continue;
+                const int rc = launch_matmul_many(*ws[i], x, t, ys[i], nullptr, s->aux);
+                if (rc) return rc;
+            }
+            AQ_HIP(hipEventRecord(s->aux_out, s->aux));
+        }
         for (int i = 0; i < n; i++) {
+            if (ws[i]->type == AQ_TYPE_F32) continue;
             const int rc = mm(s, *ws[i], x, t, ys[i]);
             if (rc) return rc;
         }
+        if (f32) AQ_HIP(hipStreamWaitEvent(s->stream, s->aux_out, 0));
         return 0;
     }
     bool grouped = is_kquant(ws[0]->type);
@@ -944,6 +968,9 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
     if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) rc = fail(AQ_EHIP, "state: stream");
     for (hipEvent_t &e : s->ev)
         if (!rc && hipEventCreate(&e) != hipSuccess) rc = fail(AQ_EHIP, "state: event");
+    if (!rc && hipStreamCreateWithFlags(&s->aux, hipStreamNonBlocking) != hipSuccess) rc = fail(AQ_EHIP, "state: stream");
+    for (hipEvent_t *e : {&s->aux_in, &s->aux_out})
+        if (!rc && hipEventCreateWithFlags(e, hipEventDisableTiming) != hipSuccess) rc = fail(AQ_EHIP, "state: event");
     s->rec.assign(c.n_layer, nullptr);
     s->conv0.assign(c.n_layer, nullptr);
     s->conv1.assign(c.n_layer, nullptr);
