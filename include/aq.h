@@ -151,6 +151,13 @@ int aq_act_get_q8_0(const aq_act *a, void *ggml_out, size_t ncols);
  * switch, K-quant weights take `dot_q4_k_q8` / `dot_q5_k_q8` / `dot_q6_k_q8` (dot.rs:69-160). `y_dev` is a device
  * buffer of ncols * rows f32. The activation must have been quantised for w's type under the same switch. */
 int aq_matmul(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, float *y_dev);
+/* aq_act_quantize and aq_matmul on the caller's HIP stream (`stream`: a hipStream_t of the context's device; NULL:
+ * the context's own), returning once the work is queued, without synchronising: the forms for a caller that orders
+ * its work on a stream of its own (the reference's operators, matvec.rs:336 and :377, are synchronous calls into its
+ * thread pool). The caller orders the activation's f32 rows before the quantisation on that stream, and reads y_dev
+ * only after the stream has reached it. Same kernels, same bits as the synchronous forms. */
+int aq_act_quantize_on(aq_act *a, int weight_type, size_t ncols, void *stream);
+int aq_matmul_on(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, float *y_dev, void *stream);
 /* The exact integers of the K-quant dot, from the same kernel and grid aq_matmul runs (instantiated with its
  * integer outputs on): per column c < ncols (1, 4 or 8), row and super-block the 8 i32 lane sums and (Q4_K/Q5_K) the
  * 4 i32 min products the reference keeps in `sumi` / `prod` (kdot.rs:37-140; Q6_K lanes after the -32 fold).

@@ -126,6 +126,8 @@ def lib():
         "aq_matmul_time": (i, [P, P, sz, P, sz, P, i, C.POINTER(C.c_double)]),
         "aq_matmul_time_each": (i, [P, P, sz, P, sz, P, i, P]),
         "aq_read_floor_time": (i, [P, P, sz, sz, P, i, C.POINTER(C.c_double)]),
+        "aq_act_quantize_on": (i, [P, i, sz, P]),
+        "aq_matmul_on": (i, [P, P, P, sz, P, P]),
         "aq_synth_host": (i, [P, P, i]),
         "aq_weight_synth": (i, [P, P, C.POINTER(P)]),
         "aq_model_plan": (i, [P, i, C.c_uint64, P, sz, C.POINTER(sz)]),
@@ -412,6 +414,17 @@ def matmul_time_each(ctx: Context, ws, x: Act, ncols, y: DeviceBuffer, iters):
     out = np.zeros(iters, np.float32)
     check(lib().aq_matmul_time_each(ctx.h, arr, len(ws), x.h, ncols, y.p, iters, ptr(out)))
     return out
+
+
+def quantize_on(a, weight_type, ncols, stream):
+    """aq_act_quantize on a caller's HIP stream (an integer hipStream_t, e.g. torch.cuda.Stream().cuda_stream),
+    queued without waiting."""
+    check(lib().aq_act_quantize_on(a.h, weight_type, ncols, C.c_void_p(stream)))
+
+
+def matmul_on(ctx: Context, w, a, ncols, y: DeviceBuffer, stream):
+    """aq_matmul into the device buffer y on a caller's HIP stream, queued without waiting."""
+    check(lib().aq_matmul_on(ctx.h, w.h, a.h, ncols, y.p, C.c_void_p(stream)))
 
 
 def read_floor_time(ctx: Context, nbytes, iters=1000, nbuf=8):

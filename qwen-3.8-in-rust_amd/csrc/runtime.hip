@@ -362,20 +362,28 @@ int aq_act_set_f32(aq_act *a, const float *host, size_t ncols) {
     return 0;
 }
 
-int aq_act_quantize(aq_act *a, int weight_type, size_t ncols) {
+static int act_quantize(aq_act *a, int weight_type, size_t ncols, hipStream_t stream) {
     AQ_REQUIRE(a, "aq_act_quantize: null act");
     AQ_REQUIRE(ncols >= 1 && ncols <= a->a.ncols, "aq_act_quantize: ncols out of range");
     AQ_HIP(hipSetDevice(a->ctx->device));
     if (is_kquant(weight_type) && !q8_fine()) {
         AQ_REQUIRE(a->a.n % 256 == 0, "aq_act_quantize: Q8_K needs n % 256 == 0 (matvec.rs:73-77)");
-        return launch_q8k_quantize(a->a, ncols, a->a.f32, a->a.n, a->ctx->stream);
+        return launch_q8k_quantize(a->a, ncols, a->a.f32, a->a.n, stream);
     }
     if (is_kquant(weight_type) || weight_type == AQ_TYPE_Q8_0 || weight_type == AQ_TYPE_Q4_0) {
         AQ_REQUIRE(a->a.n % 32 == 0, "aq_act_quantize: Q8_0 needs n % 32 == 0");
-        return launch_q8_0_quantize(a->a, ncols, a->a.f32, a->a.n, a->ctx->stream);
+        return launch_q8_0_quantize(a->a, ncols, a->a.f32, a->a.n, stream);
     }
     if (weight_type == AQ_TYPE_F32) return 0;
     return fail(AQ_EUNSUP, "aq_act_quantize: unsupported weight type");
+}
+
+int aq_act_quantize(aq_act *a, int weight_type, size_t ncols) {
+    return act_quantize(a, weight_type, ncols, a ? a->ctx->stream : nullptr);
+}
+
+int aq_act_quantize_on(aq_act *a, int weight_type, size_t ncols, void *stream) {
+    return act_quantize(a, weight_type, ncols, stream ? (hipStream_t)stream : (a ? a->ctx->stream : nullptr));
 }
 
 int aq_act_get_q8k(const aq_act *a, void *ggml_out, size_t ncols) {
@@ -440,6 +448,14 @@ int aq_matmul(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, fl
     if (rc) return rc;
     AQ_HIP(hipStreamSynchronize(ctx->stream));
     return 0;
+}
+
+int aq_matmul_on(aq_ctx *ctx, const aq_weight *w, const aq_act *x, size_t ncols, float *y_dev, void *stream) {
+    AQ_REQUIRE(ctx, "aq_matmul_on: null ctx");
+    int rc = check_matmul(w, x, ncols, y_dev);
+    if (rc) return rc;
+    AQ_HIP(hipSetDevice(ctx->device));
+    return launch_matmul_many(w->w, x->a, ncols, y_dev, nullptr, stream ? (hipStream_t)stream : ctx->stream);
 }
 
 int aq_set_q8_fine(int on) {

@@ -101,3 +101,34 @@ def test_f32_many_columns_equal_the_oracle(ctx, ncols):
     host, w, a, x, y = run(ctx, aq.F32, rows, cols, ncols, 808 + ncols)
     want = O.matmul(aq.F32, host, rows, cols, x, threads=8)
     assert np.array_equal(bits(y), bits(want))
+
+
+@pytest.mark.parametrize("t,rows,cols,ncols", [(aq.Q4_K, 1024, 5120, 4), (aq.Q6_K, 520, 2048, 33),
+                                               (aq.Q8_0, 300, 1024, 1)])
+def test_quantize_and_matmul_on_a_caller_stream(ctx, t, rows, cols, ncols):
+    """aq_act_quantize_on / aq_matmul_on queued on a stream the caller created (here through the HIP runtime this
+    process already has loaded, the one libaq uses) give the synchronous calls' bits."""
+    print(f"case caller stream type {t} {rows}x{cols} N={ncols}", flush=True)
+    hip = aq.C.CDLL("libamdhip64.so.7")  # already mapped by libaq: the same runtime instance
+    spec = aq.synth_spec(t, rows, cols, seed=31 + t)
+    w = aq.SynthWeight(ctx, spec)
+    x = (np.random.default_rng(5).standard_normal((ncols, cols)) * 1.5).astype(np.float32)
+    a_sync = aq.Act(ctx, cols, ncols)
+    a_sync.set(x)
+    a_sync.quantize(t, ncols)
+    want = aq.matmul(ctx, w, a_sync, ncols)
+    a = aq.Act(ctx, cols, ncols)
+    a.set(x)
+    y = aq.DeviceBuffer(ctx, ncols * rows * 4)
+    s = aq.C.c_void_p()
+    assert hip.hipStreamCreate(aq.C.byref(s)) == 0
+    try:
+        aq.quantize_on(a, t, ncols, s.value)
+        aq.matmul_on(ctx, w, a, ncols, y, s.value)
+        assert hip.hipStreamSynchronize(s) == 0
+    finally:
+        hip.hipStreamDestroy(s)
+    got = y.download(np.float32, ncols * rows).reshape(ncols, rows)
+    assert np.array_equal(bits(got), bits(want))
+    for o in (y, a, a_sync):
+        o.free()
