@@ -363,12 +363,18 @@ int aq_layer_run(aq_ctx *ctx, const aq_model_config *cfg, const aq_tensor *tenso
                  float *v_cache, uint32_t *kv_len, uint32_t kv_cap, float *y);
 
 /* The Gated-DeltaNet recurrence alone (deltanet.rs:43-86), with speculative rollback: from `state_dev`
- * (nv x dk x dv f32, device), t rows of q, k (t x nk*dk, already normalised), v (t x nv*dv), g and beta
+ * (nv x dk x dv f32, device), t rows (1..8: one verify batch) of q, k (t x nk*dk, already normalised), v (t x nv*dv), g and beta
  * (t x nv) give out (t x nv*dv); the state is then advanced by the first `keep` rows only (keep <= t),
  * as the reference's snapshot / restore / replay leaves it (spec.rs:154-179, 396-415). Host arrays. */
 int aq_deltanet_verify_commit(aq_ctx *ctx, uint32_t nk, uint32_t nv, uint32_t dk, uint32_t dv, size_t t, size_t keep,
                               const float *q, const float *k, const float *v, const float *g, const float *beta,
                               float *state_dev, float *out);
+/* The same on device arrays (q_dev .. beta_dev as above, out_dev t x nv*dv): nothing allocated or copied, the two
+ * launches queued on the context's stream, which is synchronised before the call returns. t is one verify batch
+ * (1..8), as for the host form. */
+int aq_deltanet_verify_commit_dev(aq_ctx *ctx, uint32_t nk, uint32_t nv, uint32_t dk, uint32_t dv, size_t t,
+                                  size_t keep, const float *q_dev, const float *k_dev, const float *v_dev,
+                                  const float *g_dev, const float *beta_dev, float *state_dev, float *out_dev);
 
 /* The device's scalar activations, elementwise on host arrays (fn: 0 exp, 1 log1p, 2 silu, 3 sigmoid, 4 softplus;
  * act.rs:7-40). No counterpart in the reference: the parity tests use it to show the device evaluates exp and

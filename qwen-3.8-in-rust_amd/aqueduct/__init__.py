@@ -151,6 +151,8 @@ def lib():
         "aq_eval_math": (i, [P, i, P, P, sz]),
         "aq_deltanet_verify_commit": (i, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, sz, sz, P, P, P, P, P,
                                           P, P]),
+        "aq_deltanet_verify_commit_dev": (i, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, sz, sz, P, P, P, P,
+                                              P, P, P]),
     }
     for name, (res, args) in sigs.items():
         f = getattr(L, name)
@@ -676,6 +678,12 @@ def deltanet_verify_commit(ctx: Context, nk, nv, dk, dv, keep, q, k, v, g, beta,
     check(lib().aq_deltanet_verify_commit(ctx.h, nk, nv, dk, dv, t, keep, ptr(q), ptr(k), ptr(v), ptr(g), ptr(beta),
                                           state.p, ptr(out)))
     return out
+
+
+def deltanet_verify_commit_dev(ctx: Context, nk, nv, dk, dv, t, keep, q, k, v, g, beta, state, out):
+    """aq_deltanet_verify_commit_dev: the same on DeviceBuffers (q, k, v, g, beta, state, out), nothing allocated."""
+    check(lib().aq_deltanet_verify_commit_dev(ctx.h, nk, nv, dk, dv, t, keep, q.p, k.p, v.p, g.p, beta.p, state.p,
+                                              out.p))
 
 
 def eval_math(ctx: Context, fn, x):

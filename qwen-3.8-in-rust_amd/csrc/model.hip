@@ -1535,12 +1535,47 @@ int aq_eval_math(aq_ctx *ctx, int fn, const float *x, float *y, size_t n) {
     return rc;
 }
 
+int aq_deltanet_verify_commit_dev(aq_ctx *ctx, uint32_t nk, uint32_t nv, uint32_t dk, uint32_t dv, size_t t,
+                                  size_t keep, const float *q_dev, const float *k_dev, const float *v_dev,
+                                  const float *g_dev, const float *beta_dev, float *state_dev, float *out_dev) {
+    AQ_REQUIRE(ctx && q_dev && k_dev && v_dev && g_dev && beta_dev && state_dev && out_dev,
+               "aq_deltanet_verify_commit: null argument");
+    AQ_REQUIRE(t >= 1 && t <= 8 && keep <= t, "aq_deltanet_verify_commit: 1 <= t <= 8 (one verify batch), keep <= t");
+    AQ_REQUIRE(nk >= 1 && nv % nk == 0, "aq_deltanet_verify_commit: heads");
+    AQ_HIP(hipSetDevice(ctx->device));
+    DnArgs d;
+    d.raw = 1;
+    d.rq = q_dev;
+    d.rk = k_dev;
+    d.rv = v_dev;
+    d.rg = g_dev;
+    d.rbeta = beta_dev;
+    d.rec = state_dev;
+    d.nk = (int)nk;
+    d.nv = (int)nv;
+    d.dk = (int)dk;
+    d.dv = (int)dv;
+    // verify: every row's output from the committed state, the state untouched
+    d.t = (int)t;
+    d.write_state = 0;
+    d.out = out_dev;
+    int rc = launch_dn_core(d, ctx->stream);
+    // commit: the kept rows again, state written (the outputs of the kept rows are recomputed identically)
+    if (!rc && keep > 0) {
+        d.t = (int)keep;
+        d.write_state = 1;
+        d.out = nullptr;
+        rc = launch_dn_core(d, ctx->stream);
+    }
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess && !rc) rc = fail(AQ_EHIP, "deltanet: sync");
+    return rc;
+}
+
 int aq_deltanet_verify_commit(aq_ctx *ctx, uint32_t nk, uint32_t nv, uint32_t dk, uint32_t dv, size_t t, size_t keep,
                               const float *q, const float *k, const float *v, const float *g, const float *beta,
                               float *state_dev, float *out) {
     AQ_REQUIRE(ctx && q && k && v && g && beta && state_dev && out, "aq_deltanet_verify_commit: null argument");
-    AQ_REQUIRE(t >= 1 && t <= 64 && keep <= t, "aq_deltanet_verify_commit: 1 <= t <= 64, keep <= t");
-    AQ_REQUIRE(nk >= 1 && nv % nk == 0, "aq_deltanet_verify_commit: heads");
+    AQ_REQUIRE(t >= 1 && t <= 8 && keep <= t, "aq_deltanet_verify_commit: 1 <= t <= 8 (one verify batch), keep <= t");
     AQ_HIP(hipSetDevice(ctx->device));
     const size_t kd = (size_t)nk * dk, vd = (size_t)nv * dv;
     const size_t bytes[5] = {t * kd * 4, t * kd * 4, t * vd * 4, t * nv * 4, t * nv * 4};
@@ -1553,33 +1588,11 @@ int aq_deltanet_verify_commit(aq_ctx *ctx, uint32_t nk, uint32_t nv, uint32_t dk
             rc = fail(AQ_EHIP, "deltanet: upload");
     }
     if (!rc && dev_malloc(&dev[5], t * vd * 4 + 256) != hipSuccess) rc = fail(AQ_ENOMEM, "deltanet: output");
-    DnArgs d;
-    d.raw = 1;
-    d.rq = dev[0];
-    d.rk = dev[1];
-    d.rv = dev[2];
-    d.rg = dev[3];
-    d.rbeta = dev[4];
-    d.rec = state_dev;
-    d.nk = (int)nk;
-    d.nv = (int)nv;
-    d.dk = (int)dk;
-    d.dv = (int)dv;
-    // verify: every row's output from the committed state, the state untouched
-    d.t = (int)t;
-    d.write_state = 0;
-    d.out = dev[5];
-    if (!rc) rc = launch_dn_core(d, ctx->stream);
-    // commit: the kept rows again, state written (the outputs of the kept rows are recomputed identically)
-    if (!rc && keep > 0) {
-        d.t = (int)keep;
-        d.write_state = 1;
-        d.out = nullptr;
-        rc = launch_dn_core(d, ctx->stream);
-    }
-    if (!rc && hipMemcpyAsync(out, dev[5], t * vd * 4, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess)
+    if (!rc) rc = aq_deltanet_verify_commit_dev(ctx, nk, nv, dk, dv, t, keep, dev[0], dev[1], dev[2], dev[3], dev[4],
+                                                state_dev, dev[5]);
+    if (!rc && hipMemcpy(out, dev[5], t * vd * 4, hipMemcpyDeviceToHost) != hipSuccess)
         rc = fail(AQ_EHIP, "deltanet: download");
-    if (hipStreamSynchronize(ctx->stream) != hipSuccess && !rc) rc = fail(AQ_EHIP, "deltanet: sync");
+    (void)hipStreamSynchronize(ctx->stream);
     for (float *p : dev)
         if (p) (void)hipFree(p);
     return rc;

@@ -361,6 +361,21 @@ def test_deltanet_recurrence_rollback(ctx):
         st2.upload(s0)
         aq.deltanet_verify_commit(ctx, nk, nv, dk, dv, keep, q[:keep], k[:keep], v[:keep], g[:keep], beta[:keep], st2)
         s_seq = st2.download(np.float32, s0.size).reshape(s0.shape)
+        # the device-array form: same bits, no allocation
+        bufs = []
+        for arr in (q, k, v, g, beta):
+            b = aq.DeviceBuffer(ctx, arr.nbytes)
+            b.upload(arr)
+            bufs.append(b)
+        st3, ob = aq.DeviceBuffer(ctx, s0.nbytes), aq.DeviceBuffer(ctx, out_g.nbytes)
+        st3.upload(s0)
+        before = aq.alloc_counts()
+        aq.deltanet_verify_commit_dev(ctx, nk, nv, dk, dv, t, keep, *bufs, st3, ob)
+        assert aq.alloc_counts() == before, "the device-array form allocated"
+        assert np.array_equal(ob.download(np.float32, out_g.size).reshape(out_g.shape), out_g)
+        assert np.array_equal(st3.download(np.float32, s0.size).reshape(s0.shape), s_dev)
+        for b in bufs + [st3, ob]:
+            b.free()
         r_out, r_state = rel(out_g, out_o), rel(s_dev, s_keep)
         print(f"deltanet keep {keep}: out rel {r_out:.2e}, state rel {r_state:.2e}, "
               f"exact {np.array_equal(out_g, out_o)}/{np.array_equal(s_dev, s_keep)}", flush=True)
