@@ -20,6 +20,9 @@ ARCH = "gfx950"
 COMMON = ["-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-mllvm", "-amdgpu-mfma-vgpr-form",  # matrix-core results in VGPRs: no accumulator-register copies
+          # the leading scalar / pointer kernel arguments arrive in SGPRs at wave launch instead of by a scalar load
+          # from the kernel-argument segment (the small kernels' first loads no longer wait on it)
+          "-mllvm", "-amdgpu-kernarg-preload-count=16",
           "-Wall", "-Wno-unused-function",
           "-Wno-unused-variable", "-Wno-unused-but-set-variable"]
 
