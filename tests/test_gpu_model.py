@@ -439,3 +439,26 @@ def test_tiny_prompt_chunks_equal_token_by_token_and_oracle(ctx, tiny):
     for _ in range(4):  # and decoding continues identically
         tg, tf = g.forward_token(tg), f.forward_token(tf)
         assert tg == tf
+
+
+def test_tiny_prompt_past_the_attention_lds_equals_token_by_token(ctx, tiny):
+    """A 16,400-token prompt on the tiny model, whose attention kernel keeps the scores of at most 16,288 positions
+    in LDS (head_dim 64): the chunks before that run attention over the whole chunk, the chunk that crosses it and
+    those after run it in 8-row pieces with the score rows in device memory. Logits and the whole state equal a
+    token-by-token feed of the same prompt, bit for bit (model.rs:443-461: prefill row i is forward_token on row i)."""
+    n = 16400
+    print(f"case tiny {n}-token prompt across the attention LDS limit", flush=True)
+    prompt = np.random.default_rng(SEED + 11).integers(0, tiny["cfg"].vocab, n).astype(np.uint32)
+    g = aq.State(tiny["gm"], 0, n + 16)
+    tg, lg = g.prefill(prompt, want_logits=True)
+    f = aq.State(tiny["gm"], 0, n + 16)
+    f.prefill(prompt[:1])
+    for i, tok in enumerate(prompt[1:-1]):
+        f.forward_token(int(tok))
+        if i % 4096 == 0:
+            print(f"token-by-token feed at {i + 1}", flush=True)
+    tf, lf = f.forward_token(int(prompt[-1]), want_logits=True)
+    assert tf == tg and np.array_equal(lf, lg), "chunked prefill past the LDS limit differs from the token feed"
+    assert np.array_equal(f.export(), g.export())
+    g.free()
+    f.free()
