@@ -24,9 +24,11 @@ Printed as one JSON line, with
   prefill       the 64-token prompt's prefill (one pass over the weights per chunk of up to 64 rows) on a fresh state;
   sustained     --spec 3 rounds kept running for --sustain-seconds after the timed ones (the GPU busy long enough to
                 be seen by a utilisation sampler), tokens/s over that stretch;
-  cpu_baseline  the CPU oracle (a scalar C restatement of the reference's CPU path, not its hand-written AVX2
-                kernels) on the box's physical cores (at most 16, the box's share): config 4's 64-token prompt, then
-                --spec 3 rounds for --cpu-seconds, plus its matvec / verify GB/s at the config-2/3 shapes;
+  cpu_baseline  the CPU oracle (a C restatement of the reference's CPU path whose K-quant and Q8_0 / Q4_0 dots
+                run in AVX2 forms bit-identical to its scalar ones, as the reference's avx2.rs kernels are) on the
+                box's physical cores (at most 16, the box's share): config 4's 64-token prompt, then --spec 3
+                rounds for --cpu-seconds, plus its matvec / verify GB/s at the config-2/3 shapes (and the scalar
+                dots' GB/s beside them);
 and the per-round byte model (weights read once + DeltaNet state + KV + MTP) as round_roofline.
 """
 import argparse
@@ -205,10 +207,20 @@ def cpu_matmul_gbs(O, threads):
 def cpu_baseline(cfg, plan, k, seconds, gpu_model, prompt):
     """The CPU oracle on the same synthetic 27B model and config 4's prompt: the prefill, then --spec k rounds until
     `seconds` of rounds have run (tokens/s over the rounds). Also checks that the device emits the same ids for the
-    same prompt over those rounds, and times the oracle's matvec / verify op alone."""
+    same prompt over those rounds, and times the oracle's matvec / verify op alone. The oracle runs with its AVX2
+    dots on (oracle_simd.c, bit-identical to its scalar ones), as the reference's CPU path runs its avx2.rs kernels;
+    the scalar dots' matvec / verify GB/s are reported beside them."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O  # the checker / CPU baseline only
 
+    with O.simd(True):
+        res = cpu_baseline_run(O, cfg, plan, k, seconds, gpu_model, prompt)
+    with O.simd(False):
+        res["matmul_scalar"] = cpu_matmul_gbs(O, res["cores"])
+    return res
+
+
+def cpu_baseline_run(O, cfg, plan, k, seconds, gpu_model, prompt):
     info = cpu_info()
     threads = max(1, min(16, info["physical_cores"]))  # cpu.rs:1-12 uses the physical cores; the box's share is 16
     t0 = time.time()
@@ -224,7 +236,7 @@ def cpu_baseline(cfg, plan, k, seconds, gpu_model, prompt):
     prefill_s = time.time() - t0
     log(f"cpu baseline: {len(prompt)}-token spec prefill in {prefill_s:.1f} s")
     rounds, emitted, t_rounds = 0, 0, 0.0
-    while (t_rounds < seconds or rounds < 2) and rounds < 40:
+    while (t_rounds < seconds or rounds < 2) and rounds < 200:  # the state holds prompt + 256 positions
         t1 = time.time()
         m, em = st.spec_round(out[-1])
         t_rounds += time.time() - t1
@@ -243,8 +255,9 @@ def cpu_baseline(cfg, plan, k, seconds, gpu_model, prompt):
     return {"value": round(emitted / t_rounds, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"27B-shape Q4_K_M, {len(prompt)}-token prompt (spec prefill {prefill_s:.1f} s, not in the "
                       f"rate), then {rounds} greedy --spec {k} rounds ({emitted} tokens, {t_rounds:.1f} s) on the "
-                      f"scalar C restatement of the reference's CPU path (not its hand-written AVX2 kernels), "
-                      f"{threads} threads on physical cores",
+                      f"C restatement of the reference's CPU path with AVX2 forms of its K-quant x Q8_K and "
+                      f"Q8_0 / Q4_0 dots (bit-identical to the scalar restatement, as the reference's avx2.rs "
+                      f"kernels are to its scalar ones), {threads} threads on physical cores",
             "cpu": info, "prefill_s": round(prefill_s, 2), "matmul": mm, "ids_match_device": bool(match)}
 
 

@@ -11,7 +11,7 @@ import subprocess
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-SOURCES = ["oracle_kernels.c", "oracle_model.c", "oracle_sample.c"]
+SOURCES = ["oracle_kernels.c", "oracle_model.c", "oracle_sample.c", "oracle_simd.c"]
 LIB = os.path.join(HERE, "liboracle.so")
 
 MATH_DIR = os.path.join(os.path.dirname(HERE), "qwen-3.8-in-rust_amd", "csrc")  # aq_math.h, shared with the device

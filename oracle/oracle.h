@@ -48,6 +48,10 @@ float or_dot_f32(const float *w, const float *x, size_t n);
  * Q8_0 activations (dot.rs:69-160). */
 void or_set_q8_fine(int on);
 int or_q8_fine(void);
+/* The AVX2 forms of the K-quant x Q8_K and Q8_0 / Q4_0 dots (oracle_simd.c; the reference's avx2.rs kernels are
+ * selected the same way, kdot.rs:147, 318): process-wide, off by default; the bits are the scalar forms'. */
+void or_set_simd(int on);
+int or_simd(void);
 void or_matmul(int type, const uint8_t *w, size_t rows, size_t cols, const float *x, size_t ncols, float *y,
                int threads);
 

@@ -33,5 +33,8 @@ void or_q8_from_ggml(const uint8_t *in, size_t n, or_q8 *r);
 float or_dot_q8k_row(int type, const uint8_t *w, const or_q8k *x);
 void or_dot_q8k_rows(int type, const uint8_t *w, const or_q8k *const *xs, size_t t, float *out);
 float or_dot_q8_row(int type, const uint8_t *w, const or_q8 *x);
+/* oracle_simd.c: AVX2 forms, bit-identical to the two above (K-quant rows; Q8_0 / Q4_0 weights) */
+void or_dot_q8k_rows_simd(int type, const uint8_t *w, const or_q8k *const *xs, size_t t, float *out);
+float or_dot_q8_row_simd(int type, const uint8_t *w, const or_q8 *x);
 
 #endif

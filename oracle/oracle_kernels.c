@@ -429,8 +429,17 @@ float or_dot_q8k_row(int type, const uint8_t *w, const or_q8k *x) {
 }
 
 /* kdot.rs:176-333 the blocked form: codes and scales unpacked once per super-block, then each activation row
- * gets the arithmetic of the single-row kernel, so out[i] == or_dot_q8k_row(w, xs[i]) bit for bit. */
+ * gets the arithmetic of the single-row kernel, so out[i] == or_dot_q8k_row(w, xs[i]) bit for bit. With the simd
+ * switch on, the AVX2 form (oracle_simd.c, the same bits) runs instead. */
+static void dot_q8k_rows_scalar(int type, const uint8_t *w, const or_q8k *const *xs, size_t t, float *out);
 void or_dot_q8k_rows(int type, const uint8_t *w, const or_q8k *const *xs, size_t t, float *out) {
+    if (or_simd())
+        or_dot_q8k_rows_simd(type, w, xs, t, out);
+    else
+        dot_q8k_rows_scalar(type, w, xs, t, out);
+}
+
+static void dot_q8k_rows_scalar(int type, const uint8_t *w, const or_q8k *const *xs, size_t t, float *out) {
     size_t bb = kq_block_bytes(type);
     size_t nb = xs[0]->nb;
     float acc[16][8], accm[16][4];
@@ -616,6 +625,7 @@ static float dot_q6_k_q8(const uint8_t *w, const or_q8 *x) {
 /* dot.rs:29-45 `dot_q8_0_q8` and dot.rs:48-66 `dot_q4_0_q8`: one f32 accumulator, blocks left to right; K-quant
  * weights take the Q8_0-grain kernels above (dot.rs:202-226 `dot_q8` routes every type). */
 float or_dot_q8_row(int type, const uint8_t *w, const or_q8 *x) {
+    if (or_simd() && (type == AQ_TYPE_Q8_0 || type == AQ_TYPE_Q4_0)) return or_dot_q8_row_simd(type, w, x);
     if (type == AQ_TYPE_Q4_K || type == AQ_TYPE_Q5_K) return dot_q45_k_q8(type == AQ_TYPE_Q5_K, w, x);
     if (type == AQ_TYPE_Q6_K) return dot_q6_k_q8(w, x);
     float acc = 0.0f;

@@ -90,6 +90,8 @@ def lib():
         "or_matmul": (None, [C.c_int, P, sz, sz, P, sz, P, C.c_int]),
         "or_set_q8_fine": (None, [C.c_int]),
         "or_q8_fine": (C.c_int, []),
+        "or_set_simd": (None, [C.c_int]),
+        "or_simd": (C.c_int, []),
         "or_rmsnorm": (None, [P, P, C.c_float, P, sz]),
         "or_rmsnorm_gated": (None, [P, P, P, C.c_float, P, sz]),
         "or_softmax": (None, [P, P, sz]),
@@ -221,6 +223,21 @@ class q8_fine:
 
     def __exit__(self, *exc):
         lib().or_set_q8_fine(self.prev)
+
+
+class simd:
+    """Context manager: the oracle's AVX2 dots (oracle_simd.c, bit-identical to the scalar ones) on inside the block."""
+
+    def __init__(self, on=True):
+        self.on = on
+
+    def __enter__(self):
+        self.prev = lib().or_simd()
+        lib().or_set_simd(1 if self.on else 0)
+        return self
+
+    def __exit__(self, *exc):
+        lib().or_set_simd(self.prev)
 
 
 def matmul(t, w, rows, cols, x, threads=4):
