@@ -7,10 +7,13 @@ in the Q4_K_M mix, generated on the device, against the CPU oracle holding the s
 * greedy decoding: device plain ids == device --spec 3 ids == oracle --spec 3 ids over 6 tokens, round by round
   the oracle's drafts and accepted counts (tests/spec_identity.rs:34-119 at the full shape);
 * forced drafts accepted up to position m = 1, 2, 3, 0: after every round the device state equals the plain
-  state at the same position bit for bit, and the oracle's (tests/spec_identity.rs:136-170 at the full shape).
+  state at the same position bit for bit, and the oracle's (tests/spec_identity.rs:136-170 at the full shape);
+* config 4 as the bench runs it (a 64-token prompt, then 12 --spec 3 rounds and 4 forced rounds accepting 3, 1, 2, 0):
+  drafts, accepted counts and emitted ids equal the oracle's round by round, and the whole state after the last
+  round is bit-identical.
 
-The oracle is the checker only (a C restatement of the reference's CPU path, oracle/); it runs on the host cores
-at ~4 s per 27B token, so the sample stays short.
+The oracle is the checker only (a C restatement of the reference's CPU path, oracle/); with its scalar dots it runs
+at ~4 s per 27B token on the host cores, so those samples stay short; the config-4 sample runs its AVX2 dots.
 """
 import os
 import sys
@@ -129,6 +132,52 @@ def test_27b_forced_drafts_rollback_state(big):
         assert np.array_equal(a[: b.size], b), f"round {r}: spec state differs from the plain state"
         assert np.array_equal(a, os_.export()), f"round {r}: spec state differs from the oracle's"
         assert gs.drafts() == os_.drafts()
+
+
+def test_27b_config4_prompt_spec3_rounds_match_oracle(big):
+    """Config 4 as the bench runs it: a 64-token seeded prompt through the spec prefill (one 64-row chunk on the
+    device), then 12 greedy --spec 3 rounds and 4 rounds whose drafts are forced to accept 3, 1, 2 and 0 tokens of
+    the plain continuation; round by round the drafts, the accepted count and the emitted ids equal the oracle's
+    (and the plain ids), and after the last round every per-layer state tensor is bit-identical. The oracle runs its AVX2
+    dots here (bit-identical to its scalar ones, tests/test_oracle_simd.py), which makes this sample affordable."""
+    print("case 27B config 4: 64-token prompt, 12 --spec 3 rounds vs the oracle", flush=True)
+    prompt = np.random.default_rng(SEED).integers(0, big["cfg"].vocab, 64).astype(np.uint32)
+    gs = aq.State(big["gm"], 3, 160)
+    os_ = O.State(big["om"], 3, 160)
+    with O.simd(True):
+        g = [gs.spec_prefill(prompt)]
+        o = [os_.spec_prefill(prompt)]
+        assert g == o
+        for r in range(12):
+            gd, od = gs.drafts(), os_.drafts()
+            m, em = gs.spec_round(g[-1])
+            mo, emo = os_.spec_round(o[-1])
+            print(f"27B config 4 round {r}: drafts {gd} accepted {m} emitted {em}", flush=True)
+            assert gd == od and (m, em) == (mo, emo), f"round {r}"
+            g += em
+            o += emo
+        # then forced rounds accepting 3, 1, 2, 0 drafts of the plain continuation (spec_identity.rs:136-170)
+        gp = aq.State(big["gm"], 0, 160)
+        plain = [gp.prefill(prompt)]
+        while len(plain) < len(g) + 16:
+            plain.append(gp.forward_token(plain[-1]))
+        assert plain[:len(g)] == g
+        vocab = big["cfg"].vocab
+        for r, n_ok in enumerate([3, 1, 2, 0]):
+            j = len(g)
+            d = [plain[j + i] if i < n_ok else (plain[j + i] + 1) % vocab for i in range(3)]
+            gs.set_drafts(d)
+            os_.set_drafts(d)
+            m, em = gs.spec_round(g[-1])
+            mo, emo = os_.spec_round(o[-1])
+            print(f"27B config 4 forced round {r}: accepted {m} emitted {em}", flush=True)
+            assert (m, em) == (mo, emo) and m == n_ok and em == plain[j:j + len(em)], f"forced round {r}"
+            g += em
+            o += emo
+    assert gs.pos == os_.pos
+    se, so = gs.export(), os_.export()
+    print(f"27B config 4: {len(g)} ids, state ({se.size} floats) bit-identical {np.array_equal(se, so)}", flush=True)
+    assert np.array_equal(se, so)
 
 
 def test_27b_prompt_chunks_equal_token_by_token_feed(big):
