@@ -10,7 +10,9 @@ in the Q4_K_M mix, generated on the device, against the CPU oracle holding the s
   state at the same position bit for bit, and the oracle's (tests/spec_identity.rs:136-170 at the full shape);
 * config 4 as the bench runs it (a 64-token prompt, then 12 --spec 3 rounds and 4 forced rounds accepting 3, 1, 2, 0):
   drafts, accepted counts and emitted ids equal the oracle's round by round, and the whole state after the last
-  round is bit-identical.
+  round is bit-identical;
+* sampled --spec 3 (top-k 40 / top-p 0.95, and temperature 1.2 over the whole vocabulary): accepted counts, emitted
+  ids, drafts and the generator state equal the oracle's round by round, the final state bit-identical.
 
 The oracle is the checker only (a C restatement of the reference's CPU path, oracle/); with its scalar dots it runs
 at ~4 s per 27B token on the host cores, so those samples stay short; the config-4 sample runs its AVX2 dots.
@@ -178,6 +180,33 @@ def test_27b_config4_prompt_spec3_rounds_match_oracle(big):
     se, so = gs.export(), os_.export()
     print(f"27B config 4: {len(g)} ids, state ({se.size} floats) bit-identical {np.array_equal(se, so)}", flush=True)
     assert np.array_equal(se, so)
+
+
+@pytest.mark.parametrize("kw", [dict(temperature=1.0, top_k=40, top_p=0.95), dict(temperature=1.2)])
+def test_27b_sampled_spec3_rounds_match_oracle(big, kw):
+    """Sampled --spec 3 at the full shape (sample.rs:279 accept_or_resample via spec.rs:367-380, the sampler over
+    the 248,320-entry vocabulary: top-k by sorted chunks, or with no top-k the whole row sorted): a 16-token prompt,
+    then 8 rounds; round by round the accepted count, the emitted ids, the next drafts and the generator state equal
+    the oracle's (with its AVX2 dots), and the state after the last round is bit-identical."""
+    print(f"case 27B sampled --spec 3 {kw}", flush=True)
+    vocab = big["cfg"].vocab
+    prompt = np.random.default_rng(SEED + 5).integers(0, vocab, 16).astype(np.uint32)
+    ds = aq.Sampler(big["ctx"], aq.sampler_config(**kw, seed=11), vocab)
+    os_ = O.Sampler(O.sampler_config(**kw, seed=11), vocab)
+    g, o = aq.State(big["gm"], 3, 96), O.State(big["om"], 3, 96)
+    with O.simd(True):
+        xg, xo = g.spec_prefill(prompt, sampler=ds), o.spec_prefill(prompt, sampler=os_)
+        assert xg == xo and g.drafts() == o.drafts()
+        for r in range(8):
+            mg, eg = g.spec_round(xg, sampler=ds)
+            mo, eo = o.spec_round(xo, sampler=os_)
+            print(f"27B sampled round {r}: accepted {mg} emitted {eg}", flush=True)
+            assert (mg, eg) == (mo, eo), f"round {r}: {(mg, eg)} vs {(mo, eo)}"
+            assert g.drafts() == o.drafts(), f"round {r}: drafts"
+            assert np.array_equal(ds.rng(), os_.rng()), f"round {r}: generator state"
+            xg, xo = eg[-1], eo[-1]
+    assert np.array_equal(g.export(), o.export())
+    ds.free()
 
 
 def test_27b_prompt_chunks_equal_token_by_token_feed(big):
