@@ -12,7 +12,8 @@ in the Q4_K_M mix, generated on the device, against the CPU oracle holding the s
   drafts, accepted counts and emitted ids equal the oracle's round by round, and the whole state after the last
   round is bit-identical;
 * sampled --spec 3 (top-k 40 / top-p 0.95, and temperature 1.2 over the whole vocabulary): accepted counts, emitted
-  ids, drafts and the generator state equal the oracle's round by round, the final state bit-identical.
+  ids, drafts and the generator state equal the oracle's round by round, the final state bit-identical;
+* --q8-fine: the prefill's logits and state bit-identical, then 3 --spec 3 rounds equal to the oracle's.
 
 The oracle is the checker only (a C restatement of the reference's CPU path, oracle/); with its scalar dots it runs
 at ~4 s per 27B token on the host cores, so those samples stay short; the config-4 sample runs its AVX2 dots.
@@ -207,6 +208,33 @@ def test_27b_sampled_spec3_rounds_match_oracle(big, kw):
             xg, xo = eg[-1], eo[-1]
     assert np.array_equal(g.export(), o.export())
     ds.free()
+
+
+def test_27b_q8_fine_prefill_and_spec_rounds_match_oracle(big):
+    """--q8-fine at the full shape (matvec.rs:129-160: K-quant weights against Q8_0-grain activations, dot.rs:69-160):
+    the 4-token prompt's logits and every state tensor bit-identical to the oracle's, then a spec prefill and 3
+    greedy --spec 3 rounds with the same drafts, accepted counts and emitted ids. The oracle runs its scalar
+    q8-fine dots."""
+    print("case 27B q8-fine prefill and --spec 3 rounds", flush=True)
+    with aq.q8_fine(), O.q8_fine():
+        gs, os_ = aq.State(big["gm"], 0, 32), O.State(big["om"], 0, 32)
+        tg, lg = gs.prefill(big["prompt"], want_logits=True)
+        to, lo = os_.prefill(big["prompt"], want_logits=True)
+        print(f"27B q8-fine prefill: argmax {tg} / {to}, logits bit-identical {np.array_equal(lg, lo)}", flush=True)
+        assert tg == to and np.array_equal(lg, lo)
+        assert np.array_equal(gs.export(), os_.export())
+        gs, os_ = aq.State(big["gm"], 3, 48), O.State(big["om"], 3, 48)
+        g, o = [gs.spec_prefill(big["prompt"])], [os_.spec_prefill(big["prompt"])]
+        assert g == o
+        for r in range(3):
+            gd, od = gs.drafts(), os_.drafts()
+            m, em = gs.spec_round(g[-1])
+            mo, emo = os_.spec_round(o[-1])
+            print(f"27B q8-fine round {r}: drafts {gd} accepted {m} emitted {em}", flush=True)
+            assert gd == od and (m, em) == (mo, emo), f"round {r}"
+            g += em
+            o += emo
+        assert np.array_equal(gs.export(), os_.export())
 
 
 def test_27b_prompt_chunks_equal_token_by_token_feed(big):
