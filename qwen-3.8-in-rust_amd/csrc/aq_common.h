@@ -153,6 +153,10 @@ int launch_gemm(const Weight &w, const Act &x, size_t ncols, float *y, const flo
 // Any column count: launch_matmul up to 8 columns, launch_gemm past that where it applies, else 8-column pieces.
 int launch_matmul_many(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
 int launch_repack(Weight &w, const uint8_t *ggml_dev, bool to_planes, hipStream_t stream);
+// n matrices that read the same activations, all Q8_0 or all Q4_0 of one K (y_i = W_i x, no residual): one launch
+// of the wave kernel for up to Q8_MAXSEG of them when its activation staging fits, else one launch each. ncols 1..8.
+constexpr int Q8_MAXSEG = 3;
+int launch_q8_group(const Weight *const *ws, float *const *ys, int n, const Act &x, size_t ncols, hipStream_t stream);
 
 } // namespace aq
 

@@ -26,6 +26,14 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
 // left-to-right f32 partial for F32), then ONE f32 accumulator over the blocks left to right. The block
 // products are independent, so a work-group computes them in parallel into LDS, then one lane per
 // (row, column) adds them in block order: the reference's chain, bit for bit.
+// One matrix of a grouped wave-kernel launch (matrices sharing the activations, the type and K): its planes, its
+// output, its rows, and the first work-group of the launch that computes it.
+struct Q8Seg {
+    const uint8_t *qa, *dm;
+    float *y;
+    int rows, wg0;
+};
+
 struct Q8Args {
     int type;
     const uint8_t *qa, *dm; // codes plane, f16 scales (F32: qa = rows)
@@ -38,6 +46,8 @@ struct Q8Args {
     float *y;
     const float *resid;
     int ncols; // columns of the launch (the F32 kernel: groups of NC along grid y)
+    int nseg;  // wave kernel: > 1 when the launch computes the matrices seg[0 .. nseg) (qa, dm, y, rows unused)
+    Q8Seg seg[Q8_MAXSEG];
 };
 
 template <int NC, int RPB>
@@ -153,19 +163,43 @@ __global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int r = lane / KS, ks = lane % KS;
     const int nwv = (int)(blockDim.x >> 6); // waves per work-group
-    const int row0 = ((int)blockIdx.x * nwv + wid) * RPW;
+    // this work-group's matrix (a grouped launch: the segment its index falls in; uniform) and its index within it
+    int wg = (int)blockIdx.x;
+    const uint8_t *wqa = a.qa, *wdm = a.dm;
+    float *wy = a.y;
+    const float *wres = a.resid;
+    int rows = a.rows;
+    if (a.nseg > 1) { // fixed indices only, so the segment table stays in the argument segment (no private copy)
+        int base = 0;
+        wqa = a.seg[0].qa;
+        wdm = a.seg[0].dm;
+        wy = a.seg[0].y;
+        rows = a.seg[0].rows;
+#pragma unroll
+        for (int i = 1; i < Q8_MAXSEG; i++)
+            if (i < a.nseg && wg >= a.seg[i].wg0) { // the wg0 increase: the last one reached is this one's
+                base = a.seg[i].wg0;
+                wqa = a.seg[i].qa;
+                wdm = a.seg[i].dm;
+                wy = a.seg[i].y;
+                rows = a.seg[i].rows;
+            }
+        wg -= base;
+        wres = nullptr;
+    }
+    const int row0 = (wg * nwv + wid) * RPW;
     int row = row0 + r;
-    if (row >= a.rows) row = a.rows - 1;
+    if (row >= rows) row = rows - 1;
     const size_t rowb = (size_t)row * nb;
     auto load = [&](Q8Regs<TYPE> &w, int blk) {
         const size_t wb = rowb + (blk < nb ? blk : nb - 1);
         if constexpr (Q4) {
-            w.c0 = *reinterpret_cast<const uint4 *>(a.qa + wb * 16);
+            w.c0 = *reinterpret_cast<const uint4 *>(wqa + wb * 16);
         } else {
-            w.c0 = *reinterpret_cast<const uint4 *>(a.qa + wb * 32);
-            w.c1 = *reinterpret_cast<const uint4 *>(a.qa + wb * 32 + 16);
+            w.c0 = *reinterpret_cast<const uint4 *>(wqa + wb * 32);
+            w.c1 = *reinterpret_cast<const uint4 *>(wqa + wb * 32 + 16);
         }
-        w.d = *reinterpret_cast<const uint16_t *>(a.dm + wb * 2);
+        w.d = *reinterpret_cast<const uint16_t *>(wdm + wb * 2);
     };
     Q8Regs<TYPE> wr[Q8W_PF];
     const int NT = (int)blockDim.x;
@@ -211,7 +245,7 @@ __global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
         }
     }
     __syncthreads();
-    if (row0 >= a.rows) return; // no barrier follows
+    if (row0 >= rows) return; // no barrier follows
     // one float of padding per (column, row) record: the chain owners' reads fall in different banks
     constexpr int KP = KS + 1;
     float *xw = xch + (size_t)wid * NC * RPW * KP;
@@ -277,9 +311,9 @@ __global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
 #pragma unroll
     for (int p = 0; p < Q8W_PF; p++)
         if (nfull + p < nr) round_body(wr[p], nfull + p, false);
-    if (lane < RPW * NC && row0 + orr < a.rows) {
-        const size_t o = (size_t)oc * a.rows + row0 + orr;
-        a.y[o] = a.resid ? a.resid[o] + acc : acc;
+    if (lane < RPW * NC && row0 + orr < rows) {
+        const size_t o = (size_t)oc * rows + row0 + orr;
+        wy[o] = wres ? wres[o] + acc : acc;
     }
 }
 
@@ -449,10 +483,16 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
         // the wave kernel: activations staged in LDS
         // per wave: NC x RPW records of 64 / RPW + 1 floats (at most NC * 68)
         const size_t stage = (size_t)args.nb32 * (q8w_xs(NC) + NC * 8), xw = (size_t)NC * 68 * 4;
+        if (args.nseg > 1 && stage + 4 * xw > 64 * 1024) return fail(AQ_EUNSUP, "q8 group: staging does not fit");
         if (stage + 4 * xw <= 64 * 1024) {
             // rows per wave: the most that still give the grid about four waves per SIMD (one column: two rows
             // from 4096, measured faster for the MTP's Q4_0 matrices)
-            const int rpw = args.rows >= 16384 ? 4 : (args.rows >= 8192 || (NC == 1 && args.rows >= 4096) ? 2 : 1);
+            long all_rows = args.rows;
+            if (args.nseg > 1) {
+                all_rows = 0;
+                for (int i = 0; i < args.nseg; i++) all_rows += args.seg[i].rows;
+            }
+            const int rpw = all_rows >= 16384 ? 4 : (all_rows >= 8192 || (NC == 1 && all_rows >= 4096) ? 2 : 1);
             const bool q4 = args.type == AQ_TYPE_Q4_0;
             const void *k4[2] = {(const void *)&q8_wave_kernel<AQ_TYPE_Q8_0, NC, 4>,
                                  (const void *)&q8_wave_kernel<AQ_TYPE_Q4_0, NC, 4>};
@@ -468,7 +508,7 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
             const long cus = q8_cus();
             for (int w : {16, 8, 4}) {
                 const size_t lds = stage + w * xw;
-                const long grid = (args.rows + (long)w * rpw - 1) / ((long)w * rpw);
+                const long grid = (all_rows + (long)w * rpw - 1) / ((long)w * rpw);
                 if (lds > 64 * 1024 || grid > q8_capacity(fn, 64 * w, lds)) continue;
                 const long busiest = (grid + cus - 1) / cus * w;
                 if (best < 0 || busiest < best) {
@@ -478,12 +518,21 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
             }
             const size_t lds = stage + nwv * xw;
             const int rpg = nwv * rpw; // rows per work-group
-            const dim3 grid((unsigned)((args.rows + rpg - 1) / rpg)), block(64 * nwv);
+            long nwg = (args.rows + rpg - 1) / rpg;
+            Q8Args ga = args;
+            if (args.nseg > 1) { // each matrix its own whole work-groups, in order
+                nwg = 0;
+                for (int i = 0; i < args.nseg; i++) {
+                    ga.seg[i].wg0 = (int)nwg;
+                    nwg += (args.seg[i].rows + rpg - 1) / rpg;
+                }
+            }
+            const dim3 grid((unsigned)nwg), block(64 * nwv);
 #define AQ_Q8W(R)                                                                                             \
     if (q4)                                                                                                   \
-        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q4_0, NC, R>), grid, block, lds, stream, args);              \
+        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q4_0, NC, R>), grid, block, lds, stream, ga);                \
     else                                                                                                      \
-        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q8_0, NC, R>), grid, block, lds, stream, args);
+        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q8_0, NC, R>), grid, block, lds, stream, ga);
             if (rpw == 4) {
                 AQ_Q8W(4)
             } else if (rpw == 2) {
@@ -569,6 +618,47 @@ int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const f
     case 7: return launch_q8_nc<7>(args, stream);
     case 8: return launch_q8_nc<8>(args, stream);
     default: return fail(AQ_EINVAL, "matmul: ncols must be 1..8 for Q8_0/Q4_0/F32 weights in this build");
+    }
+}
+
+int launch_q8_group(const Weight *const *ws, float *const *ys, int n, const Act &x, size_t ncols, hipStream_t stream) {
+    const int t = ws[0]->type;
+    bool one = n >= 2 && n <= Q8_MAXSEG && ncols >= 1 && ncols <= 8 && (t == AQ_TYPE_Q8_0 || t == AQ_TYPE_Q4_0);
+    for (int i = 1; i < n && one; i++) one = ws[i]->type == t && ws[i]->nb == ws[0]->nb && ws[i]->cols == ws[0]->cols;
+    // the wave kernel's staging for ncols columns (the condition launch_q8_nc applies)
+    const size_t stage = ws[0]->nb * ((size_t)q8w_xs((int)ncols) + ncols * 8), xw = ncols * 68 * 4;
+    if (!one || stage + 4 * xw > 64 * 1024) {
+        for (int i = 0; i < n; i++) {
+            const int rc = launch_matmul(*ws[i], x, ncols, ys[i], nullptr, stream);
+            if (rc) return rc;
+        }
+        return 0;
+    }
+    Q8Args args{};
+    args.type = t;
+    args.qa = ws[0]->qa;
+    args.dm = ws[0]->dm;
+    args.rows = (int)ws[0]->rows;
+    args.nb32 = (int)ws[0]->nb;
+    args.xq = x.q0;
+    args.xd = x.d0;
+    args.xs = x.s0;
+    args.xf = x.f32;
+    args.n = x.n;
+    args.y = ys[0];
+    args.resid = nullptr;
+    args.ncols = (int)ncols;
+    args.nseg = n;
+    for (int i = 0; i < n; i++) args.seg[i] = Q8Seg{ws[i]->qa, ws[i]->dm, ys[i], (int)ws[i]->rows, 0};
+    switch (ncols) {
+    case 1: return launch_q8_nc<1>(args, stream);
+    case 2: return launch_q8_nc<2>(args, stream);
+    case 3: return launch_q8_nc<3>(args, stream);
+    case 4: return launch_q8_nc<4>(args, stream);
+    case 5: return launch_q8_nc<5>(args, stream);
+    case 6: return launch_q8_nc<6>(args, stream);
+    case 7: return launch_q8_nc<7>(args, stream);
+    default: return launch_q8_nc<8>(args, stream);
     }
 }
 

@@ -566,6 +566,8 @@ int mm_multi(aq_state *s, int n, const Weight *const *ws, float *const *ys, cons
     }
     grouped = grouped && nf <= 2;
     if (grouped) return launch_kq_group(ws, ys, nullptr, n, x, t, s->stream);
+    if (n >= 2 && n <= Q8_MAXSEG && (ws[0]->type == AQ_TYPE_Q8_0 || ws[0]->type == AQ_TYPE_Q4_0))
+        return launch_q8_group(ws, ys, n, x, t, s->stream); // the MTP's Q4_0 q / k / v and gate / up
     for (int i = 0; i < n; i++) {
         const int rc = mm(s, *ws[i], x, t, ys[i]);
         if (rc) return rc;
