@@ -256,7 +256,8 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
 }
 
 // --------------------------------------------------------------------------------------------------- swiglu
-// act.rs:24-30: h = silu(g) * u. Q8_K: one wave per 256-block; Q8_0 / none: one lane per 32-block.
+// act.rs:24-30: h = silu(g) * u. Q8_K: one wave per 256-block; Q8_0 / none: one lane per element, a half wave per
+// 32-block.
 __global__ void __launch_bounds__(256) swiglu_q8k_kernel(const float *g, const float *u, size_t n, size_t total,
                                                          float *h, Act qa, size_t col0) {
     const int lane = threadIdx.x & 63;
@@ -272,20 +273,18 @@ __global__ void __launch_bounds__(256) swiglu_q8k_kernel(const float *g, const f
 
 __global__ void __launch_bounds__(256) swiglu_q80_kernel(const float *g, const float *u, size_t n, size_t total,
                                                          float *h, Act qa, size_t col0, int quant) {
-    const size_t blk = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (blk >= total) return;
-    const size_t nb = n / 32, row = blk / nb, b = blk % nb;
-    const size_t e = row * n + b * 32;
-    float v[32], gv[32], uv[32];
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-        gv[i] = g[e + i];
-        uv[i] = u[e + i];
+    // one lane per element, one Q8_0 block per 32-lane half wave (n % 32 == 0, so a half never spans two blocks and
+    // is past the end as a whole or not at all); the block's d, codes and code sum by the half's reductions
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x, blk = e / 32;
+    const bool live = blk < total;
+    const int lane = (int)(threadIdx.x & 63);
+    float v = 0.0f;
+    if (live) {
+        v = silu_f(g[e]) * u[e];
+        if (h) h[e] = v;
     }
-    for (int i = 0; i < 32; i++) v[i] = silu_f(gv[i]) * uv[i];
-    if (h)
-        for (int i = 0; i < 32; i++) h[e + i] = v[i];
-    if (quant) q8_0_block_store(qa, col0 + row, b, v);
+    const size_t nb = n / 32, row = blk / nb, b = blk % nb;
+    if (quant && live) q8_0_block_half(qa, col0 + row, b, v, lane); // `live` is uniform over each half wave
 }
 
 // ------------------------------------------------------------------------------------------ Gated DeltaNet
@@ -1032,8 +1031,8 @@ int launch_swiglu(const float *g, const float *u, size_t n, size_t t, float *h_f
         AQ_REQUIRE(n % 32 == 0, "swiglu: n % 32 != 0");
         AQ_REQUIRE(q.kind == QK_Q80 || h_f32, "swiglu: no output");
         const size_t total = t * (n / 32);
-        hipLaunchKernelGGL(swiglu_q80_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, g, u, n,
-                           total, h_f32, act, q.col0, q.kind == QK_Q80 ? 1 : 0);
+        hipLaunchKernelGGL(swiglu_q80_kernel, dim3((unsigned)((total * 32 + 255) / 256)), dim3(256), 0, stream, g, u,
+                           n, total, h_f32, act, q.col0, q.kind == QK_Q80 ? 1 : 0);
     }
     return launched("swiglu");
 }
