@@ -249,9 +249,11 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
         }
     }
     if (kind == QK_Q80) {
+        // one lane per element, a half wave per 32-block: the slice is whole 256-blocks, so each pass of the loop
+        // is whole half waves (the last pass may leave whole waves idle)
         __syncthreads();
-        for (int blk = o0 / 8 + tid; blk < o1 / 8; blk += RN_THREADS)
-            q8_0_block_store(qa, col0 + row, eoff / 32 + blk, xs + blk * 32);
+        for (int e = 4 * o0 + tid; e < 4 * o1; e += RN_THREADS)
+            q8_0_block_half(qa, col0 + row, (size_t)(eoff + e) / 32, xs[e], lane);
     }
 }
 

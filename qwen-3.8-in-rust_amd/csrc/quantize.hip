@@ -17,22 +17,13 @@ __global__ void __launch_bounds__(256) q8k_quantize_kernel(const float *__restri
     q8k_block_store(a, col, b, x, lane);
 }
 
-// One lane per 32-block (q8_0_block_store).
 __global__ void __launch_bounds__(256) q8_0_quantize_kernel(const float *__restrict__ src, size_t src_stride, Act a,
                                                             size_t nblocks_total) {
-    const size_t blk = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    // one lane per element, a half wave per 32-block (a half is past the end as a whole or not at all)
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x, blk = e / 32;
     if (blk >= nblocks_total) return;
     const size_t col = blk / a.nb32, b = blk % a.nb32;
-    const float *x = src + col * src_stride + b * 32;
-    float v[32];
-    for (int i = 0; i < 8; i++) {
-        const float4 t = *reinterpret_cast<const float4 *>(x + 4 * i);
-        v[4 * i] = t.x;
-        v[4 * i + 1] = t.y;
-        v[4 * i + 2] = t.z;
-        v[4 * i + 3] = t.w;
-    }
-    q8_0_block_store(a, col, b, v);
+    q8_0_block_half(a, col, b, src[col * src_stride + b * 32 + (e & 31)], (int)(threadIdx.x & 63));
 }
 
 } // namespace
@@ -48,7 +39,7 @@ int launch_q8k_quantize(const Act &a, size_t ncols, const float *src, size_t src
 int launch_q8_0_quantize(const Act &a, size_t ncols, const float *src, size_t src_stride, hipStream_t stream) {
     const size_t total = ncols * a.nb32;
     if (total == 0) return 0;
-    const unsigned grid = (unsigned)((total + 255) / 256);
+    const unsigned grid = (unsigned)((total * 32 + 255) / 256);
     hipLaunchKernelGGL(q8_0_quantize_kernel, dim3(grid), dim3(256), 0, stream, src, src_stride, a, total);
     return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "q8_0_quantize launch");
 }
