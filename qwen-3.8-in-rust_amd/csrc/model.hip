@@ -1043,8 +1043,10 @@ int aq_state_new(aq_model *m, uint32_t spec_k, uint32_t max_pos, aq_state **out)
     AQ_S(dalloc_t(s, T, &s->ids));
     AQ_S(dalloc_t(s, T, &s->amax));
     AQ_S(dalloc_t(s, T, &s->drafts));
-    AQ_S(dalloc_t(s, T, &s->emitted));
-    AQ_S(dalloc_t(s, 8, &s->info));
+    // the round's result: info[0..3) and the emitted ids at info[16..), laid out as in `pinned`, so one
+    // device-to-host copy carries both
+    AQ_S(dalloc_t(s, 16 + T, &s->info));
+    s->emitted = s->info + 16;
     if (spec_k > 0) {
         AQ_S(dalloc_t(s, (size_t)spec_k * c.vocab, &s->q_dense));
         AQ_S(dalloc_t(s, (size_t)spec_k * c.vocab, &s->q_idx));
@@ -1212,8 +1214,7 @@ int aq_spec_round(aq_state *s, uint32_t x_p, uint32_t *emitted, uint32_t *n_emit
         if ((rc = sampler_round(s->sp, s->logits, (int)k, s->drafts, s->q_dense, s->emitted, s->info, s->stream)))
             return rc;
     }
-    AQ_HIP(hipMemcpyAsync(s->pinned, s->info, 3 * 4, hipMemcpyDeviceToHost, s->stream));
-    AQ_HIP(hipMemcpyAsync(s->pinned + 16, s->emitted, t * 4, hipMemcpyDeviceToHost, s->stream));
+    AQ_HIP(hipMemcpyAsync(s->pinned, s->info, (16 + t) * 4, hipMemcpyDeviceToHost, s->stream));
     AQ_HIP(hipEventRecord(s->ev[1], s->stream));
     // commit (replaces spec.rs:396-415's restore + replay): every DeltaNet layer's state advances by the kept rows
     // (info[2], read on the device) from the saved inputs, in one launch that runs while the host reads keep
