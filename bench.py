@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """bench.py — greedy --spec 3 decode of the random-init 27B-shaped Q4_K_M hybrid on one MI355X.
 
-The workload is the reference's headline path: 64 layers (48 Gated-DeltaNet + 16 gated GQA),
+The workload is the reference's headline path (the full 27B shape): 64 layers (48 Gated-DeltaNet + 16 gated GQA),
 hidden 5120, FFN 17408, vocab 248,320, the MTP block, weights ~N(0, 0.02) quantised to the Q4_K_M type mix and
 generated directly in HBM; a 64-token seeded prompt; then speculative rounds with k = 3 drafts. One step = one
 speculative round (verify k+1 rows reading every weight once, accept on the device, commit the DeltaNet state,

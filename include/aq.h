@@ -4,7 +4,7 @@
  *
  * The reference engine (ManeeshJupalle/Qwen-3.8-in-Rust, crate `aqueduct_core`) has no FFI; its drop-in points
  * are Rust functions. Each entry point below names the reference function it replaces (file:line under
- * crates/core/src/). A Rust-side FFI crate binds these symbols one to one (see INTEGRATION.md).
+ * crates/core/src/). A Rust-side FFI crate binds these symbols one to one.
  *
  * Conventions
  *  - Every function returns int: 0 = OK, < 0 = an AQ_E* code. Nothing aborts across the ABI; contract
