@@ -779,9 +779,19 @@ int mtp_set_rows(aq_state *s, const uint32_t *ids_dev, const float *hs, size_t t
     Needs nd;
     nd.add(m->eh_proj);
     int rc = launch_embed(m->embed, ids_dev, t, s->e, h, s->stream);
-    if (!rc) rc = norm_into(s, s->e, h, m->enorm, h, t, s->act_cat, 0, 0, nd);
-    if (!rc) rc = norm_into(s, hs, h, m->hnorm, h, t, s->act_cat, 0, h, nd);
-    return rc;
+    if (rc) return rc;
+    if (nd.q8k && nd.q80) { // two quantised forms: norm_into's path (which refuses them for half rows)
+        rc = norm_into(s, s->e, h, m->enorm, h, t, s->act_cat, 0, 0, nd);
+        if (!rc) rc = norm_into(s, hs, h, m->hnorm, h, t, s->act_cat, 0, h, nd);
+        return rc;
+    }
+    QuantOut q; // both halves in one launch
+    q.act = &s->act_cat;
+    q.col0 = 0;
+    q.elem_off = 0;
+    q.f32 = true;
+    q.kind = nd.q8k ? QK_Q8K : (nd.q80 ? QK_Q80 : QK_NONE);
+    return launch_rmsnorm_pair(s->e, h, m->enorm, hs, h, m->hnorm, h, m->cfg.rms_eps, h, t, q, s->stream);
 }
 
 // mtp.rs:108-127 `rows_in`: eh_proj, the block at positions mtp_kv.len.., shared_head_norm -> s->mtp_hout rows

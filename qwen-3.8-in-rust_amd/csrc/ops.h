@@ -33,6 +33,11 @@ int launch_embed(const Weight &w, const uint32_t *ids, size_t t, float *out, siz
 // y = (x * inv_rms(x)) * w per row (rmsnorm.rs:14-76), t rows of n; y_f32 optional (row stride y_stride).
 int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t, float *y_f32,
                    size_t y_stride, const QuantOut &q, hipStream_t stream);
+// Two RMSNorms of t rows of n into the same quantised rows in one launch: x with w into elements q.elem_off..,
+// x2 with w2 into elements eoff2.. (the MTP's [rmsnorm(embed, enorm) | rmsnorm(h, hnorm)], mtp.rs:95-104).
+int launch_rmsnorm_pair(const float *x, size_t x_stride, const float *w, const float *x2, size_t x2_stride,
+                        const float *w2, size_t eoff2, float eps, size_t n, size_t t, const QuantOut &q,
+                        hipStream_t stream);
 
 // h = silu(g) * u elementwise over t rows of n (act.rs:24-30), into the quantised form (and h_f32 if set).
 int launch_swiglu(const float *g, const float *u, size_t n, size_t t, float *h_f32, const QuantOut &q,

@@ -100,7 +100,15 @@ __host__ __device__ inline int rn_chain_stride(int n) { // floats per chain row 
 template <int PL>
 __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x, size_t x_stride, const float *w,
                                                                  float eps, int n, float *y, size_t y_stride, Act qa,
-                                                                 int kind, size_t col0, size_t eoff, int act_f32) {
+                                                                 int kind, size_t col0, size_t eoff, int act_f32,
+                                                                 const float *x2, size_t x2_stride, const float *w2,
+                                                                 size_t eoff2) {
+    if (blockIdx.z == 1) { // a pair launch: the second input, its norm weights and its place in the output row
+        x = x2;
+        x_stride = x2_stride;
+        w = w2;
+        eoff = eoff2;
+    }
     extern __shared__ float sm[]; // 8 chains of squares, 16 floats, then (Q8_0 output only) the normalised row
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int n4 = n >> 2, n8 = n / 8 * 8, clen = n8 / 8, cs = rn_chain_stride(n);
@@ -963,10 +971,20 @@ int launch_embed(const Weight &w, const uint32_t *ids, size_t t, float *out, siz
     return launched("embed");
 }
 
-int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t, float *y_f32,
-                   size_t y_stride, const QuantOut &q, hipStream_t stream) {
+// x2 set: a pair launch (grid z = 2), the second input normalised with w2 into elements eoff2.. of the same output
+// rows; it needs the vector kernel, and falls back to two launches where that does not apply.
+static int rmsnorm_launch(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t, float *y_f32,
+                          size_t y_stride, const QuantOut &q, hipStream_t stream, const float *x2, size_t x2_stride,
+                          const float *w2, size_t eoff2) {
     AQ_REQUIRE(n > 0 && n <= 16384, "rmsnorm: row length must be 1..16384");
     if (t == 0) return 0;
+    if (x2) {
+        AQ_REQUIRE(q.act && !y_f32, "rmsnorm pair: the output is the quantised rows only");
+        // the second input's place in the output rows, checked as the first's is below
+        AQ_REQUIRE(eoff2 + n <= q.act->n, "rmsnorm pair: quantised output out of range");
+        AQ_REQUIRE(q.kind != QK_Q8K || eoff2 % 256 == 0, "rmsnorm pair: Q8_K needs 256-blocks");
+        AQ_REQUIRE(q.kind != QK_Q80 || eoff2 % 32 == 0, "rmsnorm pair: Q8_0 needs 32-blocks");
+    }
     Act act{};
     if (q.act) {
         act = *q.act;
@@ -979,8 +997,15 @@ int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, s
     const auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
     const bool vec = n % 4 == 0 && n <= 4 * RN_THREADS * RN_ROUNDS && x_stride % 4 == 0 && al16(x) && al16(w) &&
                      (!y_f32 || (y_stride % 4 == 0 && al16(y_f32))) &&
-                     (!q.f32 || (act.n % 4 == 0 && q.elem_off % 4 == 0 && al16(act.f32)));
+                     (!q.f32 || (act.n % 4 == 0 && q.elem_off % 4 == 0 && al16(act.f32))) &&
+                     (!x2 || (x2_stride % 4 == 0 && al16(x2) && al16(w2) && (!q.f32 || eoff2 % 4 == 0)));
     const size_t vshmem = ((size_t)8 * rn_chain_stride((int)n) + 16 + (q.kind == QK_Q80 ? n : 0)) * sizeof(float);
+    if (x2 && !(vec && vshmem <= 65536)) { // the pair as two launches
+        QuantOut q2 = q;
+        q2.elem_off = eoff2;
+        const int rc = rmsnorm_launch(x, x_stride, w, eps, n, t, nullptr, 0, q, stream, nullptr, 0, nullptr, 0);
+        return rc ? rc : rmsnorm_launch(x2, x2_stride, w2, eps, n, t, nullptr, 0, q2, stream, nullptr, 0, nullptr, 0);
+    }
     if (vec && vshmem <= 65536) {
         const size_t shmem = vshmem;
         // slices of whole 256-blocks (about five blocks each) when the row is made of them
@@ -997,12 +1022,19 @@ int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, s
                 if (!pl && c >= need8) pl = -c;
         for (int c : pls)
             if (!pl && c >= need) pl = c;
-        const dim3 grid((unsigned)t, slices);
+        const dim3 grid((unsigned)t, slices, x2 ? 2u : 1u);
+        if (!x2) { // the kernel's second-input arguments, unread with one input
+            x2 = x;
+            x2_stride = x_stride;
+            w2 = w;
+            eoff2 = q.elem_off;
+        }
         switch (pl) {
 #define AQ_RN(P)                                                                                              \
     case P:                                                                                                   \
         hipLaunchKernelGGL((rmsnorm_vec_kernel<P>), grid, dim3(RN_THREADS), shmem, stream, x, x_stride, w, eps, (int)n, \
-                           y_f32, y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0);              \
+                           y_f32, y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0, x2, x2_stride, w2,  \
+                           eoff2);                                                                            \
         break;
             AQ_RN(0) AQ_RN(1) AQ_RN(2) AQ_RN(4) AQ_RN(6) AQ_RN(8) AQ_RN(10) AQ_RN(12) AQ_RN(16)
             AQ_RN(-4) AQ_RN(-8) AQ_RN(-16) AQ_RN(-24) AQ_RN(-32) AQ_RN(-48) AQ_RN(-64) AQ_RN(-80) AQ_RN(-96)
@@ -1014,6 +1046,18 @@ int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, s
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)t), dim3(256), shmem, stream, x, x_stride, w, eps, (int)n, y_f32,
                        y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0);
     return launched("rmsnorm");
+}
+
+int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t, float *y_f32,
+                   size_t y_stride, const QuantOut &q, hipStream_t stream) {
+    return rmsnorm_launch(x, x_stride, w, eps, n, t, y_f32, y_stride, q, stream, nullptr, 0, nullptr, 0);
+}
+
+int launch_rmsnorm_pair(const float *x, size_t x_stride, const float *w, const float *x2, size_t x2_stride,
+                        const float *w2, size_t eoff2, float eps, size_t n, size_t t, const QuantOut &q,
+                        hipStream_t stream) {
+    AQ_REQUIRE(x2 && w2, "rmsnorm pair: no second input");
+    return rmsnorm_launch(x, x_stride, w, eps, n, t, nullptr, 0, q, stream, x2, x2_stride, w2, eoff2);
 }
 
 int launch_swiglu(const float *g, const float *u, size_t n, size_t t, float *h_f32, const QuantOut &q,
