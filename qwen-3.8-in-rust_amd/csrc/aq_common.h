@@ -154,7 +154,8 @@ int launch_gemm(const Weight &w, const Act &x, size_t ncols, float *y, const flo
 int launch_matmul_many(const Weight &w, const Act &x, size_t ncols, float *y, const float *resid, hipStream_t stream);
 int launch_repack(Weight &w, const uint8_t *ggml_dev, bool to_planes, hipStream_t stream);
 // n matrices that read the same activations, all Q8_0 or all Q4_0 of one K (y_i = W_i x, no residual): one launch
-// of the wave kernel for up to Q8_MAXSEG of them when its activation staging fits, else one launch each. ncols 1..8.
+// of the wave kernel for up to Q8_MAXSEG of them when its activation staging fits and ncols <= 4, else one launch
+// each. ncols 1..8.
 constexpr int Q8_MAXSEG = 3;
 int launch_q8_group(const Weight *const *ws, float *const *ys, int n, const Act &x, size_t ncols, hipStream_t stream);
 

@@ -46,8 +46,12 @@ struct Q8Args {
     float *y;
     const float *resid;
     int ncols; // columns of the launch (the F32 kernel: groups of NC along grid y)
-    int nseg;  // wave kernel: > 1 when the launch computes the matrices seg[0 .. nseg) (qa, dm, y, rows unused)
+};
+
+// The matrices of a grouped wave-kernel launch (its own kernel argument, so single launches keep Q8Args alone).
+struct Q8Group {
     Q8Seg seg[Q8_MAXSEG];
+    int nseg;
 };
 
 template <int NC, int RPB>
@@ -150,7 +154,8 @@ struct Q8Regs {
 };
 
 template <int TYPE, int NC, int RPW>
-__global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
+__device__ __forceinline__ void q8_wave_body(const Q8Args &a, int wg, const uint8_t *wqa, const uint8_t *wdm, float *wy,
+                                             const float *wres, const int rows) {
     extern __shared__ __align__(16) uint8_t q8_lds[];
     constexpr bool Q4 = TYPE == AQ_TYPE_Q4_0;
     constexpr int KS = 64 / RPW;
@@ -163,30 +168,6 @@ __global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int r = lane / KS, ks = lane % KS;
     const int nwv = (int)(blockDim.x >> 6); // waves per work-group
-    // this work-group's matrix (a grouped launch: the segment its index falls in; uniform) and its index within it
-    int wg = (int)blockIdx.x;
-    const uint8_t *wqa = a.qa, *wdm = a.dm;
-    float *wy = a.y;
-    const float *wres = a.resid;
-    int rows = a.rows;
-    if (a.nseg > 1) { // fixed indices only, so the segment table stays in the argument segment (no private copy)
-        int base = 0;
-        wqa = a.seg[0].qa;
-        wdm = a.seg[0].dm;
-        wy = a.seg[0].y;
-        rows = a.seg[0].rows;
-#pragma unroll
-        for (int i = 1; i < Q8_MAXSEG; i++)
-            if (i < a.nseg && wg >= a.seg[i].wg0) { // the wg0 increase: the last one reached is this one's
-                base = a.seg[i].wg0;
-                wqa = a.seg[i].qa;
-                wdm = a.seg[i].dm;
-                wy = a.seg[i].y;
-                rows = a.seg[i].rows;
-            }
-        wg -= base;
-        wres = nullptr;
-    }
     const int row0 = (wg * nwv + wid) * RPW;
     int row = row0 + r;
     if (row >= rows) row = rows - 1;
@@ -315,6 +296,31 @@ __global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
         const size_t o = (size_t)oc * rows + row0 + orr;
         wy[o] = wres ? wres[o] + acc : acc;
     }
+}
+
+template <int TYPE, int NC, int RPW>
+__global__ void __launch_bounds__(1024) q8_wave_kernel(Q8Args a) {
+    q8_wave_body<TYPE, NC, RPW>(a, (int)blockIdx.x, a.qa, a.dm, a.y, a.resid, a.rows);
+}
+
+// A grouped launch: the matrix of this work-group is the segment its index falls in (uniform), found with fixed
+// indices only, so the table stays in the argument segment (no private copy); no residual.
+template <int TYPE, int NC, int RPW>
+__global__ void __launch_bounds__(1024) q8_wave_group_kernel(Q8Args a, Q8Group g) {
+    const int wg = (int)blockIdx.x;
+    int base = 0, rows = g.seg[0].rows;
+    const uint8_t *wqa = g.seg[0].qa, *wdm = g.seg[0].dm;
+    float *wy = g.seg[0].y;
+#pragma unroll
+    for (int i = 1; i < Q8_MAXSEG; i++)
+        if (i < g.nseg && wg >= g.seg[i].wg0) { // wg0 increases: the last one reached is this one's
+            base = g.seg[i].wg0;
+            wqa = g.seg[i].qa;
+            wdm = g.seg[i].dm;
+            wy = g.seg[i].y;
+            rows = g.seg[i].rows;
+        }
+    q8_wave_body<TYPE, NC, RPW>(a, wg - base, wqa, wdm, wy, nullptr, rows);
 }
 
 // ---------------------------------------------------------------------------------------------- repack
@@ -470,7 +476,7 @@ inline long q8_cus() {
 }
 
 template <int NC>
-int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
+int launch_q8_nc(const Q8Args &args, hipStream_t stream, const Q8Group *grp = nullptr) {
     if (args.type == AQ_TYPE_F32) {
         const size_t lds = (size_t)args.nb32 * NC * sizeof(float);
         if (lds > 64 * 1024) return fail(AQ_EUNSUP, "f32 matmul: row too long for the LDS chain");
@@ -483,14 +489,14 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
         // the wave kernel: activations staged in LDS
         // per wave: NC x RPW records of 64 / RPW + 1 floats (at most NC * 68)
         const size_t stage = (size_t)args.nb32 * (q8w_xs(NC) + NC * 8), xw = (size_t)NC * 68 * 4;
-        if (args.nseg > 1 && stage + 4 * xw > 64 * 1024) return fail(AQ_EUNSUP, "q8 group: staging does not fit");
+        if (grp && (stage + 4 * xw > 64 * 1024 || NC > 4)) return fail(AQ_EUNSUP, "q8 group: not this launch shape");
         if (stage + 4 * xw <= 64 * 1024) {
             // rows per wave: the most that still give the grid about four waves per SIMD (one column: two rows
             // from 4096, measured faster for the MTP's Q4_0 matrices)
             long all_rows = args.rows;
-            if (args.nseg > 1) {
+            if (grp) {
                 all_rows = 0;
-                for (int i = 0; i < args.nseg; i++) all_rows += args.seg[i].rows;
+                for (int i = 0; i < grp->nseg; i++) all_rows += grp->seg[i].rows;
             }
             const int rpw = all_rows >= 16384 ? 4 : (all_rows >= 8192 || (NC == 1 && all_rows >= 4096) ? 2 : 1);
             const bool q4 = args.type == AQ_TYPE_Q4_0;
@@ -519,20 +525,30 @@ int launch_q8_nc(const Q8Args &args, hipStream_t stream) {
             const size_t lds = stage + nwv * xw;
             const int rpg = nwv * rpw; // rows per work-group
             long nwg = (args.rows + rpg - 1) / rpg;
-            Q8Args ga = args;
-            if (args.nseg > 1) { // each matrix its own whole work-groups, in order
+            Q8Group g{};
+            if (grp) { // each matrix its own whole work-groups, in order
+                g = *grp;
                 nwg = 0;
-                for (int i = 0; i < args.nseg; i++) {
-                    ga.seg[i].wg0 = (int)nwg;
-                    nwg += (args.seg[i].rows + rpg - 1) / rpg;
+                for (int i = 0; i < g.nseg; i++) {
+                    g.seg[i].wg0 = (int)nwg;
+                    nwg += (g.seg[i].rows + rpg - 1) / rpg;
                 }
             }
             const dim3 grid((unsigned)nwg), block(64 * nwv);
 #define AQ_Q8W(R)                                                                                             \
+    if constexpr (NC <= 4) {                                                                                  \
+        if (grp) {                                                                                            \
+            if (q4)                                                                                           \
+                hipLaunchKernelGGL((q8_wave_group_kernel<AQ_TYPE_Q4_0, NC, R>), grid, block, lds, stream, args, g); \
+            else                                                                                              \
+                hipLaunchKernelGGL((q8_wave_group_kernel<AQ_TYPE_Q8_0, NC, R>), grid, block, lds, stream, args, g); \
+            return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "q8_wave group launch");              \
+        }                                                                                                     \
+    }                                                                                                         \
     if (q4)                                                                                                   \
-        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q4_0, NC, R>), grid, block, lds, stream, ga);                \
+        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q4_0, NC, R>), grid, block, lds, stream, args);             \
     else                                                                                                      \
-        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q8_0, NC, R>), grid, block, lds, stream, ga);
+        hipLaunchKernelGGL((q8_wave_kernel<AQ_TYPE_Q8_0, NC, R>), grid, block, lds, stream, args);
             if (rpw == 4) {
                 AQ_Q8W(4)
             } else if (rpw == 2) {
@@ -623,7 +639,7 @@ int launch_matmul(const Weight &w, const Act &x, size_t ncols, float *y, const f
 
 int launch_q8_group(const Weight *const *ws, float *const *ys, int n, const Act &x, size_t ncols, hipStream_t stream) {
     const int t = ws[0]->type;
-    bool one = n >= 2 && n <= Q8_MAXSEG && ncols >= 1 && ncols <= 8 && (t == AQ_TYPE_Q8_0 || t == AQ_TYPE_Q4_0);
+    bool one = n >= 2 && n <= Q8_MAXSEG && ncols >= 1 && ncols <= 4 && (t == AQ_TYPE_Q8_0 || t == AQ_TYPE_Q4_0);
     for (int i = 1; i < n && one; i++) one = ws[i]->type == t && ws[i]->nb == ws[0]->nb && ws[i]->cols == ws[0]->cols;
     // the wave kernel's staging for ncols columns (the condition launch_q8_nc applies)
     const size_t stage = ws[0]->nb * ((size_t)q8w_xs((int)ncols) + ncols * 8), xw = ncols * 68 * 4;
@@ -648,17 +664,14 @@ int launch_q8_group(const Weight *const *ws, float *const *ys, int n, const Act 
     args.y = ys[0];
     args.resid = nullptr;
     args.ncols = (int)ncols;
-    args.nseg = n;
-    for (int i = 0; i < n; i++) args.seg[i] = Q8Seg{ws[i]->qa, ws[i]->dm, ys[i], (int)ws[i]->rows, 0};
+    Q8Group g{};
+    g.nseg = n;
+    for (int i = 0; i < n; i++) g.seg[i] = Q8Seg{ws[i]->qa, ws[i]->dm, ys[i], (int)ws[i]->rows, 0};
     switch (ncols) {
-    case 1: return launch_q8_nc<1>(args, stream);
-    case 2: return launch_q8_nc<2>(args, stream);
-    case 3: return launch_q8_nc<3>(args, stream);
-    case 4: return launch_q8_nc<4>(args, stream);
-    case 5: return launch_q8_nc<5>(args, stream);
-    case 6: return launch_q8_nc<6>(args, stream);
-    case 7: return launch_q8_nc<7>(args, stream);
-    default: return launch_q8_nc<8>(args, stream);
+    case 1: return launch_q8_nc<1>(args, stream, &g);
+    case 2: return launch_q8_nc<2>(args, stream, &g);
+    case 3: return launch_q8_nc<3>(args, stream, &g);
+    default: return launch_q8_nc<4>(args, stream, &g);
     }
 }
 
