@@ -62,6 +62,8 @@ def parse():
     ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel timing (for counter runs)")
     ap.add_argument("--sweep-only", action="store_true", help="only the matmul sweep (for kernel-trace runs)")
     ap.add_argument("--prefill-only", action="store_true", help="only the prompt prefill timing (for kernel-trace runs)")
+    ap.add_argument("--shapes", default="", help="with --sweep-only: comma-separated substrings; only sweep shapes "
+                                                  "whose name (e.g. 'Q4_K 5120x6144') contains one of them")
     return ap.parse_args()
 
 
@@ -95,18 +97,30 @@ def kernel_roofline(ctx, k):
             "bytes_per_launch": traffic_alg, "achieved_GBs": achieved, "read_floor_us": round(floor, 3)}
 
 
-def kernel_sweep(ctx):
+TYPE_NAME = {aq.Q4_K: "Q4_K", aq.Q5_K: "Q5_K", aq.Q6_K: "Q6_K", aq.Q8_0: "Q8_0", aq.Q4_0: "Q4_0"}
+
+# (type, rows, cols, distinct weights, column counts) of the sweep
+SWEEP = [(aq.Q4_K, 17408, 5120, 8, (1, 2, 4, 6, 8)), (aq.Q6_K, 5120, 17408, 8, (1, 2, 4, 6, 8)),
+         (aq.Q4_K, 5120, 17408, 8, (1, 4)), (aq.Q4_K, 5120, 6144, 8, (1, 4)), (aq.Q5_K, 5120, 6144, 8, (1, 4)),
+         (aq.Q6_K, 248320, 5120, 1, (1,)), (aq.Q8_0, 5120, 6144, 8, (1, 4)),
+         (aq.Q4_0, 5120, 10240, 8, (1,)), (aq.Q4_K, 17408, 5120, 4, (64,)),
+         (aq.Q6_K, 5120, 17408, 4, (64,)), (aq.Q8_0, 5120, 6144, 4, (64,))]
+
+
+def kernel_sweep(ctx, shapes=""):
     """The matvec (N = 1) and the blocked verify op (N = k+1 in {2, 4, 6, 8}) on the single-op shapes: Q4_K
-    17408 x 5120 and Q6_K 5120 x 17408 over 8 distinct weights each (beyond the MALL), the Q6_K lm_head
-    248320 x 5120 at N = 1 (the draft chain's matvec), the Q8_0 ssm_out (N = 1, 4) and the MTP's Q4_0 eh_proj
-    (N = 1); then the prompt-chunk product (N = 64, the prefill's matrix-core GEMM) on three of them. HIP-event time
-    per launch on the context stream; GB/s from the algorithmic bytes W + N*x + N*y. Flat GB/s against N means each
-    weight super-block is read once per launch."""
+    17408 x 5120 and Q6_K 5120 x 17408 over 8 distinct weights each (beyond the MALL); the other 5120-row matrices of
+    the round at N = 1 and 4 (the Q4_K ffn_down 5120 x 17408, the Q4_K ssm_out and Q5_K attn_output 5120 x 6144); the
+    Q6_K lm_head 248320 x 5120 at N = 1 (the draft chain's matvec), the Q8_0 ssm_out (N = 1, 4) and the MTP's Q4_0
+    eh_proj (N = 1); then the prompt-chunk product (N = 64, the prefill's matrix-core GEMM) on three of them.
+    HIP-event time per launch on the context stream; GB/s from the algorithmic bytes W + N*x + N*y. Flat GB/s against
+    N means each weight super-block is read once per launch. `shapes`: comma-separated name filters (all if empty)."""
     out = []
-    for t, rows, cols, nw, ns in [(aq.Q4_K, 17408, 5120, 8, (1, 2, 4, 6, 8)), (aq.Q6_K, 5120, 17408, 8, (1, 2, 4, 6, 8)),
-                                  (aq.Q6_K, 248320, 5120, 1, (1,)), (aq.Q8_0, 5120, 6144, 8, (1, 4)),
-                                  (aq.Q4_0, 5120, 10240, 8, (1,)), (aq.Q4_K, 17408, 5120, 4, (64,)),
-                                  (aq.Q6_K, 5120, 17408, 4, (64,)), (aq.Q8_0, 5120, 6144, 4, (64,))]:
+    keys = [k.strip() for k in shapes.split(",") if k.strip()]
+    for t, rows, cols, nw, ns in SWEEP:
+        name = f"{TYPE_NAME[t]} {rows}x{cols}"
+        if keys and not any(k in name for k in keys):
+            continue
         ws = [aq.SynthWeight(ctx, aq.synth_spec(t, rows, cols, seed=SEED + 200 + i)) for i in range(nw)]
         wbytes = rows * aq.row_bytes(t, cols)
         floor = aq.read_floor_time(ctx, wbytes, iters=50 if wbytes > (256 << 20) else 500)  # the weights' bytes, plainly read
@@ -123,8 +137,7 @@ def kernel_sweep(ctx):
             xbytes = (cols // 256) * 292 if t in (aq.Q4_K, aq.Q5_K, aq.Q6_K) else (cols // 32) * 40  # Q8_K / Q8_0 rows
             nbytes = wbytes + n * xbytes + n * rows * 4
             gbs = nbytes / (us * 1e-6) / 1e9
-            name = {aq.Q4_K: "Q4_K", aq.Q6_K: "Q6_K", aq.Q8_0: "Q8_0", aq.Q4_0: "Q4_0"}[t]
-            out.append({"kernel": f"{name} {rows}x{cols}", "n": n, "us_per_launch": round(us, 2),
+            out.append({"kernel": name, "n": n, "us_per_launch": round(us, 2),
                         "median_us": round(med, 2), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                         "read_floor_us": round(floor, 2), "of_read_floor": round(floor / us, 3)})
             y.free()
@@ -307,7 +320,7 @@ def main():
     ctx = aq.Context(0)
     k = a.spec
     # the sweep also brings the clocks up before the roofline timing
-    ks = kernel_sweep(ctx) if not (a.kernel_only or a.prefill_only) else None
+    ks = kernel_sweep(ctx, a.shapes if a.sweep_only else "") if not (a.kernel_only or a.prefill_only) else None
     if a.sweep_only:
         print(json.dumps({"kernel_sweep": ks}), flush=True)
         return

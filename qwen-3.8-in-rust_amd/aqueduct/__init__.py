@@ -16,8 +16,16 @@ F32, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 2, 8, 12, 13, 14
 BLOCK = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 
 
+# status codes of include/aq.h
+AQ_EINVAL, AQ_EHIP, AQ_ENOMEM, AQ_EUNSUP, AQ_ESTATE = -1, -2, -3, -4, -5
+
+
 class AqError(RuntimeError):
-    pass
+    """A failed libaq call; `code` is its AQ_E* status."""
+
+    def __init__(self, msg, code=None):
+        super().__init__(msg)
+        self.code = code
 
 
 def row_bytes(t, cols):
@@ -164,7 +172,7 @@ def lib():
 
 def check(rc):
     if rc != 0:
-        raise AqError(f"libaq error {rc}: {lib().aq_last_error().decode()}")
+        raise AqError(f"libaq error {rc}: {lib().aq_last_error().decode()}", rc)
 
 
 def ptr(a):

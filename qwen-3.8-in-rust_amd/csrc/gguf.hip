@@ -51,7 +51,19 @@ struct TensorInfo {
 uint64_t type_bytes(uint32_t type, uint64_t n) {
     const int be = aq::block_elems((int)type), bb = aq::block_bytes((int)type);
     if (be <= 0 || bb <= 0 || n % (uint64_t)be) return 0;
-    return n / (uint64_t)be * (uint64_t)bb;
+    uint64_t bytes;
+    if (__builtin_mul_overflow(n / (uint64_t)be, (uint64_t)bb, &bytes)) return 0;
+    return bytes;
+}
+
+// The fewest bytes one array element of GGUF type `t` occupies in the file (a string: its 8-byte length).
+uint64_t elem_min_bytes(uint32_t t) {
+    switch (t) {
+    case GT_U8: case GT_I8: case GT_BOOL: return 1;
+    case GT_U16: case GT_I16: return 2;
+    case GT_U32: case GT_I32: case GT_F32: return 4;
+    default: return 8; // GT_U64, GT_I64, GT_F64, GT_STR
+    }
 }
 
 struct Reader {
@@ -96,7 +108,10 @@ struct Reader {
         case GT_ARR: {
             v.arr_type = get<uint32_t>();
             const uint64_t cnt = get<uint64_t>();
-            if (depth > 0 || v.arr_type == GT_ARR || v.arr_type > GT_F64 || cnt > n) { // one level, sane counts
+            // one level, and no more elements than the bytes left can hold (nothing is reserved for a count that
+            // a crafted file inflates)
+            if (!ok || depth > 0 || v.arr_type == GT_ARR || v.arr_type > GT_F64 ||
+                cnt > (n - at) / elem_min_bytes(v.arr_type)) {
                 ok = false;
                 break;
             }
@@ -291,9 +306,14 @@ int aq_gguf_open(const char *path, aq_gguf **out) {
             break;
         }
         uint64_t count = 1;
+        bool wrapped = false;
         for (uint32_t d = 0; d < nd; d++) {
             t.dims.push_back(r.get<uint64_t>());
-            count *= t.dims.back();
+            wrapped = __builtin_mul_overflow(count, t.dims.back(), &count) || wrapped;
+        }
+        if (wrapped) {
+            rc = fail(AQ_EINVAL, "aq_gguf_open: tensor info #" + std::to_string(i) + ": element count overflows");
+            break;
         }
         t.type = r.get<uint32_t>();
         t.rel_offset = r.get<uint64_t>();
@@ -325,7 +345,9 @@ int aq_gguf_open(const char *path, aq_gguf **out) {
     if (!rc) {
         g->data_offset = (g->header_end + g->alignment - 1) / g->alignment * g->alignment;
         for (const TensorInfo &t : g->tensors) {
-            if (t.rel_offset % g->alignment || g->data_offset + t.rel_offset + t.nbytes > g->file_size) {
+            // each comparison without a sum that could wrap: offset, then size, against the bytes left
+            const uint64_t room = g->data_offset <= g->file_size ? g->file_size - g->data_offset : 0;
+            if (t.rel_offset % g->alignment || t.rel_offset > room || t.nbytes > room - t.rel_offset) {
                 rc = fail(AQ_EINVAL, "aq_gguf_open: tensor " + t.name + " misaligned or past the end of the file");
                 break;
             }

@@ -1144,6 +1144,7 @@ int aq_state_free(aq_state *s) {
 int aq_prefill(aq_state *s, const uint32_t *ids, size_t n, float *logits_last_host, uint32_t *argmax_out) {
     AQ_REQUIRE(s && ids, "aq_prefill: null argument");
     AQ_HIP(hipSetDevice(s->m->ctx->device));
+    s->spec_ready = false; // the MTP is not fed: a round needs aq_spec_prefill again (spec.rs:337)
     int rc = run_prompt(s, ids, n);
     if (rc) return rc;
     if (logits_last_host) {
@@ -1159,6 +1160,7 @@ int aq_forward_token(aq_state *s, uint32_t id, float *logits_host, uint32_t *arg
     AQ_REQUIRE(s->pos + 1 + MAX_ROWS <= s->max_pos, "aq_forward_token: position past max_pos");
     AQ_HIP(hipSetDevice(s->m->ctx->device));
     const size_t vocab = s->m->cfg.vocab;
+    s->spec_ready = false; // as in aq_prefill
     s->pinned[8] = id;
     int rc = copy_ids_in(s, s->ids, s->pinned + 8, 1);
     if (!rc) rc = forward_rows(s, s->ids, 1, PLAIN);
@@ -1178,10 +1180,17 @@ int aq_spec_prefill(aq_state *s, const uint32_t *ids, size_t n, uint32_t *x_t) {
     aq_model *m = s->m;
     const size_t h = m->cfg.hidden;
     const uint32_t p = s->pos;
+    // spec.rs:246: the MTP holds a row for every consumed position (plus the last round's draft rows); a state
+    // whose plain calls ran past them cannot be fed at the right positions
+    if (s->mtp_kv.len < p)
+        return fail(AQ_ESTATE, "aq_spec_prefill: the MTP has " + std::to_string(s->mtp_kv.len) + " rows for " +
+                                   std::to_string(p) + " consumed positions");
+    s->spec_ready = false;
     int rc = run_prompt(s, ids, n);
     if (rc) return rc;
-    // the MTP over the prompt: row j = (x_{j+1}, h_j), the last row's token is x_T (spec.rs:243-265)
-    if (s->mtp_kv.len > p) s->mtp_kv.len = p;
+    // the MTP over the prompt: row j = (x_{j+1}, h_j), the last row's token is x_T (spec.rs:243-265); the draft
+    // rows of a used state's last round are forgotten
+    s->mtp_kv.len = p;
     if (n > 1) AQ_HIP(hipMemcpyAsync(s->shifted, s->prompt + 1, (n - 1) * 4, hipMemcpyDeviceToDevice, s->stream));
     AQ_HIP(hipMemcpyAsync(s->shifted + (n - 1), s->amax, 4, hipMemcpyDeviceToDevice, s->stream));
     size_t last = 0;
@@ -1207,6 +1216,10 @@ int aq_spec_round(aq_state *s, uint32_t x_p, uint32_t *emitted, uint32_t *n_emit
     aq_model *m = s->m;
     AQ_REQUIRE(x_p < m->cfg.vocab, "aq_spec_round: x_p out of range");
     const size_t k = s->k, t = k + 1, h = m->cfg.hidden, vocab = m->cfg.vocab;
+    // spec.rs:337: the MTP holds the consumed positions plus the k - 1 chained draft rows
+    if (s->mtp_kv.len != s->pos + k - 1)
+        return fail(AQ_ESTATE, "aq_spec_round: the MTP has " + std::to_string(s->mtp_kv.len) + " rows at position " +
+                                   std::to_string(s->pos) + " (k " + std::to_string(k) + ")");
     AQ_REQUIRE(s->pos + t + MAX_ROWS <= s->max_pos, "aq_spec_round: position past max_pos");
     AQ_HIP(hipSetDevice(m->ctx->device));
     int rc = collect_stage_times(s);

@@ -355,6 +355,10 @@ struct aq_sampler {
     void *sort_tmp = nullptr;
     size_t sort_tmp_bytes = 0, chunk_stride = 0;
     uint32_t *pinned = nullptr;
+    // recorded after every launch that touches the sampler's device buffers (generator state, kept set, candidate
+    // lists), on whichever stream made it; every later use waits for it first, so a sampled model call still
+    // queued on a state's stream and an operator call on the context stream never overlap
+    hipEvent_t last = nullptr;
 };
 
 namespace aq {
@@ -426,6 +430,18 @@ int sync_res(aq_sampler *sp, hipStream_t st) {
     return 0;
 }
 
+// Stream st takes over the sampler: it waits for the last launch that used it (on any stream).
+int join(aq_sampler *sp, hipStream_t st) {
+    AQ_HIP(hipStreamWaitEvent(st, sp->last, 0));
+    return 0;
+}
+// st's launches so far are now the sampler's last use.
+int mark(aq_sampler *sp, hipStream_t st, int rc) {
+    if (rc) return rc;
+    AQ_HIP(hipEventRecord(sp->last, st));
+    return 0;
+}
+
 } // namespace
 
 // ------------------------------------------------------------------- launchers for the model's sampled calls
@@ -436,21 +452,23 @@ int sampler_device(const aq_sampler *sp) { return sp->device; }
 int sampler_sample(aq_sampler *sp, const float *logits, uint32_t *tok_dev, hipStream_t st) {
     const uint64_t *keys;
     size_t stride;
-    int rc = candidates(sp, logits, 1, st, &keys, &stride);
+    int rc = join(sp, st);
+    if (!rc) rc = candidates(sp, logits, 1, st, &keys, &stride);
     if (rc) return rc;
     SampArgs a = base_args(sp, OP_SAMPLE);
     a.logits = logits;
     a.keys = keys;
     a.key_stride = stride;
     a.tok_out = tok_dev;
-    return run(a, st);
+    return mark(sp, st, run(a, st));
 }
 
 int sampler_draft(aq_sampler *sp, const float *logits, uint32_t *tok_dev, float *q_dense, uint32_t *q_idx,
                   uint32_t *q_n, hipStream_t st) {
     const uint64_t *keys;
     size_t stride;
-    int rc = candidates(sp, logits, 1, st, &keys, &stride);
+    int rc = join(sp, st);
+    if (!rc) rc = candidates(sp, logits, 1, st, &keys, &stride);
     if (rc) return rc;
     SampArgs a = base_args(sp, OP_DRAFT);
     a.logits = logits;
@@ -460,14 +478,15 @@ int sampler_draft(aq_sampler *sp, const float *logits, uint32_t *tok_dev, float 
     a.q_out = q_dense;
     a.q_idx = q_idx;
     a.q_n = q_n;
-    return run(a, st);
+    return mark(sp, st, run(a, st));
 }
 
 int sampler_round(aq_sampler *sp, const float *logits, int k, const uint32_t *drafts, const float *q_dense,
                   uint32_t *emitted, uint32_t *info, hipStream_t st) {
     const uint64_t *keys;
     size_t stride;
-    int rc = candidates(sp, logits, k + 1, st, &keys, &stride);
+    int rc = join(sp, st);
+    if (!rc) rc = candidates(sp, logits, k + 1, st, &keys, &stride);
     if (rc) return rc;
     SampArgs a = base_args(sp, OP_ROUND);
     a.logits = logits;
@@ -478,7 +497,7 @@ int sampler_round(aq_sampler *sp, const float *logits, int k, const uint32_t *dr
     a.emitted = emitted;
     a.info = info;
     a.k = k;
-    return run(a, st);
+    return mark(sp, st, run(a, st));
 }
 
 } // namespace aq
@@ -532,6 +551,11 @@ int aq_sampler_new(aq_ctx *ctx, const aq_sampler_config *cfg, uint32_t vocab, aq
         delete sp;
         return fail(AQ_ENOMEM, "aq_sampler_new: pinned buffer");
     }
+    if (hipEventCreateWithFlags(&sp->last, hipEventDisableTiming) != hipSuccess) {
+        sp->last = nullptr;
+        aq_sampler_free(sp);
+        return fail(AQ_EHIP, "aq_sampler_new: event");
+    }
     int rc = aq_sampler_reseed(sp, cfg->seed);
     if (!rc && hipMemsetAsync(sp->res, 0, 64, ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_sampler_new: clear");
     if (!rc && hipStreamSynchronize(ctx->stream) != hipSuccess) rc = fail(AQ_EHIP, "aq_sampler_new: sync");
@@ -546,6 +570,10 @@ int aq_sampler_new(aq_ctx *ctx, const aq_sampler_config *cfg, uint32_t vocab, aq
 int aq_sampler_free(aq_sampler *sp) {
     if (!sp) return 0;
     (void)hipSetDevice(sp->device);
+    if (sp->last) { // the last use may still be queued on a state's stream
+        (void)hipEventSynchronize(sp->last);
+        (void)hipEventDestroy(sp->last);
+    }
     if (sp->base) (void)hipFree(sp->base);
     if (sp->pinned) (void)hipHostFree(sp->pinned);
     delete sp;
@@ -564,6 +592,10 @@ int aq_sampler_reseed(aq_sampler *sp, uint64_t seed) {
         s[i] = z ^ (z >> 31);
     }
     sp->cfg.seed = seed;
+    if (sp->last) {
+        int rc = join(sp, sp->ctx->stream);
+        if (rc) return rc;
+    }
     AQ_HIP(hipMemcpyAsync(sp->rng, s, 32, hipMemcpyHostToDevice, sp->ctx->stream));
     AQ_HIP(hipStreamSynchronize(sp->ctx->stream));
     return 0;
@@ -572,6 +604,7 @@ int aq_sampler_reseed(aq_sampler *sp, uint64_t seed) {
 int aq_sampler_get_rng(aq_sampler *sp, uint64_t *out4) {
     AQ_REQUIRE(sp && out4, "aq_sampler_get_rng: null argument");
     AQ_HIP(hipSetDevice(sp->device));
+    AQ_HIP(hipEventSynchronize(sp->last)); // a sampled round's draft chain may still be drawing
     AQ_HIP(hipMemcpy(out4, sp->rng, 32, hipMemcpyDeviceToHost));
     return 0;
 }
@@ -580,7 +613,8 @@ int aq_sampler_process(aq_sampler *sp, const float *logits_dev, uint32_t *n_kept
     AQ_REQUIRE(sp && logits_dev, "aq_sampler_process: null argument");
     AQ_HIP(hipSetDevice(sp->device));
     hipStream_t st = sp->ctx->stream;
-    int rc;
+    int rc = join(sp, st);
+    if (rc) return rc;
     if (sampler_greedy(sp)) {
         rc = launch_argmax(logits_dev, sp->vocab, sp->vocab, 1, sp->res + 1, sp->amax_scratch, st);
         if (!rc) rc = run(base_args(sp, OP_GREEDY_SET), st);
@@ -596,6 +630,7 @@ int aq_sampler_process(aq_sampler *sp, const float *logits_dev, uint32_t *n_kept
             rc = run(a, st);
         }
     }
+    rc = mark(sp, st, rc);
     if (!rc) rc = sync_res(sp, st);
     if (!rc && n_kept) *n_kept = sp->pinned[0];
     return rc;
@@ -604,7 +639,8 @@ int aq_sampler_process(aq_sampler *sp, const float *logits_dev, uint32_t *n_kept
 int aq_sampler_kept(aq_sampler *sp, uint32_t *ids, float *probs, size_t cap, size_t *n) {
     AQ_REQUIRE(sp && n, "aq_sampler_kept: null argument");
     AQ_HIP(hipSetDevice(sp->device));
-    int rc = sync_res(sp, sp->ctx->stream);
+    int rc = join(sp, sp->ctx->stream);
+    if (!rc) rc = sync_res(sp, sp->ctx->stream);
     if (rc) return rc;
     const size_t nk = sp->pinned[0];
     *n = nk;
@@ -617,10 +653,11 @@ int aq_sampler_kept(aq_sampler *sp, uint32_t *ids, float *probs, size_t cap, siz
 int aq_sampler_draw(aq_sampler *sp, uint32_t *tok) {
     AQ_REQUIRE(sp && tok, "aq_sampler_draw: null argument");
     AQ_HIP(hipSetDevice(sp->device));
-    int rc = sync_res(sp, sp->ctx->stream);
+    int rc = join(sp, sp->ctx->stream);
+    if (!rc) rc = sync_res(sp, sp->ctx->stream);
     if (rc) return rc;
     AQ_REQUIRE(sp->pinned[0] > 0, "aq_sampler_draw: draw before process (sample.rs:240)");
-    rc = run(base_args(sp, OP_DRAW), sp->ctx->stream);
+    rc = mark(sp, sp->ctx->stream, run(base_args(sp, OP_DRAW), sp->ctx->stream));
     if (!rc) rc = sync_res(sp, sp->ctx->stream);
     if (!rc) *tok = sp->pinned[1];
     return rc;
@@ -634,7 +671,7 @@ int aq_sampler_sample(aq_sampler *sp, const float *logits_dev, uint32_t *tok) {
         return rc;
     }
     AQ_HIP(hipSetDevice(sp->device));
-    int rc = sampler_sample(sp, logits_dev, nullptr, sp->ctx->stream);
+    int rc = sampler_sample(sp, logits_dev, nullptr, sp->ctx->stream); // joins and marks itself
     if (!rc) rc = sync_res(sp, sp->ctx->stream);
     if (!rc) *tok = sp->pinned[1];
     return rc;
@@ -643,7 +680,8 @@ int aq_sampler_sample(aq_sampler *sp, const float *logits_dev, uint32_t *tok) {
 int aq_sampler_write_dense(aq_sampler *sp, float *dense_dev) {
     AQ_REQUIRE(sp && dense_dev, "aq_sampler_write_dense: null argument");
     AQ_HIP(hipSetDevice(sp->device));
-    int rc = sync_res(sp, sp->ctx->stream);
+    int rc = join(sp, sp->ctx->stream);
+    if (!rc) rc = sync_res(sp, sp->ctx->stream);
     if (rc) return rc;
     // sample.rs:259-265: zeros, then the kept set (the operator-level form; the model writes it on the device)
     const size_t nk = sp->pinned[0];
@@ -673,7 +711,8 @@ int aq_sampler_accept_or_resample(aq_sampler *sp, const float *target_dev, const
     hipStream_t st = sp->ctx->stream;
     const uint64_t *keys;
     size_t stride;
-    int rc = candidates(sp, target_dev, 1, st, &keys, &stride);
+    int rc = join(sp, st);
+    if (!rc) rc = candidates(sp, target_dev, 1, st, &keys, &stride);
     if (rc) return rc;
     SampArgs a = base_args(sp, OP_ACCEPT);
     a.logits = target_dev;
@@ -681,7 +720,7 @@ int aq_sampler_accept_or_resample(aq_sampler *sp, const float *target_dev, const
     a.key_stride = stride;
     a.q = q_dev;
     a.d = d;
-    rc = run(a, st);
+    rc = mark(sp, st, run(a, st));
     if (!rc) rc = sync_res(sp, st);
     if (rc) return rc;
     *tok = sp->pinned[1];

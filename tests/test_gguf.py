@@ -139,3 +139,38 @@ def test_malformed_files_are_refused(tmp_path):
     assert L.aq_gguf_open(os.fsencode(short), C.byref(h)) < 0
     assert b"past the end" in L.aq_last_error()
     assert L.aq_gguf_open(os.fsencode(tmp_path / "missing.gguf"), C.byref(h)) < 0
+
+
+def one_tensor_file(path, dims, ggml_type, rel_offset, kv=b"", n_kv=0, data=b"\0" * 256):
+    """A GGUF v3 file with the given metadata bytes and one tensor info `w` (alignment 32), then `data`."""
+    head = b"GGUF" + struct.pack("<IQQ", 3, 1, n_kv) + kv
+    head += gstr("w") + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+    head += struct.pack("<IQ", ggml_type, rel_offset)
+    head += b"\0" * (-len(head) % 32)
+    path.write_bytes(head + data)
+
+
+def test_crafted_offsets_counts_and_arrays_are_refused(tmp_path):
+    """Header fields a crafted file can make wrap in 64 bits are refused with AQ_EINVAL before anything is read or
+    reserved: a tensor offset near 2^64 (a multiple of the alignment, so offset + size wraps below the file size), an
+    element count whose dimension product overflows, and a metadata array whose count exceeds what the bytes left
+    could hold (no allocation is attempted for it). The same file with sane fields opens."""
+    L = aq.lib()
+    h = C.c_void_p()
+    p = tmp_path / "ok.gguf"
+    one_tensor_file(p, [32], 0, 0)  # 32 F32 values at offset 0: inside the 256 data bytes
+    g = aq.Gguf(p)
+    assert g.tensors()[0][4:] == (0, 128)
+    g.close()
+    for name, dims, off in [("wrap_offset", [32], (1 << 64) - 32), ("wrap_count", [1 << 33, 1 << 33], 0),
+                            ("count_times_size", [1 << 62], 0)]:
+        p = tmp_path / f"{name}.gguf"
+        one_tensor_file(p, dims, 0, off)
+        rc = L.aq_gguf_open(os.fsencode(p), C.byref(h))
+        assert rc == aq.AQ_EINVAL or rc == aq.AQ_EUNSUP, (name, rc)
+        assert rc != aq.AQ_EUNSUP or b"not supported" in L.aq_last_error()
+    # an array of 2^40 UINT64 values in a file of a few hundred bytes
+    kv = gstr("general.bad") + struct.pack("<IIQ", 9, 10, 1 << 40)
+    p = tmp_path / "big_array.gguf"
+    one_tensor_file(p, [32], 0, 0, kv=kv, n_kv=1)
+    assert L.aq_gguf_open(os.fsencode(p), C.byref(h)) == aq.AQ_EINVAL

@@ -316,6 +316,153 @@ def test_tiny_forced_drafts_state_equals_plain(ctx, tiny):
         assert np.array_equal(a, os_.export()), f"round {r}: spec state differs from the oracle's"
 
 
+# ------------------------------------------------------------- the reference's identity gate at every k
+STEPS = 200  # spec_identity.rs:20
+
+
+class PlainTracker:
+    """A plain device state advanced token by token to any consumed count (spec_identity.rs:48-72)."""
+
+    def __init__(self, model, prompt, max_pos):
+        self.st = aq.State(model, 0, max_pos)
+        self.st.prefill(prompt)
+        self.consumed = 0
+
+    def at(self, toks, consume):
+        assert consume >= self.consumed, "the plain tracker only moves forward"
+        for tok in toks[self.consumed:consume]:
+            self.st.forward_token(tok)
+        self.consumed = consume
+        return self.st
+
+
+@pytest.mark.parametrize("k", [1, 2, 4, 7])
+def test_tiny_spec_identity_every_k(ctx, tiny, k):
+    """spec_identity.rs:122-205 at k in {1, 2, 4, 7} (7: the largest batch a state takes, 8 verify rows): with the
+    MTP's own drafts, 200 greedy ids equal the plain loop's and every round's drafts and accepted count equal the
+    oracle's; with forced drafts (the continuation corrupted at position j = round % (k + 1), so every acceptance
+    count 0..k occurs), after every round the whole carried state equals a plain state that consumed the same
+    tokens bit for bit, and the oracle's."""
+    print(f"case tiny spec identity k {k}", flush=True)
+    prompt, vocab = tiny["prompt"], tiny["cfg"].vocab
+    max_pos = len(prompt) + STEPS + 64
+    plain_ids, _ = plain_run(aq.State(tiny["gm"], 0, max_pos), prompt, STEPS + 8)
+    # ---- the MTP's own drafts
+    gs, os_ = aq.State(tiny["gm"], k, max_pos), O.State(tiny["om"], k, max_pos)
+    out, oout = [gs.spec_prefill(prompt)], [os_.spec_prefill(prompt)]
+    assert out == oout
+    while len(out) < STEPS:
+        gd, od = gs.drafts(), os_.drafts()
+        m, em = gs.spec_round(out[-1])
+        mo, emo = os_.spec_round(oout[-1])
+        assert (gd, m, em) == (od, mo, emo), f"k={k} round {gs.stats()['rounds']}: differs from the oracle"
+        out += em
+        oout += emo
+    st = gs.stats()
+    print(f"tiny k={k}: {STEPS} ids; rounds {st['rounds']}, accepted {st['accepted']} of {st['drafted']}", flush=True)
+    assert out[:STEPS] == plain_ids[:STEPS], f"k={k}: spec ids differ from plain"
+    assert np.array_equal(gs.export(), os_.export())
+    # ---- forced drafts: every acceptance count, the state checked after every round
+    gs, os_ = aq.State(tiny["gm"], k, max_pos), O.State(tiny["om"], k, max_pos)
+    tracker = PlainTracker(tiny["gm"], prompt, max_pos)
+    out = [gs.spec_prefill(prompt)]
+    assert out == [os_.spec_prefill(prompt)]
+    rnd, hist = 0, [0] * (k + 1)
+    while len(out) < STEPS:
+        j, n = rnd % (k + 1), len(out)
+        d = list(plain_ids[n:n + k])
+        if j < k:
+            d[j] = (d[j] + 1) % vocab
+        gs.set_drafts(d)
+        os_.set_drafts(d)
+        m, em = gs.spec_round(out[-1])
+        mo, emo = os_.spec_round(out[-1])
+        assert (m, em) == (mo, emo), f"k={k} round {rnd}: differs from the oracle"
+        assert m == j and em == plain_ids[n:n + len(em)], f"k={k} round {rnd}: accepted {m} for j {j}"
+        out += em
+        hist[m] += 1
+        consumed = gs.pos - len(prompt)
+        assert consumed == len(out) - 1
+        ref = tracker.at(plain_ids, consumed)
+        a, b = gs.export(), ref.export()
+        assert gs.pos == ref.pos
+        assert np.array_equal(a[: b.size], b), f"k={k} round {rnd}: spec state differs from the plain state"
+        assert np.array_equal(a, os_.export()), f"k={k} round {rnd}: spec state differs from the oracle's"
+        rnd += 1
+    assert gs.stats()["hist"][: k + 1] == hist and all(c > 0 for c in hist), hist
+    print(f"tiny k={k} forced: {rnd} rounds, hist {hist}, state equal after every round", flush=True)
+
+
+@pytest.mark.parametrize("k", [1, 2, 3])
+def test_tiny_spec_prefill_on_a_used_state(ctx, tiny, k):
+    """spec_identity.rs:211-268: a second prompt fed by spec_prefill to a state that already ran speculative rounds
+    (a later chat turn) continues exactly as the plain loop over the same tokens, and as the oracle."""
+    print(f"case tiny spec prefill on a used state k {k}", flush=True)
+    prompt, vocab = tiny["prompt"], tiny["cfg"].vocab
+    second = np.random.default_rng(SEED + 5).integers(0, vocab, 6).astype(np.uint32)
+    n1, n2, max_pos = 40, 60, 256
+    plain_ids, _ = plain_run(aq.State(tiny["gm"], 0, max_pos), prompt, n1)
+    pst = aq.State(tiny["gm"], 0, max_pos)
+    pst.prefill(prompt)
+    for tok in plain_ids[:n1]:  # the plain loop consumes every emitted token before the new prompt
+        pst.forward_token(tok)
+    plain2 = [pst.prefill(second)]
+    while len(plain2) < n2:
+        plain2.append(pst.forward_token(plain2[-1]))
+    gs, os_ = aq.State(tiny["gm"], k, max_pos), O.State(tiny["om"], k, max_pos)
+    out = [gs.spec_prefill(prompt)]
+    assert out == [os_.spec_prefill(prompt)]
+    while len(out) < n1:
+        m, em = gs.spec_round(out[-1])
+        assert (m, em) == os_.spec_round(out[-1])
+        out += em
+    assert out[:n1] == plain_ids[:n1]
+    consumed = gs.pos - len(prompt)
+    if consumed > n1:
+        pytest.skip(f"k={k}: the spec state consumed {consumed} > {n1} tokens (accepted drafts past the cut)")
+    seg2 = np.concatenate([np.asarray(plain_ids[consumed:n1], np.uint32), second])
+    out2 = [gs.spec_prefill(seg2)]
+    assert out2 == [os_.spec_prefill(seg2)]
+    while len(out2) < n2:
+        m, em = gs.spec_round(out2[-1])
+        assert (m, em) == os_.spec_round(out2[-1])
+        out2 += em
+    assert out2[:n2] == plain2, f"k={k}: the second segment differs from the plain loop"
+    assert np.array_equal(gs.export(), os_.export())
+
+
+def test_spec_calls_out_of_order_are_refused(ctx, tiny):
+    """spec.rs:246 and :337 assert the MTP's row count; here the calls return AQ_ESTATE and change nothing: a
+    round after a plain call on a spec state, a spec prefill on a state whose plain calls consumed positions past
+    the MTP's rows, a spec prefill after a plain prefill on a fresh spec state."""
+    print("case spec calls out of order", flush=True)
+    prompt = tiny["prompt"]
+    st = aq.State(tiny["gm"], 3, 128)
+    x = st.spec_prefill(prompt)
+    m, em = st.spec_round(x)
+    tok = st.forward_token(em[-1])  # consumes a position; the MTP still holds pos - 1 + k - 1 rows
+    with pytest.raises(aq.AqError) as e:
+        st.spec_round(tok)
+    assert e.value.code == aq.AQ_ESTATE
+    pos = st.pos
+    st.forward_token(tok)
+    st.forward_token(tok)  # now past the MTP's rows (k - 1 = 2 draft rows beyond the consumed positions)
+    with pytest.raises(aq.AqError) as e:
+        st.spec_prefill(prompt[:4])
+    assert e.value.code == aq.AQ_ESTATE and st.pos == pos + 2
+    fresh = aq.State(tiny["gm"], 3, 128)
+    fresh.prefill(prompt)
+    with pytest.raises(aq.AqError) as e:
+        fresh.spec_prefill(prompt[:4])
+    assert e.value.code == aq.AQ_ESTATE
+    # a spec prefill whose positions the MTP still covers is taken (spec.rs:246 asks rows >= pos)
+    st2 = aq.State(tiny["gm"], 3, 128)
+    x = st2.spec_prefill(prompt)
+    st2.spec_round(x)
+    st2.forward_token(x)
+    st2.spec_prefill(prompt[:4])
+
+
 # ----------------------------------------------------------------------------------- isolated recurrence
 def test_deltanet_recurrence_rollback(ctx):
     nv, nk, dk, dv, t = 32, 16, 128, 128, 4

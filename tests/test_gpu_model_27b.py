@@ -257,3 +257,46 @@ def test_27b_prompt_chunks_equal_token_by_token_feed(big):
     assert np.array_equal(g.export(), f.export()), "chunked prefill state differs"
     g.free()
     f.free()
+
+
+def test_27b_config4_256_ids_plain_equal_spec3(big):
+    """Config 4 over its full length: the 64-token seeded prompt, then 256 greedy ids from the device's plain loop
+    and from its --spec 3 loop are identical (spec_identity.rs:34-119 at the full shape); the spec prefill and the
+    first 4 rounds equal the oracle's (its AVX2 dots), and the spec state at the end equals a plain state that
+    consumed the same tokens, bit for bit."""
+    print("case 27B config 4: 256 greedy ids, plain vs --spec 3", flush=True)
+    n = 256
+    prompt = np.random.default_rng(SEED).integers(0, big["cfg"].vocab, 64).astype(np.uint32)
+    max_pos = len(prompt) + n + 32
+    gp = aq.State(big["gm"], 0, max_pos)
+    plain = [gp.prefill(prompt)]
+    while len(plain) < n:
+        plain.append(gp.forward_token(plain[-1]))
+    gs = aq.State(big["gm"], 3, max_pos)
+    os_ = O.State(big["om"], 3, max_pos)
+    g = [gs.spec_prefill(prompt)]
+    with O.simd(True):
+        o = [os_.spec_prefill(prompt)]
+        assert g == o
+        for r in range(4):
+            gd, od = gs.drafts(), os_.drafts()
+            m, em = gs.spec_round(g[-1])
+            mo, emo = os_.spec_round(o[-1])
+            assert gd == od and (m, em) == (mo, emo), f"round {r}"
+            g += em
+            o += emo
+    del os_
+    while len(g) < n:
+        _, em = gs.spec_round(g[-1])
+        g += em
+    st = gs.stats()
+    print(f"27B config 4: {n} ids, {st['rounds']} rounds, accepted {st['accepted']}", flush=True)
+    assert g[:n] == plain, "--spec 3 ids differ from the plain ids"
+    # the plain state that consumed what the spec state consumed
+    consumed = gs.pos - len(prompt)
+    ref = aq.State(big["gm"], 0, max_pos)
+    ref.prefill(prompt)
+    for tok in g[:consumed]:
+        ref.forward_token(tok)
+    a, b = gs.export(), ref.export()
+    assert gs.pos == ref.pos and np.array_equal(a[: b.size], b)
