@@ -198,3 +198,35 @@ def test_tiny_top_k_1_sampled_spec_is_the_greedy_loop(ctx, tiny):
         xg = xs = a[1][-1]
     assert np.array_equal(g.export(), s.export())
     ds.free()
+
+
+def test_tiny_sampler_calls_right_after_a_sampled_round_see_its_draws(ctx, tiny):
+    """A sampled round returns while its MTP re-feed and draft chain are still queued on the state's stream, and
+    they draw from the sampler. Reading the generator state, or running an operator call on the sampler, right after
+    the round (no drafts() call in between, which would synchronise) must see every draw of the round: the sampler
+    orders its users by its last-use event. Checked against the oracle round by round, with a sampled operator call
+    on the context stream between rounds."""
+    vocab = tiny["cfg"].vocab
+    say("case sampler used right after a sampled round")
+    kw = dict(temperature=1.0, top_k=20, top_p=0.95)
+    ds = aq.Sampler(ctx, aq.sampler_config(**kw, seed=21), vocab)
+    os_ = O.Sampler(O.sampler_config(**kw, seed=21), vocab)
+    g, o = aq.State(tiny["gm"], 3, 200), O.State(tiny["om"], 3, 200)
+    xg, xo = g.spec_prefill(tiny["prompt"], sampler=ds), o.spec_prefill(tiny["prompt"], sampler=os_)
+    assert xg == xo
+    row = logits_rows(vocab, 1, SEED + 9)[0]
+    dev_row = aq.DeviceBuffer(ctx, row.nbytes)
+    dev_row.upload(row)
+    for r in range(8):
+        mg, eg = g.spec_round(xg, sampler=ds)
+        mo, eo = o.spec_round(xo, sampler=os_)
+        assert np.array_equal(ds.rng(), os_.rng()), f"round {r}: generator state read right after the round"
+        assert (mg, eg) == (mo, eo), f"round {r}"
+        # an operator call on the context stream while nothing has synchronised the state's stream
+        tg = ds.sample(dev_row)
+        to = os_.sample(row)
+        assert tg == to and np.array_equal(ds.rng(), os_.rng()), f"round {r}: operator sample after the round"
+        assert g.drafts() == o.drafts(), f"round {r}: drafts"
+        xg, xo = eg[-1], eo[-1]
+    assert np.array_equal(g.export(), o.export())
+    ds.free()
