@@ -196,24 +196,31 @@ def cpu_info():
     return {"model": model, "logical_cpus": os.cpu_count(), "nproc": len(allowed), "physical_cores": phys}
 
 
-def cpu_matmul_gbs(O, threads):
+def cpu_matmul_gbs(O, threads, nmat=8):
     """The oracle's matvec (N = 1, config 2) and verify op (N = 4, config 3 at k = 3) on the two single-op shapes:
-    weight GB/s (W bytes / time per call), each timed over >= 1 s."""
+    weight GB/s (W bytes / time per call), each timed over >= 1 s. `weight_GBs` rotates through `nmat` distinct
+    matrices of the shape (8 x 50-73 MB, beyond the host's last-level cache, as the GPU sweep rotates 8 past the
+    MALL), so it is a DRAM rate; `weight_GBs_one_matrix` repeats one matrix, which the cache holds."""
     out = []
     for t, rows, cols in [(aq.Q4_K, 17408, 5120), (aq.Q6_K, 5120, 17408)]:
-        host = aq.synth_host(aq.synth_spec(t, rows, cols, seed=SEED + 300), threads).view(np.uint8)
+        hosts = [aq.synth_host(aq.synth_spec(t, rows, cols, seed=SEED + 300 + i), threads).view(np.uint8)
+                 for i in range(nmat)]
         wbytes = rows * aq.row_bytes(t, cols)
         x = np.random.default_rng(3).standard_normal((4, cols)).astype(np.float32)
         for n in (1, 4):
-            O.matmul(t, host, rows, cols, x[:n], threads=threads)
-            reps, t0 = 0, time.perf_counter()
-            while time.perf_counter() - t0 < 1.0 or reps < 2:
-                O.matmul(t, host, rows, cols, x[:n], threads=threads)
-                reps += 1
-            dt = (time.perf_counter() - t0) / reps
-            name = {aq.Q4_K: "Q4_K", aq.Q6_K: "Q6_K"}[t]
-            out.append({"kernel": f"{name} {rows}x{cols}", "n": n, "ms_per_call": round(dt * 1e3, 2),
-                        "weight_GBs": round(wbytes / dt / 1e9, 2)})
+            rates = {}
+            for label, mats in (("rotate", hosts), ("one", hosts[:1])):
+                O.matmul(t, mats[0], rows, cols, x[:n], threads=threads)
+                reps, t0 = 0, time.perf_counter()
+                while time.perf_counter() - t0 < 1.0 or reps < 2 * len(mats):
+                    O.matmul(t, mats[reps % len(mats)], rows, cols, x[:n], threads=threads)
+                    reps += 1
+                rates[label] = (time.perf_counter() - t0) / reps
+            out.append({"kernel": f"{TYPE_NAME[t]} {rows}x{cols}", "n": n, "ms_per_call": round(rates["rotate"] * 1e3, 2),
+                        "weight_GBs": round(wbytes / rates["rotate"] / 1e9, 2),
+                        "weight_GBs_one_matrix": round(wbytes / rates["one"] / 1e9, 2),
+                        "matrices": nmat, "bytes_rotated": nmat * wbytes})
+        del hosts
     return out
 
 
@@ -229,7 +236,7 @@ def cpu_baseline(cfg, plan, k, seconds, gpu_model, prompt):
     with O.simd(True):
         res = cpu_baseline_run(O, cfg, plan, k, seconds, gpu_model, prompt)
     with O.simd(False):
-        res["matmul_scalar"] = cpu_matmul_gbs(O, res["cores"])
+        res["matmul_scalar"] = cpu_matmul_gbs(O, res["cores"], nmat=2)  # the scalar dots are compute-bound
     return res
 
 

@@ -92,3 +92,38 @@ def test_synth_uniform_and_const():
     assert u.min() >= -0.5 and u.max() < 0.5 and abs(float(u.mean())) < 0.03
     c = aq.synth_host(aq.synth_spec(aq.F32, 1, 48, 9, aq.CONST, 1.0, 0.0))
     assert np.all(c == 1.0)
+
+
+def c_decls():
+    """{name: parameter count} of every function include/aq.h declares."""
+    text = open(os.path.join(ROOT, "include", "aq.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(aq_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        p = params.strip()
+        out[name] = 0 if p in ("", "void") else p.count(",") + 1
+    return out
+
+
+def test_integration_rust_binding_matches_the_header():
+    """INTEGRATION.md's ffi.rs: every `pub fn` is a function aq.h declares, with as many parameters; the raw types
+    it uses are imported; every libaq entry point the integration table routes a reference function to is declared
+    in the binding (a maintainer can paste the block as written)."""
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = re.search(r"```rust\n#!\[allow\(non_camel_case_types\)\]\n(.*?)```", doc, flags=re.S).group(1)
+    decl = c_decls()
+    fns = dict(re.findall(r"pub fn (aq_[a-z0-9_]+)\(([^)]*)\)", block, flags=re.S))
+    assert len(fns) >= 40
+    for name, params in fns.items():
+        assert name in decl, f"ffi.rs declares {name}, which aq.h does not"
+        n = 0 if not params.strip() else params.count(":")
+        assert n == decl[name], f"{name}: {n} parameters in ffi.rs, {decl[name]} in aq.h"
+    imported = set(re.search(r"use std::os::raw::\{([^}]*)\}", block).group(1).replace(" ", "").split(","))
+    for ty in ("c_char", "c_int", "c_void"):
+        if re.search(rf"\b{ty}\b", block.split("\n", 2)[-1]):
+            assert ty in imported, f"ffi.rs uses {ty} without importing it"
+    table = doc[doc.index("## 3."):]
+    table = table[: table.index("\n\n", table.index("|---|"))]
+    routed = set(re.findall(r"`(aq_[a-z0-9_]+)", table)) & set(decl)  # functions, not the structs named there
+    missing = sorted(n for n in routed if n not in fns)
+    assert not missing, f"the table routes to {missing}, which ffi.rs does not declare"
