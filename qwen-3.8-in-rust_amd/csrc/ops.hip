@@ -346,7 +346,6 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
     const int j = threadIdx.x, lane = j & 63, wave = j >> 6;
     const int kh = p % a.nk;
     const int kd = a.nk * DK, vd = a.nv * DV, cd = 2 * kd + vd;
-    const bool has_v = j < DV;
     const bool gated = a.out && !raw_;
     // the gate inputs, loaded before phase A so their latency hides behind it: wave 5 computes the decays and
     // wave 7 the betas (lane i = row i), each in its own wave so neither waits for the other's branch
@@ -363,7 +362,17 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
             gdt = a.dt_bias[p];
         }
     }
-    const float nrm_w = gated && has_v ? a.ssm_norm[j] : 0.0f; // phase D's norm weight
+    const float nrm_w = gated && j < t * DV ? a.ssm_norm[j % DV] : 0.0f; // phase D's norm weight (thread's column)
+    // the state column, split by key: thread j holds keys [h KH, h KH + KH) of column c = j % DV, part h = j / DV;
+    // its loads are issued first, so their latency passes under phase A's loads (both are latency-bound phases)
+    constexpr int H = dn_parts<DK, DV>(), KH = DK / H;
+    const int c = j % DV, h = j / DV;
+    const bool has_col = h < H;
+    float *srec = a.rec + (size_t)p * DK * DV;
+    if (has_col && first) {
+#pragma unroll
+        for (int k = 0; k < KH; k++) s[k] = srec[(size_t)(h * KH + k) * DV + c];
+    }
 
     // ---- A: channels over all rows
     if (raw_) {
@@ -535,16 +544,6 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
             rbeta[i] = raw_ ? v : sigmoid_f(v);
         }
     }
-    // ---- the state column, split by key: thread j holds keys [h KH, h KH + KH) of column c = j % DV, part
-    // h = j / DV (the loads fly while waves 4-7 finish the sums above)
-    constexpr int H = dn_parts<DK, DV>(), KH = DK / H;
-    const int c = j % DV, h = j / DV;
-    const bool has_col = h < H;
-    float *srec = a.rec + (size_t)p * DK * DV;
-    if (has_col && first) {
-#pragma unroll
-        for (int k = 0; k < KH; k++) s[k] = srec[(size_t)(h * KH + k) * DV + c];
-    }
     __syncthreads();
     if (!raw_) {
         for (int e = j; e < t * DK; e += DN_THREADS) {
@@ -646,14 +645,16 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
             }
         }
         __syncthreads();
-        // the gated output, and with out_q80 its Q8_0 form (quant.rs quantize_q8_0): the head's rows are whole
-        // 32-blocks, one per half wave of the state columns (has_v is uniform over each half wave: DV % 32 == 0)
-        if (has_v)
-            for (int i = 0; i < t; i++) {
-                const float v = (nrm_w * (so[i][j] * ro[i])) * sz[i][j];
-                a.out[(size_t)(r0 + i) * vd + p * DV + j] = v;
-                if (a.out_q80) q8_0_block_half(a.q80, r0 + i, (size_t)p * (DV / 32) + (j >> 5), v, lane);
-            }
+        // the gated output, and with out_q80 its Q8_0 form (quant.rs quantize_q8_0): thread j takes row j / DV,
+        // column j % DV (rows past DN_THREADS / DV in further passes); the head's rows are whole 32-blocks, one per
+        // half wave (uniform over each half wave: DV % 32 == 0)
+        for (int e = j; e < t * DV; e += DN_THREADS) {
+            const int i = e / DV, jc = e % DV;
+            const float w = e == j ? nrm_w : a.ssm_norm[jc];
+            const float v = (w * (so[i][jc] * ro[i])) * sz[i][jc];
+            a.out[(size_t)(r0 + i) * vd + p * DV + jc] = v;
+            if (a.out_q80) q8_0_block_half(a.q80, r0 + i, (size_t)p * (DV / 32) + (jc >> 5), v, lane);
+        }
     }
 }
 
