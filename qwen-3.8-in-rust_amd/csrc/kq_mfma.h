@@ -68,6 +68,23 @@ __device__ __forceinline__ int sdot2(uint32_t a, uint32_t b) {
     return __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b), 0, false);
 }
 
+// A 4 x 4 transpose of 16-lane rows across four registers: on entry row q (lanes 16q..16q+15) of p_k holds chain k's
+// value for K slice q; on exit row q of p_m holds chain q's value for K slice m. Two v_permlane16_swap (odd rows of
+// the first register with even rows of the second), then two v_permlane32_swap (upper half of the first with lower
+// half of the second), all within the wave's registers.
+__device__ __forceinline__ void xpose4(float &p0, float &p1, float &p2, float &p3) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, p0), __builtin_bit_cast(unsigned, p1),
+                                                    false, false);
+    const auto b = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, p2), __builtin_bit_cast(unsigned, p3),
+                                                    false, false);
+    const auto c = __builtin_amdgcn_permlane32_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane32_swap(a[1], b[1], false, false);
+    p0 = __builtin_bit_cast(float, (unsigned)c[0]);
+    p2 = __builtin_bit_cast(float, (unsigned)c[1]);
+    p1 = __builtin_bit_cast(float, (unsigned)d[0]);
+    p3 = __builtin_bit_cast(float, (unsigned)d[1]);
+}
+
 __device__ __forceinline__ int sbyte(uint32_t w, int i) { return (int)(int8_t)(w >> (8 * i)); }
 __device__ __forceinline__ int ubyte(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xFF); }
 
@@ -400,22 +417,27 @@ struct KqGroup {
 // [slot][NCP], activation-sum pairs [slot][NP][NCP] (the 4 sub-block-sum pairs for Q4_K/Q5_K segments, HAS45, then
 // the 8 group-sum pairs for Q6_K segments, HAS6). 16 threads per (column, super-block) record of 256 codes, two
 // records per thread group in flight (few registers: the weight ring stays resident).
-template <int NC, bool HAS45, bool HAS6>
+template <int NC, bool HAS45, bool HAS6, int B = 2>
 __device__ __forceinline__ void kq_stage(const KqGroup &G, int8_t *sxq, float *sxd, uint32_t *sxm, int s0, int ns) {
     constexpr int NCP = (NC + 3) / 4 * 4;
     constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), P6 = HAS45 ? 4 : 0;
     const int nb = G.nb;
-    const int o = threadIdx.x & 15, nrec = ns * NC;
-    for (int r0 = (int)threadIdx.x >> 4; r0 < nrec; r0 += 32) {
-        const int ra = r0, rb = r0 + 16 < nrec ? r0 + 16 : r0; // the second record, or the first again
-        // record r = (super-block r / NC, column r % NC): NC is a constant, so no division by a runtime value
-        const int sa = ra / NC, ca = ra - sa * NC, sbb = rb / NC, cb = rb - sbb * NC;
-        const uint4 va =
-            *reinterpret_cast<const uint4 *>(G.xqs + (size_t)ca * G.xcol + (size_t)(s0 + sa) * 256 + o * 16);
-        const uint4 vb =
-            *reinterpret_cast<const uint4 *>(G.xqs + (size_t)cb * G.xcol + (size_t)(s0 + sbb) * 256 + o * 16);
-        *reinterpret_cast<uint4 *>(sxq + ((size_t)sa * NC + ca) * KQ_XS + o * 16) = va;
-        *reinterpret_cast<uint4 *>(sxq + ((size_t)sbb * NC + cb) * KQ_XS + o * 16) = vb;
+    const uint32_t o = threadIdx.x & 15u, g = threadIdx.x >> 4, nrec = (uint32_t)(ns * NC);
+    // B records per thread in flight: all B loads are issued before the first LDS write (past the end a thread
+    // reloads and rewrites the last record, so every load is issued and the wait counts stay exact)
+    for (uint32_t r0 = 0; r0 < nrec; r0 += 16u * B) { // uniform
+        uint4 v[B];
+#pragma unroll
+        for (int i = 0; i < B; i++) {
+            // record r = (super-block r / NC, column r % NC): NC is a constant, so no division by a runtime value
+            const uint32_t rc = min(r0 + g + 16u * i, nrec - 1u), sb = rc / NC, c = rc - sb * NC;
+            v[i] = *reinterpret_cast<const uint4 *>(G.xqs + (c * (uint32_t)G.xcol + (s0 + sb) * 256u + o * 16u));
+        }
+#pragma unroll
+        for (int i = 0; i < B; i++) {
+            const uint32_t rc = min(r0 + g + 16u * i, nrec - 1u), sb = rc / NC, c = rc - sb * NC;
+            *reinterpret_cast<uint4 *>(sxq + ((sb * NC + c) * KQ_XS + o * 16u)) = v[i];
+        }
     }
     for (int e = (int)threadIdx.x; e < nrec; e += 256) {
         const int sb = e / NC, c = e - sb * NC;
@@ -676,6 +698,21 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
             __builtin_amdgcn_sched_barrier(0);
         }
         const int live = nb - crd * KSW < KSW ? nb - crd * KSW : KSW; // super-blocks in this round (uniform)
+        if constexpr (KSW == 4 && NCH % 4 == 0) {
+            // chains in groups of four by register transposes: the owner of chain 4m + ks (K slice ks) then holds
+            // its four products in super-block order
+#pragma unroll
+            for (int m = 0; m < NCH / 4; m++) {
+                float q[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) q[u] = pr[(4 * m + u) / NC][(4 * m + u) % NC];
+                xpose4(q[0], q[1], q[2], q[3]);
+                acc[m] += q[0];
+                if (live > 1) acc[m] += q[1];
+                if (live > 2) acc[m] += q[2];
+                if (live > 3) acc[m] += q[3];
+            }
+        } else {
 #pragma unroll
         for (int k = 0; k < NCH; k++) xw[ks * X::S + k * NI + idx] = pr[k / NC][k % NC];
         __asm__ volatile("" ::: "memory");
@@ -700,6 +737,7 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
             }
         }
         __asm__ volatile("" ::: "memory");
+        }
         if (++crd == nr) { // uniform across the wave
             finish_tile();
             crd = 0;
@@ -838,6 +876,386 @@ kq_wave_kernel(KqGroup G) {
         kq_wave_run<T1, NC, KSW, PF, HAS45, HAS6, IS>(G, sg, wg, sxq, sxd, sxm, xw);
 }
 
+// ------------------------------------------------------------------------------------ the lane-half kernel
+// A matrix of few rows (the 5120-row down projections: 1280 tiles of 4 rows) gives the wave-split kernel about one
+// wave per SIMD, which then waits on its own latencies for most of the launch. Here a pair of waves of one
+// work-group shares each tile: wave h of the pair computes reference lane j + 4h (j = 0..3, lane pair j's thread
+// block) of every super-block, and the h = 1 wave also the Q4_K/Q5_K min lanes. The 8 lane chains are independent
+// until the final reduction (kdot.rs:1-18), so the two waves need no hand-off while they stream K; once at the end
+// they meet (a work-group barrier) and the h = 0 wave forms ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)) [+ (m0+m2)+(m1+m3)]
+// from both waves' chains. Each wave loads and unpacks only its lane's codes (half the bytes of a tile): a launch
+// has twice the waves, each with about half the work per round.
+
+// This wave's half of one super-block's weight bytes (load_w): the codes of lane j + 4h, the row's scale record, and
+// for Q5_K / Q6_K the high bits of that lane.
+template <int TYPE>
+__device__ __forceinline__ void load_w_half(WRegs<TYPE> &w, const MfArgs &a, uint32_t tile, int r, int j, int h) {
+    const uint32_t jr = (uint32_t)(j * 4 + r), hh = (uint32_t)h;
+    w.qa0 = *reinterpret_cast<const uint4 *>(a.qa + (tile * 512u + jr * 16u + hh * 256u));
+    w.sc = *reinterpret_cast<const uint4 *>(a.sc + (tile * 64u + (uint32_t)r * 16u));
+    if constexpr (TYPE == AQ_TYPE_Q5_K) {
+        w.qb.x = *reinterpret_cast<const uint32_t *>(a.qb + (tile * 128u + jr * 8u + hh * 4u));
+    } else if constexpr (TYPE == AQ_TYPE_Q6_K) {
+        const uint2 q = *reinterpret_cast<const uint2 *>(a.qb + (tile * 256u + jr * 16u + hh * 8u));
+        w.qb.x = q.x;
+        w.qb.y = q.y;
+        w.d6 = *reinterpret_cast<const uint16_t *>(a.dm + (tile * 8u + (uint32_t)r * 2u));
+    }
+}
+
+// One super-block's products for one thread of a lane-half wave: pr = the lane chain's product (dx*dw)*float(sum)
+// of lane l = j + 4h, per column; with `mins` (uniform) also pm = the min lane j's product. The integers and the
+// f32 operations are those sb_products_split (Q4_K/Q5_K) and sb_products (Q6_K) compute for the same lanes
+// (kdot.rs:37-140). With IS the integers are returned too (is: lane l's sum, ism: the min product).
+template <int TYPE, int NC, int XS = 256, bool IS = false>
+__device__ __forceinline__ void sb_half_products(const WRegs<TYPE> &wv, const int8_t *xq, const float *xd,
+                                                 const uint32_t *xm, int ncp, int j, int r, int h, bool mins,
+                                                 float *pr, float *pm, int *is = nullptr, int *ism = nullptr) {
+    constexpr int NCG = (NC + 3) / 4;
+    const uint32_t w[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w}; // lane l's codes
+    const int xo = j * 64 + h * 32;                                   // lane l's 32 activation codes in a record
+    if constexpr (TYPE == AQ_TYPE_Q6_K) {
+        const uint32_t qh[2] = {wv.qb.x, wv.qb.y};
+        const uint32_t sw[4] = {wv.sc.x, wv.sc.y, wv.sc.z, wv.sc.w};
+        uint32_t code[8];
+        int scl[8];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const int s = hh * 4 + kk;
+                const int li = kk < 2 ? hh * 2 + kk : hh * 2 + kk - 2, sh = kk < 2 ? 0 : 4;
+                code[s] = ((w[li] >> sh) & 0x0F0F0F0Fu) | (((qh[hh] >> (2 * kk)) & 0x03030303u) << 4);
+                // group hh*8 + 2kk + h: word hh*2 + kk/2, byte 2(kk&1) + h
+                scl[s] = (int)(int8_t)(sw[hh * 2 + (kk >> 1)] >> (8 * (2 * (kk & 1) + h)));
+            }
+        // the -32 fold scales of lane l: groups 2l, 2l+1 = bytes 2(j&1), 2(j&1)+1 of word 2h + j/2
+        const uint32_t ow = h ? ((j >> 1) ? sw[3] : sw[2]) : ((j >> 1) ? sw[1] : sw[0]);
+        const int osa = sbyte(ow, 2 * (j & 1)), osb = sbyte(ow, 2 * (j & 1) + 1);
+        const uint32_t osp = ((uint32_t)osa & 0xFFFFu) | ((uint32_t)osb << 16);
+        const float dw = h2f(wv.d6);
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++) {
+            const int cA = cg * 4 + r < NC ? cg * 4 + r : 0;
+            const uint4 *xp = reinterpret_cast<const uint4 *>(xq + cA * XS + xo);
+            const uint4 va = xp[0], vb = xp[1];
+            const uint32_t x[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+            int s0[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const v4i d = mfma(x[s], code[s]);
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    if (cg * 4 + c < NC) s0[c] += __mul24(scl[s], d[c]);
+            }
+            const float4 dx4 = *reinterpret_cast<const float4 *>(xd + cg * 4);
+            const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            const uint4 m = *reinterpret_cast<const uint4 *>(xm + (j + 4 * h) * ncp + cg * 4);
+            const uint32_t mw[4] = {m.x, m.y, m.z, m.w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int col = cg * 4 + c;
+                if (col < NC) {
+                    const float dd = dxs[c] * dw;
+                    const int i0 = s0[c] - 32 * sdot2(osp, mw[c]);
+                    pr[col] = dd * (float)i0;
+                    if constexpr (IS) {
+                        is[col] = i0;
+                        ism[col] = 0;
+                    }
+                }
+            }
+        }
+    } else {
+        constexpr int DB = TYPE == AQ_TYPE_Q4_K ? 3 : 2, ND = TYPE == AQ_TYPE_Q4_K ? 2 : 3;
+        constexpr uint32_t DM = (1u << DB) - 1u;
+        uint4 xh[2];
+        float4 dxh;
+        uint4 mh;
+        if constexpr (NCG == 1) { // the activation reads first: their LDS latency passes under the unpacking
+            const uint4 *xp = reinterpret_cast<const uint4 *>(xq + (r < NC ? r : 0) * XS + xo);
+            xh[0] = xp[0];
+            xh[1] = xp[1];
+            dxh = *reinterpret_cast<const float4 *>(xd);
+            mh = *reinterpret_cast<const uint4 *>(xm + j * ncp);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const uint32_t q0 = wv.sc.y, q1 = wv.sc.z, q2 = wv.sc.w;
+        const uint32_t sc_lo = q0 & 0x3F3F3F3Fu, mn_lo = q1 & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (q2 & 0x0F0F0F0Fu) | ((q0 >> 2) & 0x30303030u);
+        const uint32_t mn_hi = ((q2 >> 4) & 0x0F0F0F0Fu) | ((q1 >> 2) & 0x30303030u);
+        const uint32_t mnw = j < 2 ? mn_lo : mn_hi;
+        const uint32_t mnp = __builtin_amdgcn_perm(0u, mnw, (uint32_t)(2 * (j & 1)) | 0x0C00u |
+                                                              ((uint32_t)(2 * (j & 1) + 1) << 16) | 0x0C000000u);
+        uint32_t dig[ND][4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t src = p < 2 ? sc_lo : sc_hi, b0 = (uint32_t)(2 * (p & 1));
+            const uint32_t pw = __builtin_amdgcn_perm(0u, src, b0 | 0x0C00u | ((b0 + 1u) << 16) | 0x0C000000u);
+#pragma unroll
+            for (int i = 0; i < ND; i++) dig[i][p] = (pw >> (DB * i)) & (DM * 0x00010001u);
+        }
+        uint32_t code[8];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            code[2 * q] = w[q] & 0x0F0F0F0Fu;
+            code[2 * q + 1] = (w[q] >> 4) & 0x0F0F0F0Fu;
+        }
+        if constexpr (TYPE == AQ_TYPE_Q5_K) {
+#pragma unroll
+            for (int s = 0; s < 8; s++) code[s] |= ((wv.qb.x >> s) & 0x01010101u) << 4;
+        }
+        const float dw = h2f(wv.sc.x & 0xFFFF), dminw = h2f(wv.sc.x >> 16);
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++) {
+            const uint4 *xp = reinterpret_cast<const uint4 *>(xq + (cg * 4 + r < NC ? cg * 4 + r : 0) * XS + xo);
+            const uint4 va = NCG == 1 ? xh[0] : xp[0], vb = NCG == 1 ? xh[1] : xp[1];
+            const uint32_t x[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+            v4i acc[ND];
+#pragma unroll
+            for (int i = 0; i < ND; i++) acc[i] = (v4i){0, 0, 0, 0};
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+#pragma unroll
+                for (int i = 0; i < ND; i++) {
+                    const u16x2 dp = as_u16x2(dig[i][s >> 1]);
+                    const u16x2 d2 = (s & 1) ? (u16x2){dp.y, dp.y} : (u16x2){dp.x, dp.x};
+                    acc[i] = mfma_acc(x[s], as_u32(as_u16x2(code[s]) * d2), acc[i]);
+                }
+            }
+            const float4 dx4 = NCG == 1 ? dxh : *reinterpret_cast<const float4 *>(xd + cg * 4);
+            const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            const uint4 m0 = NCG == 1 ? mh : *reinterpret_cast<const uint4 *>(xm + j * ncp + cg * 4);
+            const uint32_t mw0[4] = {m0.x, m0.y, m0.z, m0.w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int col = cg * 4 + c;
+                if (col < NC) {
+                    int s0 = acc[ND - 1][c];
+#pragma unroll
+                    for (int i = ND - 2; i >= 0; i--) s0 = (s0 << DB) + acc[i][c];
+                    const float dd = dxs[c] * dw;
+                    pr[col] = dd * (float)s0;
+                    if constexpr (IS) is[col] = s0;
+                    // the min lane only in the h = 1 wave (uniform); one unconditional store of the result keeps
+                    // pm in registers
+                    float pv = 0.0f;
+                    int iv = 0;
+                    if (mins) {
+                        iv = sdot2(mnp, mw0[c]);
+                        pv = (-dxs[c] * dminw) * (float)iv;
+                    }
+                    pm[col] = pv;
+                    if constexpr (IS) ism[col] = iv;
+                }
+            }
+        }
+    }
+}
+
+// Chains of the h = 1 wave of a pair: lane j + 4 per column, and for Q4_K/Q5_K the min lane j per column (the h = 0
+// wave runs the first NC).
+template <int TYPE, int NC>
+constexpr int kq_lh_nch() { return (TYPE == AQ_TYPE_Q6_K ? 1 : 2) * NC; }
+
+// One wave of a lane-half pair: the pair's tile is wg * 2 + wid / 2 (4 rows; past the last one the rows are clamped
+// and nothing is stored), its lane half h = wid % 2. The round structure is kq_wave_run's with KSW = 4 and one
+// tile per wave: the K slices' products reach the chain owners through the wave's LDS slot in super-block order.
+template <int TYPE, int NC, int PF, bool HAS45, bool HAS6, bool IS = false>
+__device__ __forceinline__ void kq_lh_run(const KqGroup &G, const KqSeg &sg, int wg, int8_t *sxq, float *sxd,
+                                          uint32_t *sxm, float *xch) {
+    constexpr int KSW = 4, NI = 16;
+    constexpr int NCP = (NC + 3) / 4 * 4;
+    constexpr bool Q6 = TYPE == AQ_TYPE_Q6_K;
+    constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), POFF = Q6 && HAS45 ? 4 : 0;
+    constexpr int NCH = kq_lh_nch<TYPE, NC>();
+    constexpr int NO = (NCH + KSW - 1) / KSW;
+    using X = KqXch<NCH, KSW>;
+    MfArgs a{};
+    a.qa = sg.qa;
+    a.qb = sg.qb;
+    a.sc = sg.sc;
+    a.dm = sg.dm;
+    a.rows = sg.rows;
+    a.nb = G.nb;
+    const int nb = G.nb;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int h = wid & 1;
+    const bool mins = !Q6 && h == 1;
+    const int nch = mins ? NCH : NC; // chains of this wave (uniform)
+    const int b = lane >> 2, r = lane & 3, j = b & 3, ks = b >> 2;
+    const int idx = j * 4 + r; // chain owner index within the wave
+    float *xw = xch + wid * X::FLOATS;
+    const int chk = G.chk;
+    const int tile = wg * 2 + (wid >> 1);
+    const int row = tile * 4 + r < a.rows ? tile * 4 + r : a.rows - 1;
+    const int nr = (nb + KSW - 1) / KSW; // rounds
+    int prd = 0;
+    const uint32_t ptile = (uint32_t)(row >> 2) * (uint32_t)nb + (uint32_t)ks, plast = ptile - ks + nb - 1;
+    const int prr = row & 3;
+    auto issue = [&](WRegs<TYPE> &wv) {
+        const uint32_t tl = ptile + (uint32_t)(prd * KSW);
+        load_w_half<TYPE>(wv, a, tl < plast ? tl : plast, prr, j, h);
+        prd++;
+    };
+    WRegs<TYPE> wr[PF];
+    const int ns0 = chk < nb ? chk : nb;
+    if (ns0 * NC <= KQ_STAGE_REGS) { // uniform
+        KqStageRegs<HAS45, HAS6> R;
+        kq_stage_load<NC>(G, R, ns0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < PF; p++) issue(wr[p]);
+        __builtin_amdgcn_sched_barrier(0);
+        kq_stage_store<NC>(R, sxq, sxd, sxm, ns0);
+    } else {
+#pragma unroll
+        for (int p = 0; p < PF; p++) issue(wr[p]);
+        kq_stage<NC, HAS45, HAS6>(G, sxq, sxd, sxm, 0, ns0);
+    }
+    __syncthreads();
+    int s0 = 0; // first super-block of the staged chunk
+    float acc[NO];
+#pragma unroll
+    for (int i = 0; i < NO; i++) acc[i] = 0.0f;
+    int crd = 0; // round
+    auto round_body = [&](WRegs<TYPE> &wv, const bool prefetch) {
+        const int sb = crd * KSW + ks;
+        const int sbc = sb < nb ? sb : nb - 1;
+        float pr[2][NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) pr[1][c] = 0.0f;
+        const int ls = sbc - s0; // LDS slot
+        const int8_t *xq = sxq + (size_t)ls * NC * KQ_XS;
+        const float *xd = sxd + ls * NCP;
+        const uint32_t *xm = sxm + (ls * NP + POFF) * NCP;
+        int ip[2][IS ? NC : 1];
+        sb_half_products<TYPE, NC, KQ_XS, IS>(wv, xq, xd, xm, NCP, j, r, h, mins, pr[0], pr[1], ip[0], ip[1]);
+        if constexpr (IS) { // the exact integers of this (row, super-block): lane j + 4h, and the min lane j
+            const int orow = tile * 4 + r;
+            if (sb < nb && orow < a.rows) {
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const size_t o = ((size_t)c * a.rows + orow) * nb + sb;
+                    G.isl[o * 8 + j + 4 * h] = ip[0][c];
+                    if (!Q6 && h == 1) G.ism[o * 4 + j] = ip[1][c];
+                    if (Q6 && h == 0) G.ism[o * 4 + j] = 0;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NCH; k++) __asm__ volatile("" : "+v"(pr[k / NC][k % NC]));
+        if (prefetch) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(wv);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const int live = nb - crd * KSW < KSW ? nb - crd * KSW : KSW; // super-blocks in this round (uniform)
+        if constexpr (NC % 4 == 0) {
+            // chains in groups of four by register transposes (xpose4): the owner of chain 4m + ks then holds its
+            // four products in super-block order
+#pragma unroll
+            for (int m = 0; m < NCH / 4; m++) {
+                if (4 * m < nch) { // uniform
+                    float q[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) q[u] = pr[(4 * m + u) / NC][(4 * m + u) % NC];
+                    xpose4(q[0], q[1], q[2], q[3]);
+                    acc[m] += q[0];
+                    if (live > 1) acc[m] += q[1];
+                    if (live > 2) acc[m] += q[2];
+                    if (live > 3) acc[m] += q[3];
+                }
+            }
+        } else {
+#pragma unroll
+        for (int k = 0; k < NCH; k++)
+            if (k < nch) xw[ks * X::S + k * NI + idx] = pr[k / NC][k % NC];
+        __asm__ volatile("" ::: "memory");
+        if (live == KSW) {
+#pragma unroll
+            for (int m = 0; m < NO; m++) {
+                const int k = ks + KSW * m;
+                if (k < nch) {
+#pragma unroll
+                    for (int k2 = 0; k2 < KSW; k2++) acc[m] += xw[k2 * X::S + k * NI + idx];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < NO; m++) {
+                const int k = ks + KSW * m;
+                if (k < nch) {
+#pragma unroll
+                    for (int k2 = 0; k2 < KSW; k2++)
+                        if (k2 < live) acc[m] += xw[k2 * X::S + k * NI + idx];
+                }
+            }
+        }
+        __asm__ volatile("" ::: "memory");
+        }
+        crd++;
+    };
+    auto next_chunk = [&]() {
+        if (crd * KSW >= s0 + chk) { // uniform across the work-group
+            __syncthreads();
+            s0 += chk;
+            kq_stage<NC, HAS45, HAS6>(G, sxq, sxd, sxm, s0, nb - s0 < chk ? nb - s0 : chk);
+            __syncthreads();
+        }
+    };
+    const int nfull = nr / PF * PF;
+    for (int i = 0; i < nfull; i += PF) {
+        next_chunk();
+#pragma unroll
+        for (int p = 0; p < PF; p++) round_body(wr[p], true);
+    }
+    if (nfull < nr) next_chunk();
+#pragma unroll
+    for (int p = 0; p < PF; p++)
+        if (nfull + p < nr) round_body(wr[p], false);
+    // the final chains to the wave's slot [chain][owner]; the pair meets; the h = 0 wave reduces both halves
+#pragma unroll
+    for (int m = 0; m < NO; m++) {
+        const int k = ks + KSW * m;
+        if (k < nch) xw[k * NI + idx] = acc[m];
+    }
+    __syncthreads();
+    if (h == 0 && lane < 4 * NC) {
+        const int col = lane >> 2, rw = lane & 3;
+        const float *x1 = xw + X::FLOATS; // the partner's slot (wave wid + 1)
+        float a0[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) a0[jj] = xw[col * NI + 4 * jj + rw] + x1[col * NI + 4 * jj + rw];
+        float v = (a0[0] + a0[2]) + (a0[1] + a0[3]);
+        if constexpr (!Q6) {
+            const float *m = x1 + (NC + col) * NI + rw;
+            v = v + ((m[0] + m[8]) + (m[4] + m[12]));
+        }
+        const int orow = tile * 4 + rw;
+        if (orow < a.rows) {
+            const size_t o = (size_t)col * a.rows + orow;
+            sg.y[o] = sg.resid ? sg.resid[o] + v : v;
+        }
+    }
+}
+
+template <int T, int NC, int PF, bool IS = false>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NC <= 4 ? 4 : 1)))
+kq_lh_kernel(KqGroup G) {
+    constexpr bool HAS6 = T == AQ_TYPE_Q6_K, HAS45 = !HAS6;
+    constexpr int NCP = (NC + 3) / 4 * 4;
+    using X = KqXch<kq_lh_nch<T, NC>(), 4>;
+    extern __shared__ __align__(16) uint8_t kq_lds[];
+    __shared__ float xch[4 * X::FLOATS];
+    const int ns = G.chk < G.nb ? G.chk : G.nb;
+    int8_t *sxq = reinterpret_cast<int8_t *>(kq_lds);
+    float *sxd = reinterpret_cast<float *>(kq_lds + (size_t)ns * NC * KQ_XS);
+    uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)ns * NCP);
+    kq_lh_run<T, NC, PF, HAS45, HAS6, IS>(G, G.seg[0], (int)blockIdx.x, sxq, sxd, sxm, xch);
+}
+
 constexpr int KQ_LDS_MAX = 160 * 1024 - 512; // a CU's LDS, less a margin
 // Prefetch depth in rounds. Deeper rings cost a wave per SIMD, and measured slower even where every tile has a
 // resident wave (the down projections: 4 rounds 3-9% slower than 2).
@@ -885,9 +1303,10 @@ inline int kq_capacity(const void *fn, size_t lds) {
 // barrier between chunks). Measured on the 5120-row matrices with K = 17408 (N = 4, 1280 tiles, 320 work-groups):
 // a 76 KB budget (chunks of 48 super-blocks, one re-staging) 24.6 / 28.3 us for Q4_K / Q6_K, a 52 KB one (three
 // work-groups per CU, chunks of 32) 25.1 / 29.4 us.
-inline int kq_pick_chunk(int nb, int nc, bool has45, bool has6, int ksw, int pf) {
-    const size_t budget = (size_t)76 * 1024;
-    const size_t x = kq_xch_bytes_rt(nc, ksw), per = kq_sb_lds_bytes(nc, has45, has6);
+inline int kq_pick_chunk(int nb, int nc, bool has45, bool has6, int ksw, int pf, size_t budget = (size_t)76 * 1024,
+                         size_t x = 0) {
+    if (x == 0) x = kq_xch_bytes_rt(nc, ksw);
+    const size_t per = kq_sb_lds_bytes(nc, has45, has6);
     if (x + per * nb <= budget) return nb;
     const int unit = ksw * pf;
     const int c = (int)((budget - x) / per) / unit * unit;
@@ -982,6 +1401,47 @@ int launch_wave_pf(KqGroup G, const KqPlan &P, hipStream_t stream) {
     return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_wave launch");
 }
 
+// Lane-half launches (kq_lh_kernel): one K-quant matrix of at most KQ_LH_MAX_ROWS rows, N <= 4. One tile per wave
+// pair, two pairs per work-group; the staging budget leaves room for three work-groups per CU, so the 5120-row
+// matrices (640 work-groups) are resident in one pass.
+constexpr int KQ_LH_MAX_ROWS = 8192;
+constexpr size_t KQ_LH_BUDGET = (size_t)52 * 1024;
+constexpr int KQ_LH_PF = 2; // weight ring depth in rounds
+inline bool kq_use_lh(const KqGroup &G, size_t ncols) {
+    return G.nseg == 1 && is_kquant(G.seg[0].type) && G.seg[0].rows <= KQ_LH_MAX_ROWS && G.nb >= 4 && ncols <= 4;
+}
+template <int T, int NC, bool IS = false>
+int launch_lh(KqGroup G, hipStream_t stream) {
+    constexpr bool HAS6 = T == AQ_TYPE_Q6_K, HAS45 = !HAS6;
+    constexpr size_t xch = (size_t)4 * KqXch<kq_lh_nch<T, NC>(), 4>::FLOATS * 4;
+    G.chk = kq_pick_chunk(G.nb, NC, HAS45, HAS6, 4, KQ_LH_PF, KQ_LH_BUDGET, xch);
+    const size_t lds = kq_sb_lds_bytes(NC, HAS45, HAS6) * (size_t)(G.chk < G.nb ? G.chk : G.nb);
+    AQ_REQUIRE(lds + xch <= (size_t)KQ_LDS_MAX, "kq_mfma: activation staging exceeds LDS");
+    if (lds > 64 * 1024) {
+        static bool raised = false; // once per instantiation: allow dynamic LDS up to the CU's size
+        if (!raised) {
+            AQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&kq_lh_kernel<T, NC, KQ_LH_PF, IS>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)(KQ_LDS_MAX - xch)));
+            raised = true;
+        }
+    }
+    const long tiles = (G.seg[0].rows + 3) / 4, nwg = (tiles + 1) / 2;
+    G.seg[0].nwg = (int)nwg;
+    G.seg[0].wg_end = (int)nwg;
+    hipLaunchKernelGGL((kq_lh_kernel<T, NC, KQ_LH_PF, IS>), dim3((unsigned)nwg), dim3(256), lds, stream, G);
+    return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_lh launch");
+}
+template <int T>
+int launch_lh_t(const KqGroup &G, size_t ncols, hipStream_t stream) {
+    switch (ncols) {
+    case 1: return launch_lh<T, 1>(G, stream);
+    case 2: return launch_lh<T, 2>(G, stream);
+    case 3: return launch_lh<T, 3>(G, stream);
+    case 4: return launch_lh<T, 4>(G, stream);
+    default: return fail(AQ_EINVAL, "kq_lh: ncols must be 1..4");
+    }
+}
+
 template <int T0, int T1, int NC, int KSW>
 int launch_wave_ks(const KqGroup &G, hipStream_t stream) {
     KqPlan P;
@@ -1038,6 +1498,9 @@ int launch_run_t(const Weight *const *ws, float *const *ys, const float *const *
         sg.type = w.type;
         if (w.type != AQ_TYPE_F32) rows += (int)w.rows;
     }
+    if constexpr (T0 == T1) {
+        if (kq_use_lh(G, ncols)) return launch_lh_t<T0>(G, ncols, stream);
+    }
     return launch_wave_t<T0, T1>(G, rows, ncols, stream);
 }
 
@@ -1073,6 +1536,9 @@ int launch_isums_nc(const Weight &w, const Act &x, float *y, int32_t *lanes, int
     sg.resid = nullptr;
     sg.rows = (int)w.rows;
     sg.type = w.type;
+    if constexpr (NC <= 4) {
+        if (kq_use_lh(G, NC)) return launch_lh<T, NC, true>(G, stream);
+    }
     if (kq_pick_ksw(G.nb, sg.rows) == 2) return launch_isums_ks<T, NC, 2>(G, stream);
     return launch_isums_ks<T, NC, 4>(G, stream);
 }
