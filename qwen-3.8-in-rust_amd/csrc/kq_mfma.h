@@ -530,12 +530,17 @@ __device__ __forceinline__ void kq_stage_store(const KqStageRegs<HAS45, HAS6> &R
 
 // The exchange slot of one wave: KSW blocks (one per K slice) of NCH chains x NI chain owners, the block stride
 // padded to NI modulo 64 floats so both the writes (by slice) and the owners' reads hit distinct banks.
-template <int NCH, int KSW>
+// With XP (chains handed over by register transposes, xpose4) the slot holds only the final chains [chain][owner].
+template <int NCH, int KSW, bool XP = false>
 struct KqXch {
     static constexpr int NI = 64 / KSW;
     static constexpr int S = NCH * NI + (((NI - NCH * NI) % 64) + 64) % 64;
-    static constexpr int FLOATS = KSW > 1 ? KSW * S : 1;
+    static constexpr int FLOATS = XP ? NCH * NI : (KSW > 1 ? KSW * S : 1);
 };
+// the chains of a kernel instance go through register transposes: four K slices and whole groups of four chains
+// (3 * NC and 2 * NC for NC a multiple of 4)
+template <int NC, int KSW>
+constexpr bool kq_xp() { return KSW == 4 && NC % 4 == 0; }
 
 template <int NC>
 constexpr int kq_nch_max() { return 3 * NC; }
@@ -556,7 +561,7 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
     constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), POFF = Q6 && HAS45 ? 4 : 0;
     constexpr int NCH = (Q6 ? 2 : 3) * NC;              // f32 chains of one (row, lane pair): j, j+4, min j
     constexpr int NO = (NCH + KSW - 1) / KSW;           // chains this thread keeps
-    using X = KqXch<3 * NC, KSW>;                       // slot sized for the largest NCH of the kernel
+    using X = KqXch<3 * NC, KSW, kq_xp<NC, KSW>()>;     // slot sized for the largest NCH of the kernel
     constexpr int NI = X::NI;
     MfArgs a{};
     a.qa = sg.qa;
@@ -566,7 +571,8 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
     a.rows = sg.rows;
     a.nb = G.nb;
     const int nb = G.nb;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); // uniform: the tile bookkeeping is scalar
     const int b = lane >> 2, r = lane & 3, j = b & 3, q = b >> 2;
     const int rg = q / KSW, ks = q % KSW;
     const int idx = (rg * 4 + j) * 4 + r; // chain owner index within the wave (0..NI-1)
@@ -854,7 +860,7 @@ kq_wave_kernel(KqGroup G) {
     constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
     constexpr bool HAS45 = T0 != AQ_TYPE_Q6_K || T1 != AQ_TYPE_Q6_K;
     constexpr int NCP = (NC + 3) / 4 * 4;
-    using X = KqXch<3 * NC, KSW>;
+    using X = KqXch<3 * NC, KSW, kq_xp<NC, KSW>()>;
     extern __shared__ __align__(16) uint8_t kq_lds[];
     __shared__ float xch[4 * X::FLOATS];
     int si = 0; // this work-group's segment (uniform)
@@ -1070,7 +1076,7 @@ __device__ __forceinline__ void kq_lh_run(const KqGroup &G, const KqSeg &sg, int
     constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), POFF = Q6 && HAS45 ? 4 : 0;
     constexpr int NCH = kq_lh_nch<TYPE, NC>();
     constexpr int NO = (NCH + KSW - 1) / KSW;
-    using X = KqXch<NCH, KSW>;
+    using X = KqXch<NCH, KSW, NC % 4 == 0>;
     MfArgs a{};
     a.qa = sg.qa;
     a.qb = sg.qb;
@@ -1246,7 +1252,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NC <= 
 kq_lh_kernel(KqGroup G) {
     constexpr bool HAS6 = T == AQ_TYPE_Q6_K, HAS45 = !HAS6;
     constexpr int NCP = (NC + 3) / 4 * 4;
-    using X = KqXch<kq_lh_nch<T, NC>(), 4>;
+    using X = KqXch<kq_lh_nch<T, NC>(), 4, NC % 4 == 0>;
     extern __shared__ __align__(16) uint8_t kq_lds[];
     __shared__ float xch[4 * X::FLOATS];
     const int ns = G.chk < G.nb ? G.chk : G.nb;
@@ -1262,11 +1268,12 @@ constexpr int KQ_LDS_MAX = 160 * 1024 - 512; // a CU's LDS, less a margin
 constexpr int KQ_PF = 2;
 
 template <int NC, int KSW>
-constexpr size_t kq_xch_bytes() { return (size_t)4 * KqXch<3 * NC, KSW>::FLOATS * 4; }
+constexpr size_t kq_xch_bytes() { return (size_t)4 * KqXch<3 * NC, KSW, kq_xp<NC, KSW>()>::FLOATS * 4; }
 
 // Host mirror of the kernel's LDS use: the four waves' exchange slots, and the staging per super-block.
 inline size_t kq_xch_bytes_rt(int nc, int ksw) {
     if (ksw == 1) return 4 * 4;
+    if (ksw == 4 && nc % 4 == 0) return (size_t)4 * 3 * nc * 16 * 4; // final chains only (register transposes)
     const int nch = 3 * nc, ni = 64 / ksw;
     const int s = nch * ni + (((ni - nch * ni) % 64) + 64) % 64;
     return (size_t)4 * ksw * s * 4;
@@ -1408,12 +1415,12 @@ constexpr int KQ_LH_MAX_ROWS = 8192;
 constexpr size_t KQ_LH_BUDGET = (size_t)52 * 1024;
 constexpr int KQ_LH_PF = 2; // weight ring depth in rounds
 inline bool kq_use_lh(const KqGroup &G, size_t ncols) {
-    return G.nseg == 1 && is_kquant(G.seg[0].type) && G.seg[0].rows <= KQ_LH_MAX_ROWS && G.nb >= 4 && ncols <= 4;
+    return G.nseg == 1 && is_kquant(G.seg[0].type) && G.seg[0].rows <= KQ_LH_MAX_ROWS && G.nb >= 4 && ncols <= 8;
 }
 template <int T, int NC, bool IS = false>
 int launch_lh(KqGroup G, hipStream_t stream) {
     constexpr bool HAS6 = T == AQ_TYPE_Q6_K, HAS45 = !HAS6;
-    constexpr size_t xch = (size_t)4 * KqXch<kq_lh_nch<T, NC>(), 4>::FLOATS * 4;
+    constexpr size_t xch = (size_t)4 * KqXch<kq_lh_nch<T, NC>(), 4, NC % 4 == 0>::FLOATS * 4;
     G.chk = kq_pick_chunk(G.nb, NC, HAS45, HAS6, 4, KQ_LH_PF, KQ_LH_BUDGET, xch);
     const size_t lds = kq_sb_lds_bytes(NC, HAS45, HAS6) * (size_t)(G.chk < G.nb ? G.chk : G.nb);
     AQ_REQUIRE(lds + xch <= (size_t)KQ_LDS_MAX, "kq_mfma: activation staging exceeds LDS");
@@ -1438,7 +1445,11 @@ int launch_lh_t(const KqGroup &G, size_t ncols, hipStream_t stream) {
     case 2: return launch_lh<T, 2>(G, stream);
     case 3: return launch_lh<T, 3>(G, stream);
     case 4: return launch_lh<T, 4>(G, stream);
-    default: return fail(AQ_EINVAL, "kq_lh: ncols must be 1..4");
+    case 5: return launch_lh<T, 5>(G, stream);
+    case 6: return launch_lh<T, 6>(G, stream);
+    case 7: return launch_lh<T, 7>(G, stream);
+    case 8: return launch_lh<T, 8>(G, stream);
+    default: return fail(AQ_EINVAL, "kq_lh: ncols must be 1..8");
     }
 }
 
@@ -1536,9 +1547,7 @@ int launch_isums_nc(const Weight &w, const Act &x, float *y, int32_t *lanes, int
     sg.resid = nullptr;
     sg.rows = (int)w.rows;
     sg.type = w.type;
-    if constexpr (NC <= 4) {
-        if (kq_use_lh(G, NC)) return launch_lh<T, NC, true>(G, stream);
-    }
+    if (kq_use_lh(G, NC)) return launch_lh<T, NC, true>(G, stream);
     if (kq_pick_ksw(G.nb, sg.rows) == 2) return launch_isums_ks<T, NC, 2>(G, stream);
     return launch_isums_ks<T, NC, 4>(G, stream);
 }
