@@ -123,10 +123,8 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
 #pragma unroll
     for (int r = 0; r < RN_ROUNDS; r++) {
         const int i4 = tid + r * RN_THREADS;
-        if (i4 < n4) {
-            xv[r] = x4[i4];
-            wv[r] = w4[i4];
-        }
+        if (i4 < n4) xv[r] = x4[i4];
+        if (i4 >= o0 && i4 < o1) wv[r] = w4[i4]; // the norm weights of this work-group's slice only
     }
 #pragma unroll
     for (int r = 0; r < RN_ROUNDS; r++) {
