@@ -537,10 +537,10 @@ struct KqXch {
     static constexpr int S = NCH * NI + (((NI - NCH * NI) % 64) + 64) % 64;
     static constexpr int FLOATS = XP ? NCH * NI : (KSW > 1 ? KSW * S : 1);
 };
-// the chains of a kernel instance go through register transposes: four K slices and whole groups of four chains
-// (3 * NC and 2 * NC for NC a multiple of 4)
+// the chains of a kernel instance go through register transposes: four K slices (the chains in groups of four, the
+// last group padded with zeros)
 template <int NC, int KSW>
-constexpr bool kq_xp() { return KSW == 4 && NC % 4 == 0; }
+constexpr bool kq_xp() { return KSW == 4; }
 
 template <int NC>
 constexpr int kq_nch_max() { return 3 * NC; }
@@ -704,14 +704,14 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
             __builtin_amdgcn_sched_barrier(0);
         }
         const int live = nb - crd * KSW < KSW ? nb - crd * KSW : KSW; // super-blocks in this round (uniform)
-        if constexpr (KSW == 4 && NCH % 4 == 0) {
-            // chains in groups of four by register transposes: the owner of chain 4m + ks (K slice ks) then holds
-            // its four products in super-block order
+        if constexpr (KSW == 4) {
+            // chains in groups of four by register transposes (the last group padded with zeros): the owner of
+            // chain 4m + ks (K slice ks) then holds its four products in super-block order
 #pragma unroll
-            for (int m = 0; m < NCH / 4; m++) {
+            for (int m = 0; m < (NCH + 3) / 4; m++) {
                 float q[4];
 #pragma unroll
-                for (int u = 0; u < 4; u++) q[u] = pr[(4 * m + u) / NC][(4 * m + u) % NC];
+                for (int u = 0; u < 4; u++) q[u] = 4 * m + u < NCH ? pr[(4 * m + u) / NC][(4 * m + u) % NC] : 0.0f;
                 xpose4(q[0], q[1], q[2], q[3]);
                 acc[m] += q[0];
                 if (live > 1) acc[m] += q[1];
@@ -1066,7 +1066,8 @@ constexpr int kq_lh_nch() { return (TYPE == AQ_TYPE_Q6_K ? 1 : 2) * NC; }
 
 // One wave of a lane-half pair: the pair's tile is wg * 2 + wid / 2 (4 rows; past the last one the rows are clamped
 // and nothing is stored), its lane half h = wid % 2. The round structure is kq_wave_run's with KSW = 4 and one
-// tile per wave: the K slices' products reach the chain owners through the wave's LDS slot in super-block order.
+// tile per wave: the K slices' products reach the chain owners by register transposes, in super-block order; the
+// wave's LDS slot holds only the final chains.
 template <int TYPE, int NC, int PF, bool HAS45, bool HAS6, bool IS = false>
 __device__ __forceinline__ void kq_lh_run(const KqGroup &G, const KqSeg &sg, int wg, int8_t *sxq, float *sxd,
                                           uint32_t *sxm, float *xch) {
@@ -1076,7 +1077,7 @@ __device__ __forceinline__ void kq_lh_run(const KqGroup &G, const KqSeg &sg, int
     constexpr int NP = (HAS45 ? 4 : 0) + (HAS6 ? 8 : 0), POFF = Q6 && HAS45 ? 4 : 0;
     constexpr int NCH = kq_lh_nch<TYPE, NC>();
     constexpr int NO = (NCH + KSW - 1) / KSW;
-    using X = KqXch<NCH, KSW, NC % 4 == 0>;
+    using X = KqXch<NCH, KSW, true>;
     MfArgs a{};
     a.qa = sg.qa;
     a.qb = sg.qb;
@@ -1158,48 +1159,20 @@ __device__ __forceinline__ void kq_lh_run(const KqGroup &G, const KqSeg &sg, int
             __builtin_amdgcn_sched_barrier(0);
         }
         const int live = nb - crd * KSW < KSW ? nb - crd * KSW : KSW; // super-blocks in this round (uniform)
-        if constexpr (NC % 4 == 0) {
-            // chains in groups of four by register transposes (xpose4): the owner of chain 4m + ks then holds its
-            // four products in super-block order
+        // chains in groups of four by register transposes (xpose4, the last group padded with zeros): the owner of
+        // chain 4m + ks then holds its four products in super-block order
 #pragma unroll
-            for (int m = 0; m < NCH / 4; m++) {
-                if (4 * m < nch) { // uniform
-                    float q[4];
+        for (int m = 0; m < (NCH + 3) / 4; m++) {
+            if (4 * m < nch) { // uniform
+                float q[4];
 #pragma unroll
-                    for (int u = 0; u < 4; u++) q[u] = pr[(4 * m + u) / NC][(4 * m + u) % NC];
-                    xpose4(q[0], q[1], q[2], q[3]);
-                    acc[m] += q[0];
-                    if (live > 1) acc[m] += q[1];
-                    if (live > 2) acc[m] += q[2];
-                    if (live > 3) acc[m] += q[3];
-                }
+                for (int u = 0; u < 4; u++) q[u] = 4 * m + u < nch ? pr[(4 * m + u) / NC][(4 * m + u) % NC] : 0.0f;
+                xpose4(q[0], q[1], q[2], q[3]);
+                acc[m] += q[0];
+                if (live > 1) acc[m] += q[1];
+                if (live > 2) acc[m] += q[2];
+                if (live > 3) acc[m] += q[3];
             }
-        } else {
-#pragma unroll
-        for (int k = 0; k < NCH; k++)
-            if (k < nch) xw[ks * X::S + k * NI + idx] = pr[k / NC][k % NC];
-        __asm__ volatile("" ::: "memory");
-        if (live == KSW) {
-#pragma unroll
-            for (int m = 0; m < NO; m++) {
-                const int k = ks + KSW * m;
-                if (k < nch) {
-#pragma unroll
-                    for (int k2 = 0; k2 < KSW; k2++) acc[m] += xw[k2 * X::S + k * NI + idx];
-                }
-            }
-        } else {
-#pragma unroll
-            for (int m = 0; m < NO; m++) {
-                const int k = ks + KSW * m;
-                if (k < nch) {
-#pragma unroll
-                    for (int k2 = 0; k2 < KSW; k2++)
-                        if (k2 < live) acc[m] += xw[k2 * X::S + k * NI + idx];
-                }
-            }
-        }
-        __asm__ volatile("" ::: "memory");
         }
         crd++;
     };
@@ -1252,7 +1225,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NC <= 
 kq_lh_kernel(KqGroup G) {
     constexpr bool HAS6 = T == AQ_TYPE_Q6_K, HAS45 = !HAS6;
     constexpr int NCP = (NC + 3) / 4 * 4;
-    using X = KqXch<kq_lh_nch<T, NC>(), 4, NC % 4 == 0>;
+    using X = KqXch<kq_lh_nch<T, NC>(), 4, true>;
     extern __shared__ __align__(16) uint8_t kq_lds[];
     __shared__ float xch[4 * X::FLOATS];
     const int ns = G.chk < G.nb ? G.chk : G.nb;
@@ -1273,7 +1246,7 @@ constexpr size_t kq_xch_bytes() { return (size_t)4 * KqXch<3 * NC, KSW, kq_xp<NC
 // Host mirror of the kernel's LDS use: the four waves' exchange slots, and the staging per super-block.
 inline size_t kq_xch_bytes_rt(int nc, int ksw) {
     if (ksw == 1) return 4 * 4;
-    if (ksw == 4 && nc % 4 == 0) return (size_t)4 * 3 * nc * 16 * 4; // final chains only (register transposes)
+    if (ksw == 4) return (size_t)4 * 3 * nc * 16 * 4; // final chains only (register transposes)
     const int nch = 3 * nc, ni = 64 / ksw;
     const int s = nch * ni + (((ni - nch * ni) % 64) + 64) % 64;
     return (size_t)4 * ksw * s * 4;
@@ -1420,7 +1393,7 @@ inline bool kq_use_lh(const KqGroup &G, size_t ncols) {
 template <int T, int NC, bool IS = false>
 int launch_lh(KqGroup G, hipStream_t stream) {
     constexpr bool HAS6 = T == AQ_TYPE_Q6_K, HAS45 = !HAS6;
-    constexpr size_t xch = (size_t)4 * KqXch<kq_lh_nch<T, NC>(), 4, NC % 4 == 0>::FLOATS * 4;
+    constexpr size_t xch = (size_t)4 * KqXch<kq_lh_nch<T, NC>(), 4, true>::FLOATS * 4;
     G.chk = kq_pick_chunk(G.nb, NC, HAS45, HAS6, 4, KQ_LH_PF, KQ_LH_BUDGET, xch);
     const size_t lds = kq_sb_lds_bytes(NC, HAS45, HAS6) * (size_t)(G.chk < G.nb ? G.chk : G.nb);
     AQ_REQUIRE(lds + xch <= (size_t)KQ_LDS_MAX, "kq_mfma: activation staging exceeds LDS");
