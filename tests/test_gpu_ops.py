@@ -215,6 +215,36 @@ def test_matmul_full_shapes_bit_exact_and_column_identity(ctx, t, rows, cols):
         assert bits_equal(yn, y1[:n]), f"N={n} columns differ from N=1"
 
 
+@pytest.mark.parametrize("t,rows,cols", [(aq.Q4_K, 37, 1280), (aq.Q5_K, 4, 1024), (aq.Q6_K, 4099, 1536),
+                                         (aq.Q4_K, 8192, 1024), (aq.Q6_K, 6, 2304)])
+def test_lane_half_edge_shapes_bit_exact(ctx, t, rows, cols):
+    """Single K-quant matrices of at most 8192 rows take the lane-half kernel (a pair of waves per tile of 4 rows):
+    row counts that are not a multiple of 4 (the last tile's rows clamped, nothing stored past the matrix), a single
+    pair, super-block counts that leave a partial last round (5, 6, 9 of 4 per round), and every column count 1..8:
+    each output equals the oracle bit for bit, and the integer lane sums equal the reference's at N = 1 and 4."""
+    say(f"lane-half edge shape type {t} {rows}x{cols}")
+    spec = aq.synth_spec(t, rows, cols, seed=77 + rows + t, b=0.02)
+    host = aq.synth_host(spec)
+    w = aq.SynthWeight(ctx, spec)
+    x = np.random.default_rng(rows + cols).standard_normal((8, cols)).astype(np.float32)
+    a = aq.Act(ctx, cols, 8)
+    a.set(x)
+    a.quantize(t, 8)
+    want = O.matmul(t, host.view(np.uint8), rows, cols, x, threads=8)
+    for n in range(1, 9):
+        yn = aq.matmul(ctx, w, a, n)
+        bad = int(np.sum(yn.view(np.uint32) != want[:n].view(np.uint32)))
+        assert bad == 0, f"N={n}: {bad} outputs differ from the oracle"
+    for n in (1, 4):
+        lanes, mins = aq.kq_isums(ctx, w, a, n)
+        for c in range(n):
+            want_l, want_m = O.kq_isums_mat(t, host.view(np.uint8), rows, O.q8k_quantize(x[c]), cols)
+            assert np.array_equal(lanes[c], want_l), f"N={n} column {c}: lane sums differ"
+            assert np.array_equal(mins[c], want_m), f"N={n} column {c}: min products differ"
+    a.free()
+    w.free()
+
+
 _single_cache = {}
 
 
