@@ -551,7 +551,7 @@ constexpr int kq_nch_max() { return 3 * NC; }
 // through the wave's LDS slot; per tile: the lane reduction ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)) [+ (m0+m2)+(m1+m3)]
 // (kdot.rs:1-18) and the store. With chunked staging (G.chk < nb) every wave runs exactly one tile (idle ones on
 // clamped rows), because all waves of the work-group meet at the chunk barriers.
-template <int TYPE, int NC, int KSW, int PF, bool HAS45, bool HAS6, bool IS = false>
+template <int TYPE, int NC, int KSW, int PF, bool HAS45, bool HAS6, bool IS, bool FULL>
 __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, int wg, int8_t *sxq, float *sxd,
                                             uint32_t *sxm, float *xw) {
     static_assert(KSW == 2 || KSW == 4, "K slices per wave");
@@ -664,9 +664,11 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
         __asm__ volatile("" ::: "memory");
     };
 
+    // FULL: nb is a multiple of KSW, so every round's K slices are all live (a kernel of its own: the partial
+    // rounds' guards, a select per chain and slice, stay out of its loop)
     auto round_body = [&](WRegs<TYPE> &wv, const bool prefetch) {
         const int sb = crd * KSW + ks;
-        const int sbc = sb < nb ? sb : nb - 1;
+        const int sbc = FULL || sb < nb ? sb : nb - 1;
         float pr[3][NC];
 #pragma unroll
         for (int c = 0; c < NC; c++) pr[2][c] = 0.0f;
@@ -703,7 +705,8 @@ __device__ __forceinline__ void kq_wave_run(const KqGroup &G, const KqSeg &sg, i
             issue(wv);
             __builtin_amdgcn_sched_barrier(0);
         }
-        const int live = nb - crd * KSW < KSW ? nb - crd * KSW : KSW; // super-blocks in this round (uniform)
+        // super-blocks in this round (uniform)
+        const int live = FULL ? KSW : nb - crd * KSW < KSW ? nb - crd * KSW : KSW;
         if constexpr (KSW == 4) {
             // chains in groups of four by register transposes (the last group padded with zeros): the owner of
             // chain 4m + ks (K slice ks) then holds its four products in super-block order
@@ -854,7 +857,7 @@ template <int T0, int T1, int NC, int KSW, int PF>
 constexpr int kq_waves_per_eu() {
     return NC <= 4 && KSW == 4 && T0 != AQ_TYPE_Q5_K && T1 != AQ_TYPE_Q5_K ? 4 : 1;
 }
-template <int T0, int T1, int NC, int KSW, int PF, bool IS = false>
+template <int T0, int T1, int NC, int KSW, int PF, bool IS, bool FULL>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kq_waves_per_eu<T0, T1, NC, KSW, PF>())))
 kq_wave_kernel(KqGroup G) {
     constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
@@ -877,9 +880,9 @@ kq_wave_kernel(KqGroup G) {
     uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)ns * NCP);
     float *xw = xch + (threadIdx.x >> 6) * X::FLOATS;
     if (T0 == T1 || sg.type == T0)
-        kq_wave_run<T0, NC, KSW, PF, HAS45, HAS6, IS>(G, sg, wg, sxq, sxd, sxm, xw);
+        kq_wave_run<T0, NC, KSW, PF, HAS45, HAS6, IS, FULL>(G, sg, wg, sxq, sxd, sxm, xw);
     else
-        kq_wave_run<T1, NC, KSW, PF, HAS45, HAS6, IS>(G, sg, wg, sxq, sxd, sxm, xw);
+        kq_wave_run<T1, NC, KSW, PF, HAS45, HAS6, IS, FULL>(G, sg, wg, sxq, sxd, sxm, xw);
 }
 
 // ------------------------------------------------------------------------------------ the lane-half kernel
@@ -1068,7 +1071,7 @@ constexpr int kq_lh_nch() { return (TYPE == AQ_TYPE_Q6_K ? 1 : 2) * NC; }
 // and nothing is stored), its lane half h = wid % 2. The round structure is kq_wave_run's with KSW = 4 and one
 // tile per wave: the K slices' products reach the chain owners by register transposes, in super-block order; the
 // wave's LDS slot holds only the final chains.
-template <int TYPE, int NC, int PF, bool HAS45, bool HAS6, bool IS = false>
+template <int TYPE, int NC, int PF, bool HAS45, bool HAS6, bool IS, bool FULL>
 __device__ __forceinline__ void kq_lh_run(const KqGroup &G, const KqSeg &sg, int wg, int8_t *sxq, float *sxd,
                                           uint32_t *sxm, float *xch) {
     constexpr int KSW = 4, NI = 16;
@@ -1127,9 +1130,9 @@ __device__ __forceinline__ void kq_lh_run(const KqGroup &G, const KqSeg &sg, int
 #pragma unroll
     for (int i = 0; i < NO; i++) acc[i] = 0.0f;
     int crd = 0; // round
-    auto round_body = [&](WRegs<TYPE> &wv, const bool prefetch) {
+    auto round_body = [&](WRegs<TYPE> &wv, const bool prefetch) { // FULL as in kq_wave_run
         const int sb = crd * KSW + ks;
-        const int sbc = sb < nb ? sb : nb - 1;
+        const int sbc = FULL || sb < nb ? sb : nb - 1;
         float pr[2][NC];
 #pragma unroll
         for (int c = 0; c < NC; c++) pr[1][c] = 0.0f;
@@ -1158,7 +1161,8 @@ __device__ __forceinline__ void kq_lh_run(const KqGroup &G, const KqSeg &sg, int
             issue(wv);
             __builtin_amdgcn_sched_barrier(0);
         }
-        const int live = nb - crd * KSW < KSW ? nb - crd * KSW : KSW; // super-blocks in this round (uniform)
+        // super-blocks in this round (uniform)
+        const int live = FULL ? KSW : nb - crd * KSW < KSW ? nb - crd * KSW : KSW;
         // chains in groups of four by register transposes (xpose4, the last group padded with zeros): the owner of
         // chain 4m + ks then holds its four products in super-block order
 #pragma unroll
@@ -1220,7 +1224,7 @@ __device__ __forceinline__ void kq_lh_run(const KqGroup &G, const KqSeg &sg, int
     }
 }
 
-template <int T, int NC, int PF, bool IS = false>
+template <int T, int NC, int PF, bool IS, bool FULL>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NC <= 4 ? 4 : 1)))
 kq_lh_kernel(KqGroup G) {
     constexpr bool HAS6 = T == AQ_TYPE_Q6_K, HAS45 = !HAS6;
@@ -1232,7 +1236,7 @@ kq_lh_kernel(KqGroup G) {
     int8_t *sxq = reinterpret_cast<int8_t *>(kq_lds);
     float *sxd = reinterpret_cast<float *>(kq_lds + (size_t)ns * NC * KQ_XS);
     uint32_t *sxm = reinterpret_cast<uint32_t *>(sxd + (size_t)ns * NCP);
-    kq_lh_run<T, NC, PF, HAS45, HAS6, IS>(G, G.seg[0], (int)blockIdx.x, sxq, sxd, sxm, xch);
+    kq_lh_run<T, NC, PF, HAS45, HAS6, IS, FULL>(G, G.seg[0], (int)blockIdx.x, sxq, sxd, sxm, xch);
 }
 
 constexpr int KQ_LDS_MAX = 160 * 1024 - 512; // a CU's LDS, less a margin
@@ -1312,7 +1316,7 @@ struct KqPlan {
     long tiles, f32_wgs, cap;
     double bytes;
 };
-template <int T0, int T1, int NC, int KSW, int PF, bool IS = false>
+template <int T0, int T1, int NC, int KSW, int PF, bool IS, bool FULL>
 int kq_plan(const KqGroup &G, KqPlan &P) {
     constexpr int RW = 16 / KSW; // rows per tile
     constexpr bool HAS6 = T0 == AQ_TYPE_Q6_K || T1 == AQ_TYPE_Q6_K;
@@ -1321,7 +1325,7 @@ int kq_plan(const KqGroup &G, KqPlan &P) {
     P.lds = kq_sb_lds_bytes(NC, HAS45, HAS6) * (size_t)(P.chk < G.nb ? P.chk : G.nb);
     constexpr size_t xch = kq_xch_bytes<NC, KSW>();
     AQ_REQUIRE(P.lds + xch <= (size_t)KQ_LDS_MAX, "kq_mfma: activation staging exceeds LDS");
-    const void *fn = reinterpret_cast<const void *>(&kq_wave_kernel<T0, T1, NC, KSW, PF, IS>);
+    const void *fn = reinterpret_cast<const void *>(&kq_wave_kernel<T0, T1, NC, KSW, PF, IS, FULL>);
     if (P.lds > 64 * 1024) {
         static bool raised = false; // once per instantiation: allow dynamic LDS up to the CU's size
         if (!raised) {
@@ -1347,7 +1351,7 @@ int kq_plan(const KqGroup &G, KqPlan &P) {
     return 0;
 }
 
-template <int T0, int T1, int NC, int KSW, int PF, bool IS = false>
+template <int T0, int T1, int NC, int KSW, int PF, bool IS, bool FULL>
 int launch_wave_pf(KqGroup G, const KqPlan &P, hipStream_t stream) {
     constexpr int RW = 16 / KSW; // rows per tile
     G.chk = P.chk;
@@ -1377,7 +1381,8 @@ int launch_wave_pf(KqGroup G, const KqPlan &P, hipStream_t stream) {
         wgs += (int)n;
         sg.wg_end = wgs;
     }
-    hipLaunchKernelGGL((kq_wave_kernel<T0, T1, NC, KSW, PF, IS>), dim3((unsigned)wgs), dim3(256), P.lds, stream, G);
+    hipLaunchKernelGGL((kq_wave_kernel<T0, T1, NC, KSW, PF, IS, FULL>), dim3((unsigned)wgs), dim3(256), P.lds, stream,
+                       G);
     return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_wave launch");
 }
 
@@ -1390,8 +1395,8 @@ constexpr int KQ_LH_PF = 2; // weight ring depth in rounds
 inline bool kq_use_lh(const KqGroup &G, size_t ncols) {
     return G.nseg == 1 && is_kquant(G.seg[0].type) && G.seg[0].rows <= KQ_LH_MAX_ROWS && G.nb >= 4 && ncols <= 8;
 }
-template <int T, int NC, bool IS = false>
-int launch_lh(KqGroup G, hipStream_t stream) {
+template <int T, int NC, bool IS, bool FULL>
+int launch_lh_f(KqGroup G, hipStream_t stream) {
     constexpr bool HAS6 = T == AQ_TYPE_Q6_K, HAS45 = !HAS6;
     constexpr size_t xch = (size_t)4 * KqXch<kq_lh_nch<T, NC>(), 4, true>::FLOATS * 4;
     G.chk = kq_pick_chunk(G.nb, NC, HAS45, HAS6, 4, KQ_LH_PF, KQ_LH_BUDGET, xch);
@@ -1400,7 +1405,7 @@ int launch_lh(KqGroup G, hipStream_t stream) {
     if (lds > 64 * 1024) {
         static bool raised = false; // once per instantiation: allow dynamic LDS up to the CU's size
         if (!raised) {
-            AQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&kq_lh_kernel<T, NC, KQ_LH_PF, IS>),
+            AQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&kq_lh_kernel<T, NC, KQ_LH_PF, IS, FULL>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)(KQ_LDS_MAX - xch)));
             raised = true;
         }
@@ -1408,8 +1413,13 @@ int launch_lh(KqGroup G, hipStream_t stream) {
     const long tiles = (G.seg[0].rows + 3) / 4, nwg = (tiles + 1) / 2;
     G.seg[0].nwg = (int)nwg;
     G.seg[0].wg_end = (int)nwg;
-    hipLaunchKernelGGL((kq_lh_kernel<T, NC, KQ_LH_PF, IS>), dim3((unsigned)nwg), dim3(256), lds, stream, G);
+    hipLaunchKernelGGL((kq_lh_kernel<T, NC, KQ_LH_PF, IS, FULL>), dim3((unsigned)nwg), dim3(256), lds, stream, G);
     return hipGetLastError() == hipSuccess ? 0 : fail(AQ_EHIP, "kq_lh launch");
+}
+// K in whole rounds (nb a multiple of 4: every K of the 27B shape) takes the kernel without partial-round guards
+template <int T, int NC, bool IS = false>
+int launch_lh(const KqGroup &G, hipStream_t stream) {
+    return G.nb % 4 == 0 ? launch_lh_f<T, NC, IS, true>(G, stream) : launch_lh_f<T, NC, IS, false>(G, stream);
 }
 template <int T>
 int launch_lh_t(const KqGroup &G, size_t ncols, hipStream_t stream) {
@@ -1426,12 +1436,18 @@ int launch_lh_t(const KqGroup &G, size_t ncols, hipStream_t stream) {
     }
 }
 
-template <int T0, int T1, int NC, int KSW>
-int launch_wave_ks(const KqGroup &G, hipStream_t stream) {
+template <int T0, int T1, int NC, int KSW, bool IS, bool FULL>
+int launch_wave_ksf(const KqGroup &G, hipStream_t stream) {
     KqPlan P;
-    const int rc = kq_plan<T0, T1, NC, KSW, KQ_PF>(G, P);
+    const int rc = kq_plan<T0, T1, NC, KSW, KQ_PF, IS, FULL>(G, P);
     if (rc) return rc;
-    return launch_wave_pf<T0, T1, NC, KSW, KQ_PF>(G, P, stream);
+    return launch_wave_pf<T0, T1, NC, KSW, KQ_PF, IS, FULL>(G, P, stream);
+}
+// K in whole rounds (nb a multiple of KSW) takes the kernel without partial-round guards
+template <int T0, int T1, int NC, int KSW, bool IS = false>
+int launch_wave_ks(const KqGroup &G, hipStream_t stream) {
+    return G.nb % KSW == 0 ? launch_wave_ksf<T0, T1, NC, KSW, IS, true>(G, stream)
+                           : launch_wave_ksf<T0, T1, NC, KSW, IS, false>(G, stream);
 }
 
 template <int T0, int T1, int NC>
@@ -1490,13 +1506,6 @@ int launch_run_t(const Weight *const *ws, float *const *ys, const float *const *
 
 // The integer check: the production grid and kernel of one K-quant matrix of type T (the K slices the production
 // launch would pick), with the integer outputs on; y receives the usual f32 outputs.
-template <int T, int NC, int KSW>
-int launch_isums_ks(KqGroup G, hipStream_t stream) {
-    KqPlan P;
-    const int rc = kq_plan<T, T, NC, KSW, KQ_PF, true>(G, P);
-    if (rc) return rc;
-    return launch_wave_pf<T, T, NC, KSW, KQ_PF, true>(G, P, stream);
-}
 
 template <int T, int NC>
 int launch_isums_nc(const Weight &w, const Act &x, float *y, int32_t *lanes, int32_t *mins, hipStream_t stream) {
@@ -1521,8 +1530,8 @@ int launch_isums_nc(const Weight &w, const Act &x, float *y, int32_t *lanes, int
     sg.rows = (int)w.rows;
     sg.type = w.type;
     if (kq_use_lh(G, NC)) return launch_lh<T, NC, true>(G, stream);
-    if (kq_pick_ksw(G.nb, sg.rows) == 2) return launch_isums_ks<T, NC, 2>(G, stream);
-    return launch_isums_ks<T, NC, 4>(G, stream);
+    if (kq_pick_ksw(G.nb, sg.rows) == 2) return launch_wave_ks<T, T, NC, 2, true>(G, stream);
+    return launch_wave_ks<T, T, NC, 4, true>(G, stream);
 }
 
 template <int T>
