@@ -67,6 +67,13 @@ typedef short s16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ int sdot2(uint32_t a, uint32_t b) {
     return __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b), 0, false);
 }
+// the same with the zero addend as the instruction's inline constant (the builtin's two-operand form takes an extra
+// register move to clear its accumulator)
+__device__ __forceinline__ int sdot2z(uint32_t a, uint32_t b) {
+    int r;
+    __asm__("v_dot2_i32_i16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 
 // A 4 x 4 transpose of 16-lane rows across four registers: on entry row q (lanes 16q..16q+15) of p_k holds chain k's
 // value for K slice q; on exit row q of p_m holds chain q's value for K slice m. Two v_permlane16_swap (odd rows of
@@ -358,7 +365,7 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
                     s1 = (s1 << DB) + a1[i][c];
                 }
                 const float dd = dxs[c] * dw;
-                const int im = sdot2(mnp, mw0[c]); // mn0 * lo0 + mn1 * hi0, exact
+                const int im = sdot2z(mnp, mw0[c]); // mn0 * lo0 + mn1 * hi0, exact
                 pr0[col] = dd * (float)s0;
                 pr1[col] = dd * (float)s1;
                 pm[col] = (-dxs[c] * dminw) * (float)im;
@@ -1046,16 +1053,29 @@ __device__ __forceinline__ void sb_half_products(const WRegs<TYPE> &wv, const in
                     const float dd = dxs[c] * dw;
                     pr[col] = dd * (float)s0;
                     if constexpr (IS) is[col] = s0;
-                    // the min lane only in the h = 1 wave (uniform); one unconditional store of the result keeps
-                    // pm in registers
-                    float pv = 0.0f;
-                    int iv = 0;
-                    if (mins) {
-                        iv = sdot2(mnp, mw0[c]);
-                        pv = (-dxs[c] * dminw) * (float)iv;
+                }
+            }
+            // the min lanes only in the h = 1 wave: one uniform branch over the group's columns (the empty asm keeps
+            // the compiler from computing them in both waves and selecting), then one unconditional store of each
+            // result, which keeps pm in registers
+            float pv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            int iv[4] = {0, 0, 0, 0};
+            if (mins) {
+                __asm__ volatile("");
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    if (cg * 4 + c < NC) {
+                        iv[c] = sdot2z(mnp, mw0[c]);
+                        pv[c] = (-dxs[c] * dminw) * (float)iv[c];
                     }
-                    pm[col] = pv;
-                    if constexpr (IS) ism[col] = iv;
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int col = cg * 4 + c;
+                if (col < NC) {
+                    pm[col] = pv[c];
+                    if constexpr (IS) ism[col] = iv[c];
                 }
             }
         }
