@@ -263,6 +263,25 @@ __device__ __forceinline__ void sb_products(const WRegs<TYPE> &wv, const int8_t 
     }
 }
 
+// The DB-bit digits of the 8 six-bit sub-block scales (the bytes of sc_lo, sc_hi) as 16-bit pairs: the halves of
+// dig[i][p] are digit i of scales 2p and 2p + 1. The digits are split byte-parallel (one shift and mask per digit
+// and word), then one byte permute per pair; the words are opaque to the compiler, so a half reaches both halves of
+// the code multiply through its operand select rather than a re-derived shift.
+template <int DB, int ND>
+__device__ __forceinline__ void kq_digits(uint32_t sc_lo, uint32_t sc_hi, uint32_t (&dig)[ND][4]) {
+    constexpr uint32_t BM = ((1u << DB) - 1u) * 0x01010101u;
+#pragma unroll
+    for (int i = 0; i < ND; i++) {
+        const uint32_t dlo = (sc_lo >> (DB * i)) & BM, dhi = (sc_hi >> (DB * i)) & BM;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t b0 = (uint32_t)(2 * (p & 1));
+            dig[i][p] = __builtin_amdgcn_perm(0u, p < 2 ? dlo : dhi, b0 | 0x0C00u | ((b0 + 1u) << 16) | 0x0C000000u);
+            __asm__("" : "+v"(dig[i][p]));
+        }
+    }
+}
+
 // Q4_K / Q5_K products with the sub-block scale inside the matrix-core operand. A 6-bit scale sc is split into
 // digits of DB bits (sc = sum_i digit_i << (DB*i); DB = 3 for Q4_K codes <= 15, DB = 2 for Q5_K codes <= 31), so
 // code * digit <= 105 (resp. 93) is an int8: one 32-bit multiply scales the 4 packed code bytes of a sub-block
@@ -277,7 +296,6 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
     constexpr int NCG = (NC + 3) / 4;
     constexpr int DB = TYPE == AQ_TYPE_Q4_K ? 3 : 2;   // digit bits
     constexpr int ND = TYPE == AQ_TYPE_Q4_K ? 2 : 3;   // digits of a 6-bit scale
-    constexpr uint32_t DM = (1u << DB) - 1u;
     // up to four columns: the activation reads go out first, so their LDS latency passes under the unpacking (the
     // same in the Q6_K path costs 25 registers: three waves per SIMD instead of four)
     uint4 xh[4];
@@ -302,13 +320,7 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
     // digit pair words: the 16-bit halves of dig[i][p] are digit i of sc[2p] and sc[2p + 1]; a packed multiply
     // broadcasts one half to both halves of the code word (op_sel), so no per-sub-block byte shuffle is needed
     uint32_t dig[ND][4];
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-        const uint32_t src = p < 2 ? sc_lo : sc_hi, b0 = (uint32_t)(2 * (p & 1));
-        const uint32_t pw = __builtin_amdgcn_perm(0u, src, b0 | 0x0C00u | ((b0 + 1u) << 16) | 0x0C000000u);
-#pragma unroll
-        for (int i = 0; i < ND; i++) dig[i][p] = (pw >> (DB * i)) & (DM * 0x00010001u);
-    }
+    kq_digits<DB, ND>(sc_lo, sc_hi, dig);
     uint32_t code0[8], code1[8];
     const uint32_t w0[4] = {wv.qa0.x, wv.qa0.y, wv.qa0.z, wv.qa0.w};
     const uint32_t w1[4] = {wv.qa1.x, wv.qa1.y, wv.qa1.z, wv.qa1.w};
@@ -984,7 +996,6 @@ __device__ __forceinline__ void sb_half_products(const WRegs<TYPE> &wv, const in
         }
     } else {
         constexpr int DB = TYPE == AQ_TYPE_Q4_K ? 3 : 2, ND = TYPE == AQ_TYPE_Q4_K ? 2 : 3;
-        constexpr uint32_t DM = (1u << DB) - 1u;
         uint4 xh[2];
         float4 dxh;
         uint4 mh;
@@ -1004,13 +1015,7 @@ __device__ __forceinline__ void sb_half_products(const WRegs<TYPE> &wv, const in
         const uint32_t mnp = __builtin_amdgcn_perm(0u, mnw, (uint32_t)(2 * (j & 1)) | 0x0C00u |
                                                               ((uint32_t)(2 * (j & 1) + 1) << 16) | 0x0C000000u);
         uint32_t dig[ND][4];
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const uint32_t src = p < 2 ? sc_lo : sc_hi, b0 = (uint32_t)(2 * (p & 1));
-            const uint32_t pw = __builtin_amdgcn_perm(0u, src, b0 | 0x0C00u | ((b0 + 1u) << 16) | 0x0C000000u);
-#pragma unroll
-            for (int i = 0; i < ND; i++) dig[i][p] = (pw >> (DB * i)) & (DM * 0x00010001u);
-        }
+        kq_digits<DB, ND>(sc_lo, sc_hi, dig);
         uint32_t code[8];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
