@@ -818,25 +818,32 @@ __global__ void __launch_bounds__(256) attn_core_kernel(AttnArgs a) {
         const float *vc = a.vcache + (size_t)kvh * hd + d;
         float acc = 0.0f;
         // 16 positions' loads in flight while the previous 16 are summed (double buffer); the sum stays
-        // sequential in tt
+        // sequential in tt. The last batch may be partial: its loads are clamped to the last position (all issued
+        // together, like a full batch's) and only the positions before len are added.
         constexpr int VB = 16;
-        const size_t ng = len / VB;
+        const size_t ng = (len + VB - 1) / VB;
         float va[VB], vb[VB];
-        if (ng > 0) {
+        auto vload = [&](float *buf, size_t g) {
 #pragma unroll
-            for (int u = 0; u < VB; u++) va[u] = vc[(size_t)u * a.stride];
-        }
-        for (size_t g = 0; g < ng; g++) {
-            if (g + 1 < ng) {
-#pragma unroll
-                for (int u = 0; u < VB; u++) vb[u] = vc[((g + 1) * VB + u) * a.stride];
+            for (int u = 0; u < VB; u++) {
+                const size_t tt = g * VB + u;
+                buf[u] = vc[(tt < len ? tt : len - 1) * a.stride];
             }
+        };
+        vload(va, 0);
+        for (size_t g = 0; g < ng; g++) {
+            if (g + 1 < ng) vload(vb, g + 1);
+            if ((g + 1) * VB <= len) {
 #pragma unroll
-            for (int u = 0; u < VB; u++) acc += sc[g * VB + u] * va[u];
+                for (int u = 0; u < VB; u++) acc += sc[g * VB + u] * va[u];
+            } else {
+#pragma unroll
+                for (int u = 0; u < VB; u++)
+                    if (g * VB + u < len) acc += sc[g * VB + u] * va[u];
+            }
 #pragma unroll
             for (int u = 0; u < VB; u++) va[u] = vb[u];
         }
-        for (size_t tt = ng * VB; tt < len; tt++) acc += sc[tt] * vc[tt * a.stride];
         const float gate = a.qg[(size_t)i * 2 * a.nh * hd + (size_t)h * 2 * hd + hd + d];
         const float o = acc * sigmoid_f(gate);
         a.out[(size_t)i * a.nh * hd + (size_t)h * hd + d] = o;
