@@ -399,10 +399,11 @@ __device__ __forceinline__ void sb_products_split(const WRegs<TYPE> &wv, const i
 // The 16 matrix-core blocks of a wave are (q, j): j = the lane pair (j, j+4), q = (row group rg, K slice ks) with
 // KSW K slices per wave (2 or 4) and 4 / KSW row groups of 4 rows: a wave owns 16 / KSW rows and in round rd its
 // K slice ks computes super-block rd * KSW + ks. Matrices split K four ways inside the wave, so a wave covers 4 rows
-// and the grid holds enough waves even for the 5120-row ones; K below 4 super-blocks and the lm_head take two
-// slices (kq_pick_ksw). The f32 chains stay the reference's sequential sums: each round the K slices hand their
-// products to the chain owners through the wave's own LDS slot (no work-group barrier; one wave's LDS accesses
-// execute in order), and the owner of a chain adds the KSW products in super-block order.
+// and the grid holds enough waves even for the 5120-row ones; K below 4 super-blocks and the lm_head at N > 1 take
+// two slices (kq_pick_ksw). The f32 chains stay the reference's sequential sums: each round the K slices hand their
+// products to the chain owners — by register transposes with four slices, through the wave's own LDS slot with two
+// (no work-group barrier; one wave's LDS accesses execute in order) — and the owner of a chain adds the KSW products
+// in super-block order.
 //
 // One launch can cover up to three matrices that read the same activations (gate and up; q, k and v; the
 // DeltaNet qkv and z projections): the work-groups are laid out segment after segment, each segment with its own
@@ -1286,11 +1287,13 @@ inline size_t kq_sb_lds_bytes(int nc, bool has45, bool has6) {
 }
 
 // K slices per wave: four (tiles of 4 rows, so work divides finely over the waves), two for K below 4 super-blocks
-// and for the lm_head-sized matrices (at least KQ_TALL_ROWS rows: tiles of 8 rows, a long stream either way).
-// Measured (MI355X, Q6_K 248320 x 5120): N = 1 188 vs 198 us, N = 4 234 vs 247 us with two slices; every shorter
-// matrix is slower with two (Q4_K 10240 x 5120 N = 4 13.3 vs 10.5 us, Q6_K 5120 x 17408 34.1 vs 28.1 us).
+// and for the lm_head-sized matrices (at least KQ_TALL_ROWS rows: tiles of 8 rows, a long stream either way) at more
+// than one column. Measured (MI355X, Q6_K 248320 x 5120, the current kernels): N = 4 199-201 us with two slices
+// against 202-207 with four; N = 1 176.3 against 172.9 us (four passes of 400 launches each, alternated), so the
+// matvec takes four. Every shorter matrix is slower with two (Q4_K 10240 x 5120 N = 4 13.3 vs 10.5 us, Q6_K
+// 5120 x 17408 34.1 vs 28.1 us, an earlier build).
 constexpr int KQ_TALL_ROWS = 131072;
-inline int kq_pick_ksw(int nb, int rows) { return nb < 4 || rows >= KQ_TALL_ROWS ? 2 : 4; }
+inline int kq_pick_ksw(int nb, int rows, size_t ncols) { return nb < 4 || (rows >= KQ_TALL_ROWS && ncols > 1) ? 2 : 4; }
 
 // Work-groups of `fn` (256 threads, `lds` dynamic bytes) resident on the whole device at once.
 inline int kq_capacity(const void *fn, size_t lds) {
@@ -1477,7 +1480,7 @@ int launch_wave_ks(const KqGroup &G, hipStream_t stream) {
 
 template <int T0, int T1, int NC>
 int launch_wave_nc(const KqGroup &G, int rows, hipStream_t stream) {
-    if (kq_pick_ksw(G.nb, rows) == 2) return launch_wave_ks<T0, T1, NC, 2>(G, stream);
+    if (kq_pick_ksw(G.nb, rows, NC) == 2) return launch_wave_ks<T0, T1, NC, 2>(G, stream);
     return launch_wave_ks<T0, T1, NC, 4>(G, stream);
 }
 
@@ -1555,7 +1558,7 @@ int launch_isums_nc(const Weight &w, const Act &x, float *y, int32_t *lanes, int
     sg.rows = (int)w.rows;
     sg.type = w.type;
     if (kq_use_lh(G, NC)) return launch_lh<T, NC, true>(G, stream);
-    if (kq_pick_ksw(G.nb, sg.rows) == 2) return launch_wave_ks<T, T, NC, 2, true>(G, stream);
+    if (kq_pick_ksw(G.nb, sg.rows, NC) == 2) return launch_wave_ks<T, T, NC, 2, true>(G, stream);
     return launch_wave_ks<T, T, NC, 4, true>(G, stream);
 }
 
