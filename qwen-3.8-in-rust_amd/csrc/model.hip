@@ -604,8 +604,40 @@ Needs mlp_needs(const DevLayer &L) {
 // the recurrent state and conv window are read, not written, and the qkv / alpha / beta rows are kept in the
 // layer's slot for the commit; in PLAIN mode the new conv window goes to the other buffer (the caller flips the
 // parity once per pass).
+// Whether a DeltaNet layer's ssm_alpha / ssm_beta rows come from its attn_norm launch (launch_rmsnorm_rows), so the
+// grouped qkv / z launch carries K-quant tiles only: decode and verify batches, both gates F32 over whole 256-blocks
+// and the K-quant pair grouped (not under the q8-fine switch).
+bool dn_gates_in_norm(const aq_state *s, const DevLayer &L, size_t t) {
+    return !L.attention && t >= 1 && t <= (size_t)MAX_ROWS && !q8_fine() && L.alpha.type == AQ_TYPE_F32 &&
+           L.beta.type == AQ_TYPE_F32 && is_kquant(L.qkv.type) && is_kquant(L.gate_z.type) &&
+           L.qkv.nb == L.gate_z.nb && L.alpha.cols == s->m->cfg.hidden && L.beta.cols == s->m->cfg.hidden &&
+           rmsnorm_rows_fit(s->m->cfg.hidden);
+}
+
+// Where a pass's DeltaNet gate pre-activations go: in VERIFY mode the layer's slot (kept for the commit).
+float *dn_alpha_out(aq_state *s, Mode mode, int dn_slot) { return mode == VERIFY ? s->sv_a[dn_slot] : s->a; }
+float *dn_beta_out(aq_state *s, Mode mode, int dn_slot) { return mode == VERIFY ? s->sv_b[dn_slot] : s->b; }
+
+// attn_norm of a DeltaNet layer into act_h (f32 + Q8_K) with its gate rows (dn_gates_in_norm), one launch.
+int norm_gates_into(aq_state *s, const DevLayer &L, const float *x, size_t t, Mode mode, int dn_slot) {
+    const size_t h = s->m->cfg.hidden;
+    QuantOut q;
+    q.act = &s->act_h;
+    q.kind = QK_Q8K;
+    q.f32 = true;
+    NormRows fr;
+    fr.w[0] = reinterpret_cast<const float *>(L.alpha.qa);
+    fr.w[1] = reinterpret_cast<const float *>(L.beta.qa);
+    fr.y[0] = dn_alpha_out(s, mode, dn_slot);
+    fr.y[1] = dn_beta_out(s, mode, dn_slot);
+    fr.rows[0] = (int)L.alpha.rows;
+    fr.rows[1] = (int)L.beta.rows;
+    return launch_rmsnorm_rows(x, h, L.attn_norm, s->m->cfg.rms_eps, h, t, q, fr, s->stream);
+}
+
+// gates_done: the DeltaNet gate rows are already in place (norm_gates_into).
 int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv, int dn_slot, Mode mode, float *y_out,
-          const float *resid) {
+          const float *resid, bool gates_done = false) {
     aq_model *m = s->m;
     const aq_model_config &c = m->cfg;
     int rc = 0;
@@ -670,13 +702,14 @@ int mixer(aq_state *s, const DevLayer &L, size_t t, size_t start_pos, KvDev *kv,
         return mm(s, L.o, s->act_att, t, y_out, resid);
     }
     float *mixed = mode == VERIFY ? s->sv_mixed[dn_slot] : s->mixed;
-    float *av = mode == VERIFY ? s->sv_a[dn_slot] : s->a;
-    float *bv = mode == VERIFY ? s->sv_b[dn_slot] : s->b;
+    float *av = dn_alpha_out(s, mode, dn_slot);
+    float *bv = dn_beta_out(s, mode, dn_slot);
     {
-        // qkv, z and the ssm_alpha / ssm_beta gate pre-activations in one launch (the gates kept for the commit)
+        // qkv, z and (unless the norm launch formed them) the ssm_alpha / ssm_beta gate pre-activations in one
+        // launch (the gates kept for the commit)
         const Weight *ws[4] = {&L.qkv, &L.gate_z, &L.alpha, &L.beta};
         float *ys[4] = {mixed, s->z, av, bv};
-        if ((rc = mm_multi(s, 4, ws, ys, s->act_h, t))) return rc;
+        if ((rc = mm_multi(s, gates_done ? 2 : 4, ws, ys, s->act_h, t))) return rc;
     }
     DnArgs d;
     d.mixed = mixed;
@@ -733,8 +766,10 @@ int mlp(aq_state *s, const DevLayer &L, size_t t, float *y_out, const float *res
 int decoder_layer(aq_state *s, const DevLayer &L, const float *x, size_t t, size_t start_pos, KvDev *kv, int dn_slot,
                   Mode mode, float *y_out) {
     const size_t h = s->m->cfg.hidden;
-    int rc = norm_into(s, x, h, L.attn_norm, h, t, s->act_h, 0, 0, mixer_needs(L));
-    if (!rc) rc = mixer(s, L, t, start_pos, kv, dn_slot, mode, s->y, x);
+    const bool gates = dn_gates_in_norm(s, L, t);
+    int rc = gates ? norm_gates_into(s, L, x, t, mode, dn_slot)
+                   : norm_into(s, x, h, L.attn_norm, h, t, s->act_h, 0, 0, mixer_needs(L));
+    if (!rc) rc = mixer(s, L, t, start_pos, kv, dn_slot, mode, s->y, x, gates);
     if (!rc) rc = norm_into(s, s->y, h, L.post_norm, h, t, s->act_h, 0, 0, mlp_needs(L));
     if (!rc) rc = mlp(s, L, t, y_out, s->y);
     return rc;

@@ -33,6 +33,20 @@ int launch_embed(const Weight &w, const uint32_t *ids, size_t t, float *out, siz
 // y = (x * inv_rms(x)) * w per row (rmsnorm.rs:14-76), t rows of n; y_f32 optional (row stride y_stride).
 int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t, float *y_f32,
                    size_t y_stride, const QuantOut &q, hipStream_t stream);
+// Up to two F32 matrices over the normalised rows, formed by work-groups of the norm launch itself (the DeltaNet
+// ssm_alpha / ssm_beta gate rows, gated_deltanet.rs:271-274): y[i][c * rows[i] + r] = w[i] row r . normalised row
+// c (dot.rs:180-200), w[i] rows[i] x n row-major.
+struct NormRows {
+    const float *w[2] = {nullptr, nullptr};
+    float *y[2] = {nullptr, nullptr};
+    int rows[2] = {0, 0};
+    int t = 0; // set by the launcher: the launch's input rows
+};
+// Whether launch_rmsnorm_rows takes rows of n (whole 256-blocks, each chain held by 8 lanes of one wave).
+bool rmsnorm_rows_fit(size_t n);
+// launch_rmsnorm (no y_f32) plus the rows of `fr`, one launch.
+int launch_rmsnorm_rows(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t,
+                        const QuantOut &q, const NormRows &fr, hipStream_t stream);
 // Two RMSNorms of t rows of n into the same quantised rows in one launch: x with w into elements q.elem_off..,
 // x2 with w2 into elements eoff2.. (the MTP's [rmsnorm(embed, enorm) | rmsnorm(h, hnorm)], mtp.rs:95-104).
 int launch_rmsnorm_pair(const float *x, size_t x_stride, const float *w, const float *x2, size_t x2_stride,
@@ -46,11 +60,7 @@ int launch_swiglu(const float *g, const float *u, size_t n, size_t t, float *h_f
 struct DnArgs {
     const float *mixed = nullptr; // t x cd conv inputs (the qkv projection)
     const float *z = nullptr;     // t x vd output gate (null: no output)
-    float *a = nullptr, *b = nullptr;       // t x nv gate pre-activations (written when x is set, else read)
-    const float *x = nullptr;               // when set: a, b = ssm_alpha / ssm_beta (F32) rows . x rows
-    size_t x_stride = 0;
-    const float *w_alpha = nullptr, *w_beta = nullptr; // nv x hidden F32
-    int hidden = 0;
+    const float *a = nullptr, *b = nullptr; // t x nv gate pre-activations (ssm_alpha / ssm_beta rows)
     const float *conv_src = nullptr;        // cd x (K-1) window
     float *conv_dst = nullptr;              // null: window not written
     const float *conv_w = nullptr;          // cd x K

@@ -97,12 +97,16 @@ __host__ __device__ inline int rn_chain_stride(int n) { // floats per chain row 
     return (clen + 31) / 32 * 32 + 4;
 }
 
-template <int PL>
+// FR (with PL < 0 and n a multiple of 256): a one-dimensional grid, the t x nslice norm work-groups first, then
+// t x 8 ceil(nrows / 8) work-groups each forming row g of the F32 matrices in `fr` over normalised row c instead of
+// writing a slice. Work-group i runs on XCD i mod 8 (the dispatcher's round robin), so the F32-rows index puts the
+// t work-groups of one row g on one XCD: 8 rows x t columns per group of 8 t, column-major within the group.
+template <int PL, bool FR = false>
 __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x, size_t x_stride, const float *w,
                                                                  float eps, int n, float *y, size_t y_stride, Act qa,
                                                                  int kind, size_t col0, size_t eoff, int act_f32,
                                                                  const float *x2, size_t x2_stride, const float *w2,
-                                                                 size_t eoff2) {
+                                                                 size_t eoff2, int nslice, NormRows fr) {
     if (blockIdx.z == 1) { // a pair launch: the second input, its norm weights and its place in the output row
         x = x2;
         x_stride = x2_stride;
@@ -110,21 +114,42 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
         eoff = eoff2;
     }
     extern __shared__ float sm[]; // 8 chains of squares, 16 floats, then (Q8_0 output only) the normalised row
-    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    int row = blockIdx.x, ys = blockIdx.y; // the input row, and the slice (>= nslice: F32 row ys - nslice)
+    if constexpr (FR) {
+        const int id = (int)blockIdx.x, nn = nslice * fr.t;
+        if (id < nn) {
+            row = id % fr.t;
+            ys = id / fr.t;
+        } else {
+            const int k = id - nn, grp = k / (8 * fr.t), rem = k % (8 * fr.t);
+            row = rem / 8;
+            ys = nslice + grp * 8 + rem % 8;
+        }
+    }
     const int n4 = n >> 2, n8 = n / 8 * 8, clen = n8 / 8, cs = rn_chain_stride(n);
-    // this work-group's slice of the output: float4s [o0, o1), whole 256-blocks
-    const int nslice = gridDim.y, nblk = n4 / 64;
-    const int o0 = nslice > 1 ? (int)blockIdx.y * nblk / nslice * 64 : 0;
-    const int o1 = nslice > 1 ? ((int)blockIdx.y + 1) * nblk / nslice * 64 : n4;
+    const bool frw = FR && ys >= nslice; // uniform: an F32-rows work-group
+    const int g = ys - nslice;
+    if (frw && g >= fr.rows[0] && g >= fr.rows[1]) return; // past both matrices' rows (uniform)
+    // this work-group's slice of the output: float4s [o0, o1), whole 256-blocks (an F32-rows one: the whole row)
+    const int nblk = n4 / 64;
+    const int o0 = !frw && nslice > 1 ? ys * nblk / nslice * 64 : 0;
+    const int o1 = !frw && nslice > 1 ? (ys + 1) * nblk / nslice * 64 : n4;
     float *sq = sm, *red = sm + 8 * cs, *xs = red + 16;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)row * x_stride);
     const float4 *w4 = reinterpret_cast<const float4 *>(w);
-    float4 xv[RN_ROUNDS], wv[RN_ROUNDS];
+    float4 xv[RN_ROUNDS], wv[RN_ROUNDS], fv[FR ? 2 : 1][RN_ROUNDS];
 #pragma unroll
     for (int r = 0; r < RN_ROUNDS; r++) {
         const int i4 = tid + r * RN_THREADS;
         if (i4 < n4) xv[r] = x4[i4];
         if (i4 >= o0 && i4 < o1) wv[r] = w4[i4]; // the norm weights of this work-group's slice only
+        if constexpr (FR) {
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                if (frw && g < fr.rows[i] && i4 < n4)
+                    fv[i][r] = reinterpret_cast<const float4 *>(fr.w[i] + (size_t)g * n)[i4];
+        }
     }
 #pragma unroll
     for (int r = 0; r < RN_ROUNDS; r++) {
@@ -240,6 +265,66 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
     }
     __syncthreads();
     const float inv = red[8];
+    if constexpr (FR) {
+        if (frw) {
+            // dot.rs:180-200 over the normalised row (the values the slices write): the 32-element block b is the
+            // float4s 8b..8b+7, held by lanes 8k..8k+7 of one wave in element order; its partial is summed left to
+            // right from 0 by passing the running sum one lane up (DPP row shift) after each lane's four products,
+            // so lane 8k+7 ends with it. Then the partials are added block by block in one chain per matrix (below),
+            // and the empty tail's `acc + part` (+0.0f).
+            const int nb32 = n / 32;
+            float *part = sq; // the chains are summed (the barrier above)
+#pragma unroll
+            for (int r = 0; r < RN_ROUNDS; r++) {
+                const int i4 = tid + r * RN_THREADS;
+                if (i4 < n4) { // n4 is a multiple of 64 here: wave-uniform, every lane of the wave on the DPP path
+                    const float v[4] = {(xv[r].x * inv) * wv[r].x, (xv[r].y * inv) * wv[r].y,
+                                        (xv[r].z * inv) * wv[r].z, (xv[r].w * inv) * wv[r].w};
+#pragma unroll
+                    for (int i = 0; i < 2; i++) {
+                        if (g >= fr.rows[i]) continue; // uniform
+                        const float p[4] = {fv[i][r].x * v[0], fv[i][r].y * v[1], fv[i][r].z * v[2],
+                                            fv[i][r].w * v[3]};
+                        float acc = 0.0f;
+#pragma unroll
+                        for (int m = 0; m < 8; m++) {
+                            if (m > 0)
+                                acc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                                    0, __builtin_bit_cast(int, acc), 0x111, 0xF, 0xF,
+                                                                    false));
+#pragma unroll
+                            for (int k = 0; k < 4; k++) acc += p[k];
+                        }
+                        if ((lane & 7) == 7) part[i * nb32 + (i4 >> 3)] = acc;
+                    }
+                }
+            }
+            __syncthreads();
+            // matrix i's chain in lanes 8i..8i+7 of wave 0: lane 8i + j holds partials jS..jS+S-1 in registers
+            // (+0.0f past the row's n / 32 <= -PL / 4 * 8 blocks: the sum from +0.0f is never -0.0f, so they change
+            // nothing), the running sum passed one lane up after each lane's terms, so lane 8i + 7 ends with it
+            if (tid < 16) {
+                constexpr int S = PL < 0 ? -PL / 4 : 1;
+                const int i = tid >> 3, j = tid & 7;
+                const float *pc = part + i * nb32 + j * S;
+                float rv[S];
+#pragma unroll
+                for (int k = 0; k < S; k++) rv[k] = j * S + k < nb32 ? pc[k] : 0.0f;
+                float acc = 0.0f;
+#pragma unroll
+                for (int m = 0; m < 8; m++) {
+                    if (m > 0)
+                        acc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
+                                                                                   0x111, 0xF, 0xF, false));
+#pragma unroll
+                    for (int k = 0; k < S; k++) acc += rv[k];
+                }
+                const int rows_i = i ? fr.rows[1] : fr.rows[0];
+                if (j == 7 && g < rows_i) (i ? fr.y[1] : fr.y[0])[(size_t)row * rows_i + g] = acc + 0.0f;
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int r = 0; r < RN_ROUNDS; r++) {
         const int i4 = tid + r * RN_THREADS;
@@ -315,7 +400,6 @@ __global__ void __launch_bounds__(256) swiglu_q80_kernel(const float *g, const f
 // work-groups sharing a K head never read a window another one has already advanced): v channels by every head,
 // q/k channels by head p == kh.
 constexpr int DN_TMAX = 8;      // rows per DeltaNet launch
-constexpr int DN_BLK_MAX = 256; // 32-blocks of the alpha/beta rows (hidden <= 8192)
 constexpr int DN_THREADS = 512; // waves 0-3 hold state columns (dv <= 256); 4-6 run the per-row sums
 
 // Parts per state column in the recurrence: as many as the work-group holds (H * DV <= DN_THREADS), at most four,
@@ -334,12 +418,10 @@ constexpr int dn_kh() { return DK / dn_parts<DK, DV>(); }
 template <int DK, int DV, bool CHUNK = false>
 __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const int t, float (&s)[dn_kh<DK, DV>()],
                                              const int r0, const bool first, const bool last) {
-    // CHUNK: the host admits no raw rows and no in-kernel gate projection, so both paths compile away
+    // CHUNK: the host admits no raw rows, so that path compiles away
     const bool raw_ = !CHUNK && a.raw;
-    const float *const ax_ = CHUNK ? nullptr : a.x;
     static_assert(DK <= 256 && DV <= 256 && DN_THREADS >= 448 && DN_TMAX * 2 <= 16, "DeltaNet work-group shape");
     __shared__ float sq[DN_TMAX][DK], sk[DN_TMAX][DK], sv[DN_TMAX][DV], sz[DN_TMAX][DV], so[DN_TMAX][DV];
-    __shared__ float part[2][DN_TMAX][DN_BLK_MAX];
     __shared__ float rdec[DN_TMAX], rbeta[DN_TMAX], rq[DN_TMAX], rk[DN_TMAX], ro[DN_TMAX];
     const int j = threadIdx.x, lane = j & 63, wave = j >> 6;
     const int kh = p % a.nk;
@@ -351,10 +433,8 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
     const int gr = wave == 5 ? 0 : 1;
     float gv = 0.0f, gsa = 0.0f, gdt = 0.0f;
     if (gate_lane) {
-        if (raw_)
-            gv = (gr == 0 ? a.rg : a.rbeta)[(size_t)(r0 + lane) * a.nv + p];
-        else if (!ax_)
-            gv = (gr == 0 ? a.a : a.b)[(size_t)(r0 + lane) * a.nv + p];
+        gv = raw_ ? (gr == 0 ? a.rg : a.rbeta)[(size_t)(r0 + lane) * a.nv + p]
+                  : (gr == 0 ? a.a : a.b)[(size_t)(r0 + lane) * a.nv + p];
         if (gr == 0 && !raw_) {
             gsa = a.ssm_a[p];
             gdt = a.dt_bias[p];
@@ -384,54 +464,6 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
             sv[i][c] = a.rv[(size_t)(r0 + i) * vd + p * DV + c];
         }
     } else {
-        if (ax_) {
-            // gated_deltanet.rs:271-274 ssm_alpha / ssm_beta rows of this head on the t input rows: per 32-block a
-            // left-to-right partial for every row (four rows' chains interleaved)
-            const int n = a.hidden, nblk = (n + 31) / 32;
-            const bool vec = (n & 3) == 0 && (a.x_stride & 3) == 0;
-            for (int task = j; task < 2 * nblk; task += DN_THREADS) {
-                const int r = task / nblk, b = task % nblk;
-                const float *w = (r == 0 ? a.w_alpha : a.w_beta) + (size_t)p * n;
-                const int e0 = b * 32, ne = n - e0 < 32 ? n - e0 : 32;
-                if (ne == 32 && vec) {
-                    float wv[32];
-#pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        const float4 f = *reinterpret_cast<const float4 *>(w + e0 + 4 * u);
-                        wv[4 * u] = f.x, wv[4 * u + 1] = f.y, wv[4 * u + 2] = f.z, wv[4 * u + 3] = f.w;
-                    }
-                    for (int i0 = 0; i0 < t; i0 += 4) {
-                        float xv[4][32];
-#pragma unroll
-                        for (int q = 0; q < 4; q++) {
-                            const int i = i0 + q < t ? i0 + q : t - 1;
-                            const float *xr = ax_ + (size_t)(r0 + i) * a.x_stride + e0;
-#pragma unroll
-                            for (int u = 0; u < 8; u++) {
-                                const float4 f = *reinterpret_cast<const float4 *>(xr + 4 * u);
-                                xv[q][4 * u] = f.x, xv[q][4 * u + 1] = f.y, xv[q][4 * u + 2] = f.z,
-                                          xv[q][4 * u + 3] = f.w;
-                            }
-                        }
-                        float pt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                        for (int e = 0; e < 32; e++)
-#pragma unroll
-                            for (int q = 0; q < 4; q++) pt[q] += wv[e] * xv[q][e];
-#pragma unroll
-                        for (int q = 0; q < 4; q++)
-                            if (i0 + q < t) part[r][i0 + q][b] = pt[q];
-                    }
-                } else {
-                    for (int i = 0; i < t; i++) {
-                        const float *xr = ax_ + (size_t)(r0 + i) * a.x_stride + e0;
-                        float pt = 0.0f;
-                        for (int e = 0; e < ne; e++) pt += w[e0 + e] * xr[e];
-                        part[r][i][b] = pt;
-                    }
-                }
-            }
-        }
         // task c: q channel c (c < DK), k channel c - DK, v channel c - 2 DK (conv, conv.rs:11-36), then the
         // z channels (silu only)
         const int n_conv = 2 * DK + DV, n_task = n_conv + (gated ? DV : 0);
@@ -527,14 +559,7 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
     }
     if (gate_lane) {
         const int i = lane;
-        float v = gv;
-        if (!raw_ && ax_) {
-            // dot.rs:180-200: the block chain, `acc + part` with the short tail (0.0f when there is none)
-            const int n = a.hidden, nblk = (n + 31) / 32;
-            v = seq_sum<false>(&part[gr][i][0], 0, nblk, 1, 0.0f);
-            if (n % 32 == 0) v = v + 0.0f;
-            (gr == 0 ? a.a : a.b)[(size_t)(r0 + i) * a.nv + p] = v; // kept for the commit
-        }
+        const float v = gv;
         if (gr == 0) {
             const float g = raw_ ? v : gsa * softplus_f(v + gdt); // deltanet.rs:32-35 gate_g
             rdec[i] = exp_f(g);
@@ -977,11 +1002,33 @@ int launch_embed(const Weight &w, const uint32_t *ids, size_t t, float *out, siz
     return launched("embed");
 }
 
+// Chain terms per lane of the vector kernel for rows of n: 8 lanes per chain in one wave when a chain is whole
+// float4s and fits (negative counts), else one wave per chain (the smallest built count that holds a chain), else 0
+// (the chains read from LDS).
+static int rn_pick_pl(size_t n) {
+    const int clen = (int)(n / 8), need8 = (clen + 7) / 8, need = (clen + 63) / 64;
+    const int t8s[] = {4, 8, 16, 24, 32, 48, 64, 80, 96};
+    const int pls[] = {1, 2, 4, 6, 8, 10, 12, 16};
+    int pl = 0;
+    if (clen % 4 == 0)
+        for (int c : t8s)
+            if (!pl && c >= need8) pl = -c;
+    for (int c : pls)
+        if (!pl && c >= need) pl = c;
+    return pl;
+}
+
+bool rmsnorm_rows_fit(size_t n) {
+    return n > 0 && n % 256 == 0 && n <= (size_t)4 * RN_THREADS * RN_ROUNDS && rn_pick_pl(n) < 0 &&
+           ((size_t)8 * rn_chain_stride((int)n) + 16) * sizeof(float) <= 65536;
+}
+
 // x2 set: a pair launch (grid z = 2), the second input normalised with w2 into elements eoff2.. of the same output
-// rows; it needs the vector kernel, and falls back to two launches where that does not apply.
+// rows; it needs the vector kernel, and falls back to two launches where that does not apply. fr set: the F32 rows
+// of fr by work-groups past the slices (grid y), in the same launch.
 static int rmsnorm_launch(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t, float *y_f32,
                           size_t y_stride, const QuantOut &q, hipStream_t stream, const float *x2, size_t x2_stride,
-                          const float *w2, size_t eoff2) {
+                          const float *w2, size_t eoff2, const NormRows *fr = nullptr) {
     AQ_REQUIRE(n > 0 && n <= 16384, "rmsnorm: row length must be 1..16384");
     if (t == 0) return 0;
     if (x2) {
@@ -1012,35 +1059,51 @@ static int rmsnorm_launch(const float *x, size_t x_stride, const float *w, float
         const int rc = rmsnorm_launch(x, x_stride, w, eps, n, t, nullptr, 0, q, stream, nullptr, 0, nullptr, 0);
         return rc ? rc : rmsnorm_launch(x2, x2_stride, w2, eps, n, t, nullptr, 0, q2, stream, nullptr, 0, nullptr, 0);
     }
+    int nfr = 0;
+    if (fr) {
+        AQ_REQUIRE(!x2 && !y_f32 && vec && rmsnorm_rows_fit(n), "rmsnorm rows: unsupported shape");
+        for (int i = 0; i < 2; i++) {
+            AQ_REQUIRE(fr->rows[i] >= 0 && fr->rows[i] <= 4096, "rmsnorm rows: row count");
+            AQ_REQUIRE(!fr->rows[i] || (fr->w[i] && fr->y[i] && al16(fr->w[i])), "rmsnorm rows: buffers");
+            nfr = fr->rows[i] > nfr ? fr->rows[i] : nfr;
+        }
+    }
     if (vec && vshmem <= 65536) {
         const size_t shmem = vshmem;
         // slices of whole 256-blocks (about five blocks each) when the row is made of them
         const int nblk = n % 256 == 0 ? (int)(n / 256) : 0;
         const unsigned slices = nblk >= 8 ? (unsigned)((nblk + 4) / 5) : 1;
-        // chain terms per lane: 8 lanes per chain in one wave when a chain is whole float4s and fits (negative
-        // counts), else one wave per chain (the smallest built count that holds a chain), else LDS
-        const int clen = (int)(n / 8), need8 = (clen + 7) / 8, need = (clen + 63) / 64;
-        const int t8s[] = {4, 8, 16, 24, 32, 48, 64, 80, 96};
-        const int pls[] = {1, 2, 4, 6, 8, 10, 12, 16};
-        int pl = 0;
-        if (clen % 4 == 0)
-            for (int c : t8s)
-                if (!pl && c >= need8) pl = -c;
-        for (int c : pls)
-            if (!pl && c >= need) pl = c;
-        const dim3 grid((unsigned)t, slices, x2 ? 2u : 1u);
+        const int pl = rn_pick_pl(n);
+        const dim3 grid = fr ? dim3((unsigned)(t * (slices + 8 * ((nfr + 7) / 8)))) // the F32-rows index, in the kernel
+                             : dim3((unsigned)t, slices, x2 ? 2u : 1u);
         if (!x2) { // the kernel's second-input arguments, unread with one input
             x2 = x;
             x2_stride = x_stride;
             w2 = w;
             eoff2 = q.elem_off;
         }
+        NormRows frv = fr ? *fr : NormRows{};
+        frv.t = (int)t;
+        if (fr) {
+            switch (pl) {
+#define AQ_RNF(P)                                                                                             \
+    case P:                                                                                                   \
+        hipLaunchKernelGGL((rmsnorm_vec_kernel<P, true>), grid, dim3(RN_THREADS), shmem, stream, x, x_stride, w, eps, \
+                           (int)n, y_f32, y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0, x2,        \
+                           x2_stride, w2, eoff2, (int)slices, frv);                                           \
+        break;
+                AQ_RNF(-4) AQ_RNF(-8) AQ_RNF(-16) AQ_RNF(-24) AQ_RNF(-32) AQ_RNF(-48) AQ_RNF(-64) AQ_RNF(-80) AQ_RNF(-96)
+#undef AQ_RNF
+            default: return fail(AQ_EUNSUP, "rmsnorm rows: chain form");
+            }
+            return launched("rmsnorm rows");
+        }
         switch (pl) {
 #define AQ_RN(P)                                                                                              \
     case P:                                                                                                   \
         hipLaunchKernelGGL((rmsnorm_vec_kernel<P>), grid, dim3(RN_THREADS), shmem, stream, x, x_stride, w, eps, (int)n, \
                            y_f32, y_stride, act, (int)q.kind, q.col0, q.elem_off, q.f32 ? 1 : 0, x2, x2_stride, w2,  \
-                           eoff2);                                                                            \
+                           eoff2, (int)slices, frv);                                                          \
         break;
             AQ_RN(0) AQ_RN(1) AQ_RN(2) AQ_RN(4) AQ_RN(6) AQ_RN(8) AQ_RN(10) AQ_RN(12) AQ_RN(16)
             AQ_RN(-4) AQ_RN(-8) AQ_RN(-16) AQ_RN(-24) AQ_RN(-32) AQ_RN(-48) AQ_RN(-64) AQ_RN(-80) AQ_RN(-96)
@@ -1057,6 +1120,11 @@ static int rmsnorm_launch(const float *x, size_t x_stride, const float *w, float
 int launch_rmsnorm(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t, float *y_f32,
                    size_t y_stride, const QuantOut &q, hipStream_t stream) {
     return rmsnorm_launch(x, x_stride, w, eps, n, t, y_f32, y_stride, q, stream, nullptr, 0, nullptr, 0);
+}
+
+int launch_rmsnorm_rows(const float *x, size_t x_stride, const float *w, float eps, size_t n, size_t t,
+                        const QuantOut &q, const NormRows &fr, hipStream_t stream) {
+    return rmsnorm_launch(x, x_stride, w, eps, n, t, nullptr, 0, q, stream, nullptr, 0, nullptr, 0, &fr);
 }
 
 int launch_rmsnorm_pair(const float *x, size_t x_stride, const float *w, const float *x2, size_t x2_stride,
@@ -1103,11 +1171,9 @@ int launch_dn_core(const DnArgs &a, hipStream_t stream) {
     } else {
         AQ_REQUIRE(a.rq && a.rk && a.rv && a.rg && a.rbeta, "deltanet: raw inputs");
     }
-    AQ_REQUIRE(a.t <= DN_TMAX || (!a.raw && !a.x && a.t <= 4096),
-               "deltanet: more than 8 rows in one launch need the projected gates (no raw mode, no x) and t <= 4096");
-    AQ_REQUIRE(a.raw || a.x || (a.a && a.b), "deltanet: gate inputs");
-    AQ_REQUIRE(!a.x || (a.w_alpha && a.w_beta && a.a && a.b && a.hidden > 0 && a.hidden <= 32 * DN_BLK_MAX),
-               "deltanet: alpha/beta projection");
+    AQ_REQUIRE(a.t <= DN_TMAX || (!a.raw && a.t <= 4096),
+               "deltanet: more than 8 rows in one launch need the projected gates (no raw mode) and t <= 4096");
+    AQ_REQUIRE(a.raw || (a.a && a.b), "deltanet: gate inputs");
     const int threads = DN_THREADS;
     const int key = a.dk * 1000 + a.dv;
     switch (key) {
@@ -1128,7 +1194,7 @@ int launch_dn_core(const DnArgs &a, hipStream_t stream) {
 
 int launch_dn_core_multi(const DnArgs *args_dev, const DnArgs &like, int n, hipStream_t stream) {
     AQ_REQUIRE(n >= 1 && args_dev, "deltanet: no layers");
-    AQ_REQUIRE(!like.raw && !like.x && !like.out, "deltanet multi: commit form only (saved gates, no output)");
+    AQ_REQUIRE(!like.raw && !like.out, "deltanet multi: commit form only (saved gates, no output)");
     const int key = like.dk * 1000 + like.dv;
     switch (key) {
 #define AQ_DN(K, V)                                                                                           \
