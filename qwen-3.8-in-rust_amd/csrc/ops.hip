@@ -91,6 +91,11 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float *x, size_t x_s
 // work-groups; with Q8_K output, wave w holds whole 256-blocks (its float4s are block w + 8r, lane order), so the
 // quantiser runs on registers.
 constexpr int RN_THREADS = 512, RN_ROUNDS = 8; // n <= 4 * 512 * 8
+// float4 rounds per thread an instance needs: with 8 lanes per chain (PL < 0) a chain holds at most 8 * -PL terms,
+// so n / 4 <= 16 * -PL + 1 (the vector path takes n % 4 == 0, the chains n8 = n / 8 * 8 elements)
+__host__ __device__ constexpr int rn_rounds(int pl) {
+    return pl < 0 ? (16 * -pl + 1 + RN_THREADS - 1) / RN_THREADS : RN_ROUNDS;
+}
 
 __host__ __device__ inline int rn_chain_stride(int n) { // floats per chain row in LDS: 4 (mod 32), 16-byte rows
     const int clen = n / 8;
@@ -138,9 +143,10 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
     float *sq = sm, *red = sm + 8 * cs, *xs = red + 16;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)row * x_stride);
     const float4 *w4 = reinterpret_cast<const float4 *>(w);
-    float4 xv[RN_ROUNDS], wv[RN_ROUNDS], fv[FR ? 2 : 1][RN_ROUNDS];
+    constexpr int R = rn_rounds(PL);
+    float4 xv[R], wv[R], fv[FR ? 2 : 1][R];
 #pragma unroll
-    for (int r = 0; r < RN_ROUNDS; r++) {
+    for (int r = 0; r < R; r++) {
         const int i4 = tid + r * RN_THREADS;
         if (i4 < n4) xv[r] = x4[i4];
         if (i4 >= o0 && i4 < o1) wv[r] = w4[i4]; // the norm weights of this work-group's slice only
@@ -152,7 +158,7 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
         }
     }
 #pragma unroll
-    for (int r = 0; r < RN_ROUNDS; r++) {
+    for (int r = 0; r < R; r++) {
         const int i4 = tid + r * RN_THREADS;
         if (i4 < n4) {
             const float c[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
@@ -275,7 +281,7 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
             const int nb32 = n / 32;
             float *part = sq; // the chains are summed (the barrier above)
 #pragma unroll
-            for (int r = 0; r < RN_ROUNDS; r++) {
+            for (int r = 0; r < R; r++) {
                 const int i4 = tid + r * RN_THREADS;
                 if (i4 < n4) { // n4 is a multiple of 64 here: wave-uniform, every lane of the wave on the DPP path
                     const float v[4] = {(xv[r].x * inv) * wv[r].x, (xv[r].y * inv) * wv[r].y,
@@ -326,7 +332,7 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
         }
     }
 #pragma unroll
-    for (int r = 0; r < RN_ROUNDS; r++) {
+    for (int r = 0; r < R; r++) {
         const int i4 = tid + r * RN_THREADS;
         // n4 is a multiple of 64 when the output is Q8_K: the conditions are wave-uniform there
         if (i4 < n4 && i4 >= o0 && i4 < o1) {
@@ -1074,6 +1080,7 @@ static int rmsnorm_launch(const float *x, size_t x_stride, const float *w, float
         const int nblk = n % 256 == 0 ? (int)(n / 256) : 0;
         const unsigned slices = nblk >= 8 ? (unsigned)((nblk + 4) / 5) : 1;
         const int pl = rn_pick_pl(n);
+        AQ_REQUIRE(n / 4 <= (size_t)rn_rounds(pl) * RN_THREADS, "rmsnorm: row longer than the kernel's rounds");
         const dim3 grid = fr ? dim3((unsigned)(t * (slices + 8 * ((nfr + 7) / 8)))) // the F32-rows index, in the kernel
                              : dim3((unsigned)t, slices, x2 ? 2u : 1u);
         if (!x2) { // the kernel's second-input arguments, unread with one input
