@@ -420,10 +420,14 @@ constexpr int dn_kh() { return DK / dn_parts<DK, DV>(); }
 
 // Rows r0 .. r0 + t - 1 (t <= DN_TMAX) of the launch's rows. `s` is the thread's part of the state column: loaded
 // from a.rec when `first`, written back when `last` (and a.write_state), carried in registers between the pieces of
-// one launch otherwise. The conv window of a piece after the first is the three input rows before it.
-template <int DK, int DV, bool CHUNK = false>
-__device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const int t, float (&s)[dn_kh<DK, DV>()],
+// one launch otherwise. The conv window of a piece after the first is the three input rows before it. TT > 0: the
+// row count is TT (the input loops run over exactly those rows), else t_in.
+template <int DK, int DV, bool CHUNK = false, int TT = 0>
+__device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const int t_in, float (&s)[dn_kh<DK, DV>()],
                                              const int r0, const bool first, const bool last) {
+    static_assert(TT >= 0 && TT <= DN_TMAX, "rows per launch");
+    constexpr int TM = TT ? TT : DN_TMAX; // the input loops' bound
+    const int t = TT ? TT : t_in;
     // CHUNK: the host admits no raw rows, so that path compiles away
     const bool raw_ = !CHUNK && a.raw;
     static_assert(DK <= 256 && DV <= 256 && DN_THREADS >= 448 && DN_TMAX * 2 <= 16, "DeltaNet work-group shape");
@@ -478,7 +482,7 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
                 const int kind = c < DK ? 0 : c < 2 * DK ? 1 : 2;
                 const int cc = kind == 2 ? c - 2 * DK : c - kind * DK;
                 const int ch = kind == 0 ? kh * DK + cc : kind == 1 ? kd + kh * DK + cc : 2 * kd + p * DV + cc;
-                float seq[DN_TMAX + 3];
+                float seq[TM + 3];
 #pragma unroll
                 for (int e = 0; e < 3; e++)
                     seq[e] = first ? a.conv_src[(size_t)ch * 3 + e] : a.mixed[(size_t)(r0 - 3 + e) * cd + ch];
@@ -486,11 +490,11 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
 #pragma unroll
                 for (int e = 0; e < 4; e++) cw[e] = a.conv_w[(size_t)ch * 4 + e];
 #pragma unroll
-                for (int i = 0; i < DN_TMAX; i++) seq[3 + i] = a.mixed[(size_t)(r0 + (i < t ? i : t - 1)) * cd + ch];
+                for (int i = 0; i < TM; i++) seq[3 + i] = a.mixed[(size_t)(r0 + (i < t ? i : t - 1)) * cd + ch];
                 float *dst = kind == 0 ? &sq[0][cc] : kind == 1 ? &sk[0][cc] : &sv[0][cc];
                 const int dstride = kind == 2 ? DV : DK;
 #pragma unroll
-                for (int i = 0; i < DN_TMAX; i++) {
+                for (int i = 0; i < TM; i++) {
                     if (i < t) {
                         float acc = 0.0f;
                         acc += cw[0] * seq[i];
@@ -502,17 +506,17 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
                 }
                 if (a.conv_dst && last && (kind == 2 || p == kh)) {
 #pragma unroll
-                    for (int i = 0; i <= DN_TMAX; i++) // the window after row t - 1: seq[t .. t + 2]
+                    for (int i = 0; i <= TM; i++) // the window after row t - 1: seq[t .. t + 2]
                         if (i == t)
                             for (int e = 0; e < 3; e++) a.conv_dst[(size_t)ch * 3 + e] = seq[i + e];
                 }
             } else {
                 const int cc = c - n_conv;
-                float zr[DN_TMAX];
+                float zr[TM];
 #pragma unroll
-                for (int i = 0; i < DN_TMAX; i++) zr[i] = a.z[(size_t)(r0 + (i < t ? i : t - 1)) * vd + p * DV + cc];
+                for (int i = 0; i < TM; i++) zr[i] = a.z[(size_t)(r0 + (i < t ? i : t - 1)) * vd + p * DV + cc];
 #pragma unroll
-                for (int i = 0; i < DN_TMAX; i++)
+                for (int i = 0; i < TM; i++)
                     if (i < t) sz[i][cc] = silu_f(zr[i]);
             }
         }
@@ -687,10 +691,11 @@ __device__ __forceinline__ void dn_core_body(const DnArgs &a, const int p, const
     }
 }
 
-template <int DK, int DV>
+// TT > 0: a.t == TT rows (the verify's k + 1 and decode's 1 take such an instance), else any row count up to 8
+template <int DK, int DV, int TT>
 __global__ void __launch_bounds__(DN_THREADS) dn_core_kernel(DnArgs a) {
     float s[dn_kh<DK, DV>()];
-    dn_core_body<DK, DV>(a, (int)blockIdx.x, a.t, s, 0, true, true);
+    dn_core_body<DK, DV, false, TT>(a, (int)blockIdx.x, a.t, s, 0, true, true);
 }
 
 // A prompt chunk of more than DN_TMAX rows in one launch (gated_deltanet.rs:197-199 steps the recurrence token by
@@ -1186,8 +1191,12 @@ int launch_dn_core(const DnArgs &a, hipStream_t stream) {
     switch (key) {
 #define AQ_DN(K, V)                                                                                           \
     case K * 1000 + V:                                                                                        \
-        if (a.t <= DN_TMAX)                                                                                   \
-            hipLaunchKernelGGL((dn_core_kernel<K, V>), dim3((unsigned)a.nv), dim3(threads), 0, stream, a);     \
+        if (a.t == 4)                                                                                         \
+            hipLaunchKernelGGL((dn_core_kernel<K, V, 4>), dim3((unsigned)a.nv), dim3(threads), 0, stream, a);  \
+        else if (a.t == 1)                                                                                    \
+            hipLaunchKernelGGL((dn_core_kernel<K, V, 1>), dim3((unsigned)a.nv), dim3(threads), 0, stream, a);  \
+        else if (a.t <= DN_TMAX)                                                                              \
+            hipLaunchKernelGGL((dn_core_kernel<K, V, 0>), dim3((unsigned)a.nv), dim3(threads), 0, stream, a);  \
         else                                                                                                  \
             hipLaunchKernelGGL((dn_core_chunk_kernel<K, V>), dim3((unsigned)a.nv), dim3(threads), 0, stream, a); \
         break;
