@@ -93,6 +93,27 @@ __host__ __device__ inline size_t kq_dm_off(size_t row, size_t sb, size_t nb) {
 // j+4, the pair one kernel thread owns, are adjacent.
 __host__ __device__ inline int lane_slot(int l) { return 2 * (l & 3) + (l >> 2); }
 
+// Weight loads marked non-temporal (the `nt` bit): each weight byte is read once per round, so its lines are the
+// first the caches give up, and what the round reads again (activations, the DeltaNet state, the gate rows, the KV
+// cache) stays resident instead of being pushed out by ~17 GB of weights per round (K-quant and Q8_0 / Q4_0 weight
+// loads: the greedy --spec 3 round 8.05 -> 7.76 ms).
+typedef unsigned int kq_nt_u4 __attribute__((ext_vector_type(4)));
+typedef unsigned int kq_nt_u2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ld_nt4(const uint8_t *p) {
+    const kq_nt_u4 v = __builtin_nontemporal_load(reinterpret_cast<const kq_nt_u4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_nt2(const uint8_t *p) {
+    const kq_nt_u2 v = __builtin_nontemporal_load(reinterpret_cast<const kq_nt_u2 *>(p));
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ld_nt1(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+}
+__device__ __forceinline__ uint16_t ld_nth(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
+}
+
 struct Weight {
     int type = 0;
     size_t rows = 0, cols = 0, nb = 0; // nb: blocks per row

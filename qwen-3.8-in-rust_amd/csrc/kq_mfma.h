@@ -111,15 +111,15 @@ template <int TYPE>
 __device__ __forceinline__ void load_w(WRegs<TYPE> &w, const MfArgs &a, uint32_t tile, int r, int j) {
     const uint32_t jr = (uint32_t)(j * 4 + r);
     const uint8_t *qa = a.qa + (tile * 512u + jr * 16u);
-    w.qa0 = *reinterpret_cast<const uint4 *>(qa);       // lane j
-    w.qa1 = *reinterpret_cast<const uint4 *>(qa + 256); // lane j + 4
-    w.sc = *reinterpret_cast<const uint4 *>(a.sc + (tile * 64u + (uint32_t)r * 16u));
+    w.qa0 = ld_nt4(qa);       // lane j
+    w.qa1 = ld_nt4(qa + 256); // lane j + 4
+    w.sc = ld_nt4(a.sc + (tile * 64u + (uint32_t)r * 16u));
     if constexpr (TYPE == AQ_TYPE_Q5_K) {
-        const uint2 h = *reinterpret_cast<const uint2 *>(a.qb + (tile * 128u + jr * 8u));
+        const uint2 h = ld_nt2(a.qb + (tile * 128u + jr * 8u));
         w.qb = make_uint4(h.x, h.y, 0, 0);
     } else if constexpr (TYPE == AQ_TYPE_Q6_K) {
-        w.qb = *reinterpret_cast<const uint4 *>(a.qb + (tile * 256u + jr * 16u));
-        w.d6 = *reinterpret_cast<const uint16_t *>(a.dm + (tile * 8u + (uint32_t)r * 2u));
+        w.qb = ld_nt4(a.qb + (tile * 256u + jr * 16u));
+        w.d6 = ld_nth(a.dm + (tile * 8u + (uint32_t)r * 2u));
     }
 }
 
@@ -920,15 +920,15 @@ kq_wave_kernel(KqGroup G) {
 template <int TYPE>
 __device__ __forceinline__ void load_w_half(WRegs<TYPE> &w, const MfArgs &a, uint32_t tile, int r, int j, int h) {
     const uint32_t jr = (uint32_t)(j * 4 + r), hh = (uint32_t)h;
-    w.qa0 = *reinterpret_cast<const uint4 *>(a.qa + (tile * 512u + jr * 16u + hh * 256u));
-    w.sc = *reinterpret_cast<const uint4 *>(a.sc + (tile * 64u + (uint32_t)r * 16u));
+    w.qa0 = ld_nt4(a.qa + (tile * 512u + jr * 16u + hh * 256u));
+    w.sc = ld_nt4(a.sc + (tile * 64u + (uint32_t)r * 16u));
     if constexpr (TYPE == AQ_TYPE_Q5_K) {
-        w.qb.x = *reinterpret_cast<const uint32_t *>(a.qb + (tile * 128u + jr * 8u + hh * 4u));
+        w.qb.x = ld_nt1(a.qb + (tile * 128u + jr * 8u + hh * 4u));
     } else if constexpr (TYPE == AQ_TYPE_Q6_K) {
-        const uint2 q = *reinterpret_cast<const uint2 *>(a.qb + (tile * 256u + jr * 16u + hh * 8u));
+        const uint2 q = ld_nt2(a.qb + (tile * 256u + jr * 16u + hh * 8u));
         w.qb.x = q.x;
         w.qb.y = q.y;
-        w.d6 = *reinterpret_cast<const uint16_t *>(a.dm + (tile * 8u + (uint32_t)r * 2u));
+        w.d6 = ld_nth(a.dm + (tile * 8u + (uint32_t)r * 2u));
     }
 }
 

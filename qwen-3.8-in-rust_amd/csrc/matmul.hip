@@ -175,12 +175,12 @@ __device__ __forceinline__ void q8_wave_body(const Q8Args &a, int wg, const uint
     auto load = [&](Q8Regs<TYPE> &w, int blk) {
         const size_t wb = rowb + (blk < nb ? blk : nb - 1);
         if constexpr (Q4) {
-            w.c0 = *reinterpret_cast<const uint4 *>(wqa + wb * 16);
+            w.c0 = ld_nt4(wqa + wb * 16);
         } else {
-            w.c0 = *reinterpret_cast<const uint4 *>(wqa + wb * 32);
-            w.c1 = *reinterpret_cast<const uint4 *>(wqa + wb * 32 + 16);
+            w.c0 = ld_nt4(wqa + wb * 32);
+            w.c1 = ld_nt4(wqa + wb * 32 + 16);
         }
-        w.d = *reinterpret_cast<const uint16_t *>(wdm + wb * 2);
+        w.d = ld_nth(wdm + wb * 2);
     };
     Q8Regs<TYPE> wr[Q8W_PF];
     const int NT = (int)blockDim.x;
