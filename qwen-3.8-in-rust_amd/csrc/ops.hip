@@ -153,8 +153,13 @@ __global__ void __launch_bounds__(RN_THREADS) rmsnorm_vec_kernel(const float *x,
         if constexpr (FR) {
 #pragma unroll
             for (int i = 0; i < 2; i++)
-                if (frw && g < fr.rows[i] && i4 < n4)
-                    fv[i][r] = reinterpret_cast<const float4 *>(fr.w[i] + (size_t)g * n)[i4];
+                if (frw && g < fr.rows[i] && i4 < n4) {
+                    // weights read once per pass (94 MB over the 27B shape's 48 layers): non-temporal, like the
+                    // matmuls' weights, so the DeltaNet state and the KV rows stay in the memory-side cache
+                    const uint4 u = ld_nt4(reinterpret_cast<const uint8_t *>(fr.w[i] + (size_t)g * n) + (size_t)i4 * 16);
+                    fv[i][r] = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                                           __uint_as_float(u.w));
+                }
         }
     }
 #pragma unroll
